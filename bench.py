@@ -1,0 +1,334 @@
+"""Benchmark of the MI355X expert-paging hot path (one GPU).
+
+Headline (the `value`): Huffman decode GB/s -- one step is one launch of the
+batched row expansion over 256 synthetic experts (w13 fp8 1024x2048 + w2 fp8
+2048x512, N(0, 0.02) weights quantised to e4m3 with 128x128 block scales,
+compressed per row at pitch 0.89), inputs resident in HBM. Bytes per row
+= 4(G+1) + N/2 + 4*gstart[G] + 512 + N (header, nibbles, Huffman words
+consumed, LUT, raw output). Also reported: slot gather GB/s from pinned host
+RAM against the in-run host-link ceiling (large pinned H2D copies), acquire
+microseconds per layer inside a captured hipGraph, and the oracle's CPU
+decoder on a bounded sample as the CPU baseline.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+
+import argparse
+import concurrent.futures as cf
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "vllm-expert-pager_amd"))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+SHAPES = ((1024, 2048), (2048, 512))  # w13, w2 (rows, cols) of fp8
+PITCH_RATIO = 0.89
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synthetic_experts(count: int, seed: int, dev) -> list[torch.Tensor]:
+    """fp8 e4m3 bytes of `count` experts per name, generated on the GPU: (count, N) uint8."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = []
+    for r, c in SHAPES:
+        rows = torch.empty((count, r * c), dtype=torch.uint8, device=dev)
+        for j in range(count):
+            w = torch.randn((r, c), generator=g, device=dev) * 0.02
+            blk = w.view(r // 128, 128, c // 128, 128)
+            s = blk.abs().amax(dim=(1, 3), keepdim=True).clamp(min=1e-12) / 448.0
+            rows[j] = (blk / s).to(torch.float8_e4m3fn).view(torch.uint8).reshape(-1)
+        out.append(rows)
+    return out
+
+
+def encode_batch(raws_host: list[np.ndarray], threads: int):
+    from vllm_expert_pager import codec
+
+    count = raws_host[0].shape[0]
+    pitches = [codec.pitch_of(r.shape[1], PITCH_RATIO, 4096) for r in raws_host]
+    stg = [np.empty((count, p), np.uint8) for p in pitches]
+    luts = np.empty((count, len(raws_host), 512), np.uint8)
+
+    def one(args):
+        k, j = args
+        codec.encode_into(raws_host[k][j], stg[k][j], luts[j, k])
+
+    with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(one, [(k, j) for k in range(len(raws_host)) for j in range(count)]))
+    return stg, luts
+
+
+def algorithmic_bytes(stg: list[np.ndarray], n_bytes: list[int], chunk: int = 512) -> int:
+    total = 0
+    for k, s in enumerate(stg):
+        n = n_bytes[k]
+        G = n // (chunk * 32)
+        words = s[:, 4 * G : 4 * G + 4].view(np.int32).astype(np.int64).reshape(-1)  # gstart[G]
+        total += int(((4 * (G + 1) + n // 2 + 512 + n) * s.shape[0]) + 4 * words.sum())
+    return total
+
+
+def bench_decode(args, dev, cores):
+    from oracle import codec_ref
+    from vllm_expert_pager import codec
+
+    count = args.rows
+    t0 = time.time()
+    raws = synthetic_experts(count, 1234, dev)
+    raws_host = [r.cpu().numpy() for r in raws]
+    stg_np, luts_np = encode_batch(raws_host, threads=max(1, min(16, cores)))
+    log(f"prepared {count} experts in {time.time() - t0:.1f}s")
+    n_bytes = [r.shape[1] for r in raws_host]
+    stg = [torch.from_numpy(s).to(dev) for s in stg_np]
+    lut = torch.from_numpy(luts_np).to(dev)
+    dst = [torch.zeros_like(r) for r in raws]
+    todo = torch.arange(count, dtype=torch.int64, device=dev)
+    dst_row = torch.arange(count, dtype=torch.int64, device=dev)
+    no_cache = torch.full((count,), -1, dtype=torch.int64, device=dev)
+    alg = algorithmic_bytes(stg_np, n_bytes)
+
+    def step():
+        codec.decode_rows(todo, dst_row, no_cache, stg, dst, lut)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    ok = all(torch.equal(d, r) for d, r in zip(dst, raws))
+    if not ok:
+        raise SystemExit("decode output differs from the raw rows")
+    gbps = alg / (ms * 1e-3) / 1e9
+    raw_gbps = sum(n_bytes) * count / (ms * 1e-3) / 1e9
+    log(f"decode: {ms:.3f} ms/launch, {gbps:.1f} GB/s algorithmic, {raw_gbps:.1f} GB/s raw output")
+
+    # Sweep of rows per launch (32..256): same kernel, shorter todo.
+    sweep = {}
+    for r in (32, 64, 128):
+        if r >= count:
+            continue
+        t = todo[:r]
+        for _ in range(2):
+            codec.decode_rows(t, dst_row, no_cache, stg, dst, lut)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(5):
+            codec.decode_rows(t, dst_row, no_cache, stg, dst, lut)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_r = e0.elapsed_time(e1) / 5
+        sweep[str(r)] = round(algorithmic_bytes([s[:r] for s in stg_np], n_bytes) / (ms_r * 1e-3) / 1e9, 1)
+    sweep[str(count)] = round(gbps, 1)
+
+    # CPU baseline: the oracle's C decoder on a bounded sample, all cores.
+    sample = max(1, min(args.cpu_rows, count))
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for k in range(len(stg_np)):
+            out = codec_ref.decode_fast(stg_np[k][:sample], luts_np[:sample, k], n_bytes[k], threads=cores)
+            assert np.array_equal(out, raws_host[k][:sample])
+        reps += 1
+        if time.perf_counter() - t0 > args.cpu_seconds:
+            break
+    cpu_s = (time.perf_counter() - t0) / reps
+    cpu_gbps = algorithmic_bytes([s[:sample] for s in stg_np], n_bytes) / cpu_s / 1e9
+    log(f"cpu decode: {cpu_gbps:.2f} GB/s on {cores} threads ({sample} experts x {reps} reps)")
+    return {
+        "ms": ms,
+        "gbps": gbps,
+        "raw_gbps": raw_gbps,
+        "alg_bytes": alg,
+        "sweep": sweep,
+        "cpu": {"value": round(cpu_gbps, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                "sample": f"oracle C decoder (the reference's sequential decode rule), {sample} of the "
+                          f"{count} experts (w13+w2 rows), {reps} repetitions, threads over groups"},
+    }
+
+
+def bench_gather(args, dev):
+    """Slot gather from pinned host RAM vs the in-run host-link ceiling."""
+    from vllm_expert_pager import gather
+    from vllm_expert_pager.store import PinnedBuffer
+
+    n_bytes = [r * c for r, c in SHAPES]
+    rows = 64
+    K = 32
+    out = {}
+    for coherent in (True, False):
+        bufs = [PinnedBuffer(rows * n, coherent) for n in n_bytes]
+        host = [b.tensor(torch.uint8, (rows, n)) for b, n in zip(bufs, n_bytes)]
+        for h in host:
+            h.copy_(torch.randint(0, 256, h.shape, dtype=torch.uint8))
+        from vllm_expert_pager.gather import DeviceRows
+
+        src = [DeviceRows(h, b.device_ptr) for h, b in zip(host, bufs)]
+        dst = [torch.empty((K, n), dtype=torch.uint8, device=dev) for n in n_bytes]
+        scale = [torch.zeros((rows, 16), dtype=torch.int32, device=dev) for _ in n_bytes]
+        sdst = [torch.zeros((K, 16), dtype=torch.int32, device=dev) for _ in n_bytes]
+        todo = torch.arange(K, dtype=torch.int64, device=dev)
+        dst_row = torch.arange(rows, dtype=torch.int64, device=dev) % K
+        no_cache = torch.full((rows,), -1, dtype=torch.int64, device=dev)
+        src_row = torch.arange(rows, dtype=torch.int64, device=dev)
+        total = K * sum(n_bytes)
+
+        def run():
+            gather.gather_rows(todo, dst_row, no_cache, src_row, 0, src, dst, dst, None, scale, sdst)
+
+        for _ in range(2):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.gather_steps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.gather_steps
+        ok = all(torch.equal(dst[k].cpu(), host[k][:K]) for k in range(2))
+        # Host-link ceiling: the copy engine moving the same bytes, best of several.
+        best = 0.0
+        for _ in range(5):
+            e0.record()
+            for k in range(2):
+                dst[k].copy_(host[k][:K], non_blocking=True)
+            e1.record()
+            torch.cuda.synchronize()
+            best = max(best, total / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+        key = "fine" if coherent else "coarse"
+        out[key] = {"gbps": round(total / (ms * 1e-3) / 1e9, 2), "ceiling_gbps": round(best, 2), "ok": ok}
+        log(f"gather ({key}-grained pinned): {out[key]}")
+        for b in bufs:
+            b.free()
+    return out
+
+
+def bench_acquire(args, dev):
+    """Acquire of both tables for 40 layers inside one captured hipGraph."""
+    from vllm_expert_pager.acquire import AcquirePair
+    from vllm_expert_pager.table import ExpertTable
+
+    L, E, S, R = 40, 256, 32, 256
+    pairs = []
+    for _ in range(L):
+        v, r = ExpertTable(E, S, dev), ExpertTable(E, R, dev)
+        r.slot_of[:R] = r.experts[:R]
+        r.expert_in[:R] = r.experts[:R]
+        pairs.append(AcquirePair(v, r))
+    ids = torch.zeros((L, 1, 8), dtype=torch.int32, device=dev)
+    rng = np.random.default_rng(5)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for layer in range(L):
+            pairs[layer](ids[layer])
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for layer in range(L):
+                pairs[layer](ids[layer])
+    torch.cuda.synchronize()
+    perm = rng.permutation(E)
+    p = np.arange(1, E + 1, dtype=np.float64) ** -1.1
+    p /= p.sum()
+    steps = 50
+    host_ids = np.stack([[perm[rng.choice(E, 8, replace=False, p=p)] for _ in range(L)] for _ in range(steps)])
+    dev_ids = torch.from_numpy(host_ids.astype(np.int32)).to(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(3):
+        ids.copy_(dev_ids[i].view(L, 1, 8))
+        g.replay()
+    torch.cuda.synchronize()
+    total = 0.0
+    for i in range(steps):
+        ids.copy_(dev_ids[i].view(L, 1, 8))
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        total += e0.elapsed_time(e1)
+    us_layer = total / steps / L * 1e3
+    log(f"acquire: {us_layer:.2f} us/layer (graph of {L} layers, both tables)")
+    return {"us_per_layer": round(us_layer, 3)}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rows", type=int, default=256)
+    ap.add_argument("--cpu-rows", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--gather-steps", type=int, default=10)
+    ap.add_argument("--only-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        raise SystemExit(2)
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    from vllm_expert_pager import _native
+
+    _native.lib()  # fails loudly if the HIP library is not built
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cores = len(os.sched_getaffinity(0))
+
+    dec = bench_decode(args, dev, cores)
+    extras = {}
+    if not args.only_decode:
+        extras["gather"] = bench_gather(args, dev)
+        extras["acquire"] = bench_acquire(args, dev)
+    line = {
+        "metric": "Huffman decode GB/s (% HBM peak); gather GB/s; acquire us/layer; decode tok/s",
+        "value": round(dec["gbps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"codec only: batched GPU expansion of {args.rows} compressed experts per launch "
+                        "(w13 fp8 1024x2048 + w2 fp8 2048x512, N(0,0.02) e4m3 with 128x128 block scales, "
+                        "pitch 0.89)",
+            "rows_per_launch": args.rows,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(dec["gbps"], 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": dec["cpu"],
+        "decode_raw_output_gbps": round(dec["raw_gbps"], 2),
+        "decode_gbps_by_rows": dec["sweep"],
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,309 @@
+/*
+ * xp.h -- C ABI of libxp, the gfx950 (MI355X) expert-paging library.
+ *
+ * Every entry point takes plain pointers and sizes, returns an int status
+ * (XP_OK = 0) and never throws. On failure xp_last_error() describes the
+ * problem (thread-local, valid until the next failing call on that thread).
+ * GPU entry points take the hipStream_t they launch on as `void* stream`
+ * (NULL = the null stream); they only enqueue work, allocate nothing and
+ * never synchronise, so they can be captured into a hipGraph.
+ *
+ * Device pointers: all table, slab, staging, scale and LUT buffers live in
+ * HBM. RAM-tier rows and the request ring live in pinned host memory
+ * (xp_host_alloc); kernels read and write them over the host link through
+ * their device-visible address (xp_host_device_pointer).
+ *
+ * Each declaration names the reference interface it replaces
+ * (monochromegane/vllm-expert-pager v0.1.1, file:line).
+ */
+#ifndef XP_H
+#define XP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define XP_OK 0
+#define XP_E_ARG 1      /* bad argument (shape, size, null pointer) */
+#define XP_E_PITCH 2    /* compressed row does not fit in its pitch */
+#define XP_E_SHAPE 3    /* row length is not a multiple of the codec group */
+#define XP_E_HIP 4      /* a HIP runtime call failed */
+#define XP_E_LIMIT 5    /* a size exceeds what the kernel supports */
+
+/* Description of the last failure on this thread ("" if none). */
+const char* xp_last_error(void);
+/* Library version string. */
+const char* xp_version(void);
+
+/* ---- LRU tables (device state) ----
+ * One table per layer and tier. Same layout as ExpertTable
+ * (table.py:28-54): int64 tensors with one trailing sink element.
+ *   slot_of[E+1]    expert -> slot, -1 = not cached
+ *   expert_in[S+1]  slot -> expert, -1 = free
+ *   last_used[S+1]  step stamp, 0 = free
+ *   step[1]         starts at 1
+ *   hits[1], misses[1]
+ */
+typedef struct xp_table {
+  int64_t* slot_of;
+  int64_t* expert_in;
+  int64_t* last_used;
+  int64_t* step;
+  int64_t* hits;
+  int64_t* misses;
+  int64_t num_experts; /* E */
+  int64_t num_slots;   /* S (or R for the RAM tier) */
+} xp_table;
+
+/* Largest table the acquire kernels take (slots per table). */
+#define XP_MAX_SLOTS 1024
+/* Largest expert count the table kernels take. */
+#define XP_MAX_EXPERTS 2048
+
+/* Update the VRAM table and the RAM table from one step's routing, in one
+ * launch. topk holds K expert ids (int32 if topk_elem_bytes == 4, int64 if 8);
+ * negative ids are ignored. Requires K <= vram->num_slots and
+ * K <= ram->num_slots. Writes expert_map[E] (int32, slot or -1 for unneeded
+ * experts; from the VRAM table), vram_slot[E] / ram_slot[E] (slot of each
+ * expert, meaningful for needed experts) and vram_todo[K] / ram_todo[K]
+ * (misses in ascending expert id, then -1).
+ * Replaces AcquirePair.__call__ (acquire.py:168-185) and its kernel
+ * _acquire_pair_kernel / _acquire (acquire.py:25-141). */
+int xp_acquire_pair(const void* topk, int topk_elem_bytes, int64_t K,
+                    const xp_table* vram, const xp_table* ram,
+                    int32_t* expert_map, int64_t* vram_slot, int64_t* vram_todo,
+                    int64_t* ram_slot, int64_t* ram_todo, void* stream);
+
+/* One table's acquire. expert_map_i64 (nullable) receives slot or -1 as
+ * int64 (the torch version's return value), expert_map_i32 (nullable) the
+ * same as int32. Requires K <= t->num_slots.
+ * Replaces ExpertTable.acquire (table.py:75-128). */
+int xp_table_acquire(const void* topk, int topk_elem_bytes, int64_t K,
+                     const xp_table* t, int64_t* expert_map_i64,
+                     int32_t* expert_map_i32, int64_t* slot_out, int64_t* todo,
+                     void* stream);
+
+/* need[e] = 1 if expert e appears among the n ids, else 0 (uint8[E]).
+ * Replaces ExpertTable.need_mask (table.py:58-71). */
+int xp_need_mask(const void* topk, int topk_elem_bytes, int64_t n,
+                 int64_t num_experts, uint8_t* need, void* stream);
+
+/* out[E]: the experts set in mask[E], packed from the front, then -1.
+ * Replaces ExpertTable.pack (table.py:132-138). */
+int xp_pack(const uint8_t* mask, int64_t num_experts, int64_t* out,
+            void* stream);
+
+/* Seed the RAM table `ram` from a prefill's routing: acquire the
+ * max(R - S, 1) most referenced experts (ties: lower expert id first), then
+ * the VRAM table's experts that are readable (in RAM or needed), without
+ * counting hits or misses. need[E] is xp_need_mask of the same ids.
+ * Replaces ExpertTable.seed (table.py:140-171). */
+int xp_table_seed(const xp_table* ram, const xp_table* vram, const void* topk,
+                  int topk_elem_bytes, int64_t n, const uint8_t* need,
+                  void* stream);
+
+/* Plan the chunks of a working-slab step after the RAM table update.
+ * before[E] = RAM slot_of before the update, cached_row[E] = VRAM slot_of,
+ * W = working rows. With N = ceil(E / W) + 1 chunks, writes dst_row[E],
+ * src_row[E], maps[N*E] (int64, row or -1), and the listings todo, ssd,
+ * late (int64[N*W] each).
+ * Replaces ExpertTable.plan_chunks (table.py:173-247). */
+int xp_plan_chunks(const xp_table* ram, const int64_t* before,
+                   const uint8_t* need, const int64_t* cached_row, int64_t W,
+                   int64_t ram_base, int64_t working_base, int64_t* dst_row,
+                   int64_t* src_row, int64_t* maps, int64_t* todo,
+                   int64_t* ssd, int64_t* late, void* stream);
+
+/* ---- Gather (RAM tier / cache slab -> slab or staging) ---- */
+
+/* One weight name (w13 or w2) of a gather. Sizes in bytes, multiples of 16;
+ * all row bases 16-byte aligned. */
+typedef struct xp_gather_name {
+  const void* src;       /* RAM-tier rows, device-visible pinned memory */
+  int64_t src_pitch;     /* bytes per RAM-tier row (pitch P, or N raw) */
+  int64_t src_rows;      /* rows in src (row indices are checked against it) */
+  const void* cache;     /* cache slab rows (raw, N bytes each), HBM */
+  int64_t cache_rows;
+  void* dst;             /* destination slab rows (raw, N bytes each), HBM */
+  int64_t dst_rows;
+  int64_t row_bytes;     /* N */
+  void* stg;             /* compressed staging rows (P bytes each), or NULL */
+  int64_t stg_rows;
+  const void* scale;     /* scales of every expert, scale_bytes per expert */
+  void* scale_dst;       /* scales in slot order (dst_rows rows) */
+  int64_t scale_bytes;
+} xp_gather_name;
+
+/* Host<->device request ring (layout of store.py:434-457).
+ * req = [re-publishes, give-ups] + ring slots of [seq, layer, expert[block],
+ * row[block]] (int64, pinned coherent); done[1] (pinned coherent);
+ * seq[1] (HBM). */
+typedef struct xp_ring {
+  int64_t* req;
+  int64_t* done;
+  int64_t* seq;
+  int64_t block;
+  int64_t ring;
+} xp_ring;
+
+/* Copy the rows and scales of the experts in todo[K] (-1 = empty).
+ * Expert e with cache_row[e] >= 0 is copied raw from the cache slab row
+ * cache_row[e] to dst row dst_row[e]; otherwise from RAM-tier row
+ * src_row[e] + base: to staging row j (its index in todo) when the name has
+ * stg, else to dst row dst_row[e]. The scale row of e is copied to
+ * scale_dst row dst_row[e]. With ring != NULL, the same launch publishes the
+ * experts of ssd_todo[K] to the host ring for layer `layer`, waits for their
+ * done, and skips them in the copy.
+ * Replaces gather_rows (gather.py:328-393) and _gather_rows_kernel
+ * (gather.py:51-194). */
+int xp_gather_rows(const int64_t* todo, int64_t K, int64_t num_experts,
+                   const int64_t* dst_row, const int64_t* cache_row,
+                   const int64_t* src_row, int64_t base,
+                   const xp_gather_name* names, int num_names,
+                   const int64_t* ssd_todo, int64_t layer, const xp_ring* ring,
+                   void* stream);
+
+/* Number of copying workgroups of xp_gather_rows (the requests it keeps in
+ * flight over the host link scale with it). Default 32. */
+int xp_gather_set_blocks(int blocks);
+
+/* Publish the experts of todo[K] to the ring and wait for done. Expert e
+ * lands in RAM-tier row row[e] + base. No-op if todo is empty.
+ * Replaces fetch_rows (gather.py:396-407). */
+int xp_fetch_rows(const int64_t* todo, int64_t K, int64_t num_experts,
+                  const int64_t* row,
+                  int64_t base, int64_t layer, const xp_ring* ring,
+                  void* stream);
+
+/* Publish without waiting; the published seq goes to ticket[1] (HBM).
+ * Replaces fetch_publish_rows (gather.py:410-431). */
+int xp_fetch_publish_rows(const int64_t* todo, int64_t K,
+                          int64_t num_experts, const int64_t* row,
+                          int64_t base, int64_t layer, const xp_ring* ring,
+                          int64_t* ticket, void* stream);
+
+/* Wait until done >= ticket[0]; re-publish every `retry` interval and give up
+ * after `giveup` re-publishes (both in xp_fetch_set_timing). No-op if todo is
+ * empty. Replaces fetch_wait_rows (gather.py:434-439). */
+int xp_fetch_wait_rows(const int64_t* todo, int64_t K, const xp_ring* ring,
+                       const int64_t* ticket, void* stream);
+
+/* Wait policy of the fetch kernels: re-publish after retry_us microseconds
+ * without done, give up after giveup re-publishes. Defaults 500000 us and 8
+ * (the reference: 2^18 spins, about 0.5 to 1.2 s, and 8; gather.py:36-48).
+ * Affects launches made after the call. */
+int xp_fetch_set_timing(int64_t retry_us, int64_t giveup);
+
+/* ---- Codec (per-row fp8 exponent Huffman, format of codec.py:1-41) ---- */
+
+#define XP_LIMIT 9
+#define XP_LUT_BYTES 512
+#define XP_CHUNK 512
+#define XP_LANES 32
+
+/* One weight name of a decode. */
+typedef struct xp_decode_name {
+  const void* stg;    /* compressed rows, pitch bytes apart (HBM) */
+  int64_t pitch;
+  int64_t stg_rows;
+  void* dst;          /* raw destination rows, row_bytes apart (HBM) */
+  int64_t dst_rows;
+  int64_t row_bytes;  /* N, multiple of chunk * 32 */
+} xp_decode_name;
+
+/* Expand staging row j (the j-th entry of todo) into dst row dst_row[e] for
+ * every name. Skips -1 entries, experts with cache_row[e] >= 0 and (when
+ * skip != NULL) experts listed in skip[K]. lut is the layer's
+ * uint8[E][num_names][512]. chunk = values per lane (512 in production).
+ * Replaces decode_rows (codec.py:297-327) and _decode_rows_kernel /
+ * _decode_group (codec.py:204-289). */
+int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts,
+                   const int64_t* dst_row, const int64_t* cache_row,
+                   const uint8_t* lut,
+                   const xp_decode_name* names, int num_names,
+                   const int64_t* skip, int64_t chunk, void* stream);
+
+/* Host encoder: compress raw[n] (n multiple of chunk*32) into record[pitch]
+ * (zero padded) and lut[512]. *needed receives the record's used bytes.
+ * Returns XP_E_PITCH if it does not fit, XP_E_SHAPE if n is not a multiple.
+ * Replaces encode (codec.py:125-193). */
+int xp_encode_row(const uint8_t* raw, int64_t n, int64_t chunk,
+                  uint8_t* record, int64_t pitch, uint8_t* lut,
+                  int64_t* needed);
+
+/* Code of a 16-symbol histogram: lengths[16], bit-reversed codes[16] and
+ * lut[512] ((sym << 4) | len). Replaces code_lengths / Code
+ * (codec.py:61-114). */
+int xp_code_build(const int64_t* hist, int32_t* lengths, int32_t* codes,
+                  uint8_t* lut);
+
+/* ---- Pinned host memory ---- */
+
+/* hipHostMalloc of `bytes` (coherent != 0: fine-grained, else
+ * coarse-grained), mapped for the device. */
+int xp_host_alloc(void** ptr, int64_t bytes, int coherent);
+int xp_host_free(void* ptr);
+/* The device-visible address of pinned host memory. */
+int xp_host_device_pointer(void** dev, void* host);
+
+/* ---- SSD request server (host threads). Same ABI as the reference's
+ * embedded C server (store.py:253-308). ---- */
+typedef struct ssd_t ssd_t;
+ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L,
+                 long E, long rows, long record_bytes, int names,
+                 void** pinned, long* pitch, int nworkers);
+void ssd_stop(ssd_t* s);
+void ssd_stats(ssd_t* s, long* fetches, long* reads, double* io_seconds,
+               long* missed);
+const char* ssd_error(ssd_t* s);
+void ssd_test_delay(ssd_t* s, double seconds);
+
+/* ---- MoE expert compute on the slab (prefill overflow and decode) ----
+ * These replace the vLLM fused fp8 MoE the reference hands expert_map to
+ * (super().forward_modular, experts.py:579-604) and its moe_sum intercept
+ * (experts.py:546-556). Weights are fp8 e4m3 (OCP) with 128x128 fp32 block
+ * scales; activations are quantised per token and 128-column group.
+ *   w13 slab: [slots][2I][H] fp8, scale [slots][2I/128][H/128] fp32
+ *   w2  slab: [slots][H][I]  fp8, scale [slots][H/128][I/128]  fp32
+ */
+
+/* Quantise x[T][H] (bf16) to fp8 xq[T][H] and scales xs[T][H/128] (fp32).
+ * H multiple of 128. */
+int xp_quant_tokens(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq,
+                    float* xs, void* stream);
+
+/* Route (token, k) pairs to slab slots: for every pair whose expert e has
+ * expert_map[e] >= 0 (ids < 0 or >= E are skipped), list the pair under that
+ * slot. Writes counts[slots] and pairs[slots][cap] (pair = t*topk + k, in
+ * ascending pair order). cap = max pairs per slot kept (T*topk covers all).
+ * Returns XP_E_LIMIT via the device flag overflow[0] != 0 if a slot had more
+ * than cap pairs. */
+int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T,
+                 int64_t topk, const int32_t* expert_map, int64_t num_experts,
+                 int64_t slots, int64_t cap, int32_t* counts, int32_t* pairs,
+                 int32_t* overflow, void* stream);
+
+/* Expert FFN for every listed pair: out[pair][H] (bf16) =
+ * topk_weight[pair] * (w2 . q(silu(gate) * up)), gate/up from w13 . xq.
+ * act/acts are workspaces [T*topk][I] fp8 and [T*topk][I/128] fp32.
+ * Pairs that are not listed are not written. */
+int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T,
+                   int64_t topk, const float* topk_weight, int64_t H,
+                   int64_t I, const uint8_t* w13, const float* w13_scale,
+                   const uint8_t* w2, const float* w2_scale, int64_t slots,
+                   int64_t cap, const int32_t* counts, const int32_t* pairs,
+                   uint8_t* act, float* acts, uint16_t* out, void* stream);
+
+/* out[t][H] = bf16(sum_k fp32(contrib[t*topk + k][H])), summed in k order.
+ * The single top-k combine (experts.py:479-487). */
+int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk,
+                    int64_t H, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XP_H */

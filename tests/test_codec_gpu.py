@@ -1,0 +1,191 @@
+"""GPU parity of the Huffman row expansion (bit-exact bytes).
+
+Checks the decoder against the reference encoder's golden records, against
+the oracle (round trips for the reference's four distributions), the
+todo/skip/cache_row rules of the reference's tests/test_codec.py, full-size
+synthetic expert rows (w13 2 MiB + w2 1 MiB of N(0, 0.02) weights quantised to
+fp8 e4m3 with 128x128 block scales) in batches, and hipGraph replay.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import codec_ref
+
+pytestmark = pytest.mark.gpu
+
+CHUNK = 64
+N = 2 * CHUNK * 32
+EXP_P = [0.0] * 4 + [0.001, 0.002, 0.004, 0.008, 0.016, 0.032, 0.064, 0.125, 0.228, 0.315, 0.188, 0.015]
+
+
+def _codec():
+    from vllm_expert_pager import codec
+
+    return codec
+
+
+def rows(seed, n=N, p=EXP_P):
+    rng = np.random.default_rng(seed)
+    p = np.asarray(p, np.float64)
+    exp = rng.choice(16, size=n, p=p / p.sum()).astype(np.uint8)
+    sm = rng.integers(0, 256, size=n, dtype=np.uint8) & 0x87
+    return sm | (exp << 3)
+
+
+def fp8_expert(seed, shape):
+    """N(0, 0.02) weights quantised to e4m3 with 128x128 block scales, as uint8."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(shape, generator=g) * 0.02
+    r, c = shape
+    blk = w.view(r // 128, 128, c // 128, 128)
+    s = blk.abs().amax(dim=(1, 3), keepdim=True).clamp(min=1e-12) / 448.0
+    q = (blk / s).to(torch.float8_e4m3fn).view(r, c)
+    return q.view(torch.uint8).numpy().reshape(-1)
+
+
+def decode_one(codec, rec, lut, n, chunk, dst_row=0):
+    dev = torch.device("cuda")
+    stg = [torch.from_numpy(rec.reshape(1, -1)).to(dev)]
+    dst = [torch.zeros((1, n), dtype=torch.uint8, device=dev)]
+    lut_t = torch.from_numpy(lut.reshape(1, 1, -1)).to(dev)
+    todo = torch.zeros((1,), dtype=torch.int64, device=dev)
+    rowmap = torch.zeros((1,), dtype=torch.int64, device=dev)
+    cache_row = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    codec.decode_rows(todo, rowmap, cache_row, stg, dst, lut_t, chunk=chunk)
+    torch.cuda.synchronize()
+    return dst[0][0].cpu().numpy()
+
+
+def test_golden_records():
+    codec = _codec()
+    g = np.load(os.path.join(GOLDEN, "codec_vectors.npz"), allow_pickle=False)
+    for name in g["cases"]:
+        raw = g[f"{name}_raw"]
+        out = decode_one(codec, g[f"{name}_record"], g[f"{name}_lut"], raw.size, int(g[f"{name}_chunk"]))
+        np.testing.assert_array_equal(out, raw, err_msg=str(name))
+
+
+@pytest.mark.parametrize("dist", ["realistic", "uniform", "geometric", "constant", "long_codes"])
+@pytest.mark.parametrize("chunk", [64, 512])
+def test_round_trip(dist, chunk):
+    codec = _codec()
+    n = 2 * chunk * 32
+    raw = {
+        "realistic": lambda: rows(0, n),
+        "uniform": lambda: rows(1, n, [1.0] * 16),
+        "geometric": lambda: rows(2, n, [2.0**k for k in range(16)]),
+        "constant": lambda: np.full(n, 13 << 3, np.uint8),
+        # first half one exponent, second half uniform: the second half's codes
+        # are long, so its groups carry more Huffman words than the LDS stage
+        # holds at chunk 512
+        "long_codes": lambda: np.concatenate([np.full(n // 2, 13 << 3, np.uint8), rows(5, n // 2, [1.0] * 16)]),
+    }[dist]()
+    pitch = codec_ref.pitch_of(n, 1.6, 4096)
+    rec, lut = codec_ref.encode(raw, pitch, chunk)
+    np.testing.assert_array_equal(decode_one(codec, rec, lut, n, chunk), raw)
+
+
+def test_follows_todo_and_skips():
+    """tests/test_codec.py:118-154 of the reference, restated."""
+    codec = _codec()
+    dev = torch.device("cuda")
+    E = 8
+    ns = (N, N // 2)
+    pitches = [codec_ref.pitch_of(n, 1.25, 4096) for n in ns]
+    raws = {e: [rows(10 * e + k, n) for k, n in enumerate(ns)] for e in (3, 5, 6)}
+    staging = [torch.zeros((3, p), dtype=torch.uint8, device=dev) for p in pitches]
+    lut = torch.zeros((E, 2, 512), dtype=torch.uint8, device=dev)
+    for j, e in enumerate((3, 5, 6)):
+        for k in range(2):
+            rec, lt = codec_ref.encode(raws[e][k], pitches[k], CHUNK)
+            staging[k][j] = torch.from_numpy(rec).to(dev)
+            lut[e, k] = torch.from_numpy(lt).to(dev)
+    dst = [torch.zeros((2, n), dtype=torch.uint8, device=dev) for n in ns]
+    todo = torch.tensor([3, 5, 6], dtype=torch.int64, device=dev)
+    dst_row = torch.zeros((E,), dtype=torch.int64, device=dev)
+    dst_row[3], dst_row[5], dst_row[6] = 1, 0, 0
+    cache_row = torch.full((E,), -1, dtype=torch.int64, device=dev)
+    cache_row[5] = 2
+    skip = torch.tensor([6, -1, -1], dtype=torch.int64, device=dev)
+    codec.decode_rows(todo, dst_row, cache_row, staging, dst, lut, skip=skip, chunk=CHUNK)
+    torch.cuda.synchronize()
+    for k in range(2):
+        assert np.array_equal(dst[k][1].cpu().numpy(), raws[3][k])
+        assert not dst[k][0].any()
+    codec.decode_rows(todo, dst_row, cache_row, staging, dst, lut, chunk=CHUNK)
+    torch.cuda.synchronize()
+    for k in range(2):
+        assert np.array_equal(dst[k][0].cpu().numpy(), raws[6][k])
+
+
+def _expert_batch(codec, count, seed):
+    """Compressed staging (count rows per name) for synthetic full-size experts, plus the raw rows."""
+    shapes = ((1024, 2048), (2048, 512))
+    raws = [np.stack([fp8_expert(seed * 1000 + 2 * j + k, shapes[k]) for j in range(count)]) for k in range(2)]
+    pitches = [codec.pitch_of(r.shape[1], 0.89, 4096) for r in raws]
+    stg = [np.empty((count, p), np.uint8) for p in pitches]
+    luts = np.empty((count, 2, 512), np.uint8)
+    for k in range(2):
+        for j in range(count):
+            codec.encode_into(raws[k][j], stg[k][j], luts[j, k])
+    return raws, stg, luts
+
+
+def test_full_size_expert_rows():
+    codec = _codec()
+    dev = torch.device("cuda")
+    count = 12
+    raws, stg_np, luts_np = _expert_batch(codec, count, seed=1)
+    stg = [torch.from_numpy(s).to(dev) for s in stg_np]
+    lut = torch.from_numpy(luts_np).to(dev)
+    dst = [torch.zeros((count, r.shape[1]), dtype=torch.uint8, device=dev) for r in raws]
+    todo = torch.arange(count, dtype=torch.int64, device=dev)
+    dst_row = torch.arange(count - 1, -1, -1, dtype=torch.int64, device=dev)  # reversed rows
+    cache_row = torch.full((count,), -1, dtype=torch.int64, device=dev)
+    codec.decode_rows(todo, dst_row, cache_row, stg, dst, lut)
+    torch.cuda.synchronize()
+    for k in range(2):
+        got = dst[k].cpu().numpy()[::-1]
+        np.testing.assert_array_equal(got, raws[k])
+        # and the oracle decodes the same records to the same bytes
+        np.testing.assert_array_equal(codec_ref.decode_fast(stg_np[k][:2], luts_np[:2, k], raws[k].shape[1]),
+                                      raws[k][:2])
+
+
+def test_decode_in_graph_replays():
+    codec = _codec()
+    dev = torch.device("cuda")
+    count = 4
+    raws, stg_np, luts_np = _expert_batch(codec, count, seed=2)
+    stg = [torch.from_numpy(s).to(dev) for s in stg_np]
+    lut = torch.from_numpy(luts_np).to(dev)
+    dst = [torch.zeros((count, r.shape[1]), dtype=torch.uint8, device=dev) for r in raws]
+    todo = torch.full((count,), -1, dtype=torch.int64, device=dev)
+    dst_row = torch.arange(count, dtype=torch.int64, device=dev)
+    cache_row = torch.full((count,), -1, dtype=torch.int64, device=dev)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        codec.decode_rows(todo, dst_row, cache_row, stg, dst, lut)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            codec.decode_rows(todo, dst_row, cache_row, stg, dst, lut)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        pick = [(rep + i) % count for i in range(2)]
+        for d in dst:
+            d.zero_()
+        todo.copy_(torch.tensor(pick + [-1] * (count - 2), device=dev))
+        g.replay()
+        torch.cuda.synchronize()
+        for k in range(2):
+            got = dst[k].cpu().numpy()
+            for j in range(count):
+                if j in pick:
+                    np.testing.assert_array_equal(got[j], raws[k][j], err_msg=f"replay {rep}")
+                else:
+                    assert not got[j].any()

@@ -1,0 +1,119 @@
+"""Lossless fp8 e4m3 row codec: host encoder and batched GPU decoder (replaces codec.py).
+
+Format (codec.py:1-41, kept byte for byte): per row, a length-limited
+canonical Huffman code over the 4-bit exponent, sign + mantissa nibbles kept
+raw; a record of ``pitch`` bytes = int32 gstart[G+1] | nibble words in
+(group, word, lane) order | Huffman words per group in refill order. The
+512-byte LUT ((sym << 4) | len) lives outside the record.
+
+``encode`` runs on the host (C++, csrc/codec_host.cpp); ``decode_rows``
+expands staging rows on the GPU (csrc/codec.hip).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from vllm_expert_pager import _native as nat
+
+LIMIT = 9
+LUT_BYTES = 1 << LIMIT
+CHUNK = 512
+LANES = 32
+GROUP = CHUNK * LANES
+
+
+def _build(hist) -> tuple[list[int], list[int], list[int]]:
+    h = (ctypes.c_int64 * 16)(*[int(x) for x in hist])
+    lengths = (ctypes.c_int32 * 16)()
+    codes = (ctypes.c_int32 * 16)()
+    lut = (ctypes.c_uint8 * LUT_BYTES)()
+    nat.call("xp_code_build", h, lengths, codes, lut)
+    return list(lengths), list(codes), list(lut)
+
+
+def code_lengths(hist: list[int], limit: int = LIMIT) -> list[int]:
+    """Length-limited Huffman code lengths (codec.py:76-87). Only LIMIT is supported."""
+    if limit != LIMIT:
+        raise ValueError(f"only limit={LIMIT} is supported")
+    return _build(hist)[0]
+
+
+class Code:
+    """Huffman code for the 16 exponent symbols (codec.py:90-114)."""
+
+    def __init__(self, hist: list[int]) -> None:
+        self.lengths, self.codes, self.lut = _build(hist)
+
+
+def pitch_of(n_values: int, ratio: float, align: int) -> int:
+    """Fixed record length: ratio times the raw size rounded up to align (codec.py:117-119)."""
+    return -(-int(n_values * ratio) // align) * align
+
+
+def groups(n_bytes: int, chunk: int = CHUNK) -> int:
+    """Number of groups in one row (codec.py:292-294)."""
+    return n_bytes // (chunk * LANES)
+
+
+def encode_into(raw: np.ndarray, record: np.ndarray, lut: np.ndarray, chunk: int = CHUNK) -> int:
+    """Encode uint8 ``raw`` into the preallocated ``record`` (its length is the pitch) and ``lut``.
+
+    Returns the record's used bytes. Raises ValueError like codec.py:133-166.
+    """
+    assert raw.dtype == np.uint8 and record.dtype == np.uint8 and lut.dtype == np.uint8
+    assert raw.flags.c_contiguous and record.flags.c_contiguous and lut.size == LUT_BYTES
+    needed = ctypes.c_int64()
+    nat.call("xp_encode_row", raw.ctypes.data, raw.size, chunk, record.ctypes.data, record.size,
+             lut.ctypes.data, ctypes.byref(needed))
+    return needed.value
+
+
+def encode(raw: torch.Tensor, pitch: int, chunk: int = CHUNK) -> tuple[torch.Tensor, torch.Tensor]:
+    """Compress a uint8 row (N,). Returns ``(record of pitch bytes, 512 B LUT)`` on raw's device (codec.py:125-193)."""
+    host = raw.reshape(-1).to(torch.uint8).contiguous().cpu().numpy()
+    record = np.empty(pitch, np.uint8)
+    lut = np.empty(LUT_BYTES, np.uint8)
+    encode_into(host, record, lut, chunk)
+    return torch.from_numpy(record).to(raw.device), torch.from_numpy(lut).to(raw.device)
+
+
+def decode_rows(
+    todo: torch.Tensor,
+    dst_row: torch.Tensor,
+    cache_row: torch.Tensor,
+    staging: list[torch.Tensor],
+    dst: list[torch.Tensor],
+    lut: torch.Tensor,
+    skip: torch.Tensor | None = None,
+    chunk: int = CHUNK,
+) -> None:
+    """Expand ``staging[name][j]`` into ``dst[name][dst_row[todo[j]]]`` (codec.py:297-327).
+
+    ``staging`` is ``(*, pitch)`` uint8, ``dst`` ``(*, N)`` uint8, ``lut`` this
+    layer's ``(E, names, 512)``. Experts with ``cache_row[e] >= 0`` and, with
+    ``skip``, the experts in that list are skipped.
+    """
+    for t, what in ((todo, "todo"), (dst_row, "dst_row"), (cache_row, "cache_row"), (lut, "lut")):
+        nat.require_device(t, what)
+    todo = todo.to(torch.int64).contiguous()
+    dst_row = dst_row.to(torch.int64).contiguous()
+    cache_row = cache_row.to(torch.int64).contiguous()
+    skip_t = None if skip is None else skip.to(torch.int64).contiguous()
+    lut = lut.contiguous()
+    n = len(dst)
+    names = (nat.XpDecodeName * n)()
+    for i in range(n):
+        s, d = staging[i], dst[i]
+        names[i] = nat.XpDecodeName(
+            s.data_ptr(), s.shape[1] * s.element_size(), s.shape[0],
+            d.data_ptr(), d.shape[0], d.shape[1] * d.element_size(),
+        )
+    nat.call(
+        "xp_decode_rows", todo.data_ptr(), todo.shape[0], dst_row.shape[0], dst_row.data_ptr(),
+        cache_row.data_ptr(), lut.data_ptr(), names, n, None if skip_t is None else skip_t.data_ptr(),
+        chunk, nat.stream(),
+    )
