@@ -179,7 +179,8 @@ def test_decode_in_graph_replays():
         pick = [(rep + i) % count for i in range(2)]
         for d in dst:
             d.zero_()
-        todo.copy_(torch.tensor(pick + [-1] * (count - 2), device=dev))
+        # staging row j holds expert j's record, so expert j stays at position j
+        todo.copy_(torch.tensor([j if j in pick else -1 for j in range(count)], device=dev))
         g.replay()
         torch.cuda.synchronize()
         for k in range(2):

@@ -2,24 +2,35 @@
 //
 // One 64-lane wave decodes TWO 32-lane groups side by side (lanes 0-31 and
 // 32-63). Each lane owns one chunk and keeps the last two Huffman words it
-// loaded as a 64-bit funnel {hi, lo} with a bit position pos, where the
-// reference's fill level is 64 - pos: the refill rule "fewer than LIMIT bits
-// left" (codec.py:227-237) becomes pos > 64 - LIMIT. Refilling lanes of a
-// group take consecutive words from the group's read position; the offset
-// of a lane is the popcount of refilling lanes below it in its half of the
-// wave ballot (mbcnt), so the word order is exactly the encoder's
-// (symbol index, lane) refill order. The group's Huffman words are staged
-// in LDS once (coalesced), the 512-entry LUT is split into a length table
-// and a pre-shifted exponent table in LDS, and the sign/mantissa nibbles are
-// read as coalesced 32-bit words, 8 values each.
+// loaded as a 64-bit funnel {hi, lo} with a bit position pos; the
+// reference's fill level is 64 - pos, so its refill rule "fewer than LIMIT
+// bits left" (codec.py:227-237) becomes pos > 64 - LIMIT. At each symbol the
+// refilling lanes of a group take consecutive words from the group's read
+// position, a lane's offset being the number of refilling lanes below it in
+// its half of the wave ballot (mbcnt) -- exactly the encoder's
+// (symbol index, lane) word order.
+//
+// Memory: the group's Huffman words stream through a 512-word ring in LDS
+// (plus a mirror of its head, so an iteration's reads never wrap), filled
+// with coalesced loads issued one 8-symbol iteration ahead of use; the
+// 512-entry LUT is split into a length table and a pre-shifted exponent
+// table in LDS; the sign/mantissa nibbles arrive as coalesced 32-bit words
+// (8 values each), prefetched an iteration ahead.
 #include "common.h"
 
 namespace xp {
 namespace {
 
-constexpr int kThreads = 256;                    // 4 waves
-constexpr int kGroupsPerBlock = 2 * kThreads / 64;  // 8
-constexpr int kCapWords = 1536;                  // LDS staging per group (6 KiB)
+constexpr int kThreads = 256;                  // 4 waves
+constexpr int kChains = 2;                     // independent chunk streams per lane
+constexpr int kGroupsPerWave = 2 * kChains;    // lanes 0-31 and 32-63 of each chain
+constexpr int kGroupsPerBlock = kGroupsPerWave * kThreads / 64;  // 16
+constexpr uint32_t kRing = 256;                // ring words per group
+constexpr uint32_t kHalf = 4;                  // symbols between ring maintenance
+constexpr uint32_t kAhead = kHalf * 32;        // words a half-iteration may consume
+constexpr uint32_t kMirror = kAhead + 32;      // reads of a half never wrap
+constexpr uint32_t kRingPad = kRing + kMirror;
+constexpr uint32_t kFetch = 32;                // words requested per half-iteration
 constexpr int kLimit = XP_LIMIT;
 
 struct NameDev {
@@ -47,73 +58,118 @@ struct DecodeArgs {
   int blocks_per_row;
 };
 
-// Sign + mantissa of 8 values (one nibble word) placed in their output bytes:
-// byte k = (s_k & 8) << 4 | (s_k & 7). The exponent field is left zero.
-__device__ __forceinline__ void nibble_template(uint32_t x, uint32_t& t_lo, uint32_t& t_hi) {
+// Sign + mantissa of 8 values (one nibble word) in their output bytes:
+// byte k = (s_k & 8) << 4 | (s_k & 7); the exponent field is left zero.
+__device__ __forceinline__ uint2 nibble_template(uint32_t x) {
   const uint32_t ev = (x & 0x07070707u) | ((x << 4) & 0x80808080u);  // nibbles 0,2,4,6
   const uint32_t od = ((x >> 4) & 0x07070707u) | (x & 0x80808080u);  // nibbles 1,3,5,7
-  t_lo = __builtin_amdgcn_perm(od, ev, 0x05010400u);
-  t_hi = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+  return make_uint2(__builtin_amdgcn_perm(od, ev, 0x05010400u), __builtin_amdgcn_perm(od, ev, 0x07030602u));
 }
 
-template <bool kLds>
-__device__ __forceinline__ void decode_lanes(const uint32_t* __restrict__ words, int64_t nwords_limit,
-                                             const uint32_t* __restrict__ nib, uint2* __restrict__ out, int msteps,
-                                             bool valid, bool upper, const uint8_t* s_len, const uint8_t* s_sym) {
-  uint32_t lo = 0, hi = 0;
-  uint32_t pos = valid ? 64u : 0u;  // 64: nothing loaded yet, so the first step refills
-  uint32_t rp = 0;                  // words of this group consumed so far (uniform per half)
-  uint32_t x_next = valid ? nib[0] : 0u;
-  for (int m = 0; m < msteps; ++m) {
-    const uint32_t x = x_next;
-    if (valid && m + 1 < msteps) x_next = nib[(m + 1) * 32];
-    uint32_t o_lo, o_hi;
-    nibble_template(x, o_lo, o_hi);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const bool refill = valid && pos > 64u - kLimit;
-      const unsigned long long mask = __ballot(refill);
-      const uint32_t c_lo = __popc(static_cast<uint32_t>(mask));
-      const uint32_t c_hi = __popc(static_cast<uint32_t>(mask >> 32));
-      if (refill) {
-        const uint32_t pre = lane_prefix(mask) - (upper ? c_lo : 0u);
-        uint32_t w;
-        if (kLds) {
-          w = words[rp + pre];
-        } else {
-          int64_t idx = static_cast<int64_t>(rp + pre);
-          if (idx >= nwords_limit) idx = nwords_limit - 1;
-          w = nwords_limit > 0 ? words[idx] : 0u;
-        }
-        lo = hi;
-        hi = w;
-        pos -= 32u;
-      }
-      rp += upper ? c_hi : c_lo;
-      const uint64_t buf = (static_cast<uint64_t>(hi) << 32) | lo;
-      const uint32_t idx = static_cast<uint32_t>(buf >> (pos & 63u)) & (XP_LUT_BYTES - 1);
-      const uint32_t len = s_len[idx];
-      const uint32_t sym = s_sym[idx];
-      pos += valid ? len : 0u;
-      if (k < 4)
-        o_lo |= sym << (8 * k);
-      else
-        o_hi |= sym << (8 * (k - 4));
-    }
-    if (valid) out[m] = make_uint2(o_lo, o_hi);
+// Ring of one group: word w of the group's stream sits in slot w % kRing,
+// and also in slot w % kRing + kRing when that slot is below kMirror.
+__device__ __forceinline__ void ring_put(uint32_t* ring, uint32_t w_index, uint32_t value) {
+  const uint32_t s = w_index & (kRing - 1);
+  ring[s] = value;
+  if (s < kMirror) ring[s + kRing] = value;
+}
+
+// One lane's stream: a chunk of the group of this lane's half, plus the
+// state of that group's ring (uniform over the half).
+struct Chain {
+  uint64_t buf;      // {hi, lo}: the last two words loaded
+  uint32_t pos;      // next bit in buf; the fill level is 64 - pos
+  uint32_t rp;       // words of the group consumed
+  uint32_t fe;       // ring holds words [rp, fe)
+  uint32_t q;        // words requested so far (landed or in flight)
+  uint32_t a_base, a_n, a_val;  // request in flight, issued one half earlier
+  uint32_t b_base, b_n, b_val;  // request in flight, issued this half
+  uint32_t ab0;      // byte address of word rp in LDS at the half's start
+  uint32_t x_next;   // nibble word of the next iteration
+  uint32_t count;    // Huffman words of the group
+  uint32_t wlast;    // last readable word index (0 for an empty group)
+  const uint32_t* wsrc;  // the group's words (a readable address if empty)
+  const uint32_t* nib;   // this lane's nibble words (stride 32 words)
+  uint32_t* ring;
+  uint32_t ring_addr;
+};
+
+// Start of a half-iteration: make sure the ring holds the next kAhead words,
+// then request up to kFetch more (landed by the end of the next half).
+__device__ __forceinline__ void half_begin(Chain& c, uint32_t li) {
+  while (c.fe < c.count && c.fe < c.rp + kAhead) {  // slow path: the stream outran the requests
+    const uint32_t w = c.fe + li;
+    const uint32_t v = c.wsrc[w < c.wlast ? w : c.wlast];
+    if (w < c.count) ring_put(c.ring, w, v);
+    c.fe = c.fe + 32 < c.count ? c.fe + 32 : c.count;
   }
+  c.q = c.q > c.fe ? c.q : c.fe;
+  const uint32_t room = c.rp + kRing - c.q;
+  const uint32_t want = c.count - c.q;
+  uint32_t n = want < room ? want : room;
+  n = n < kFetch ? n : kFetch;
+  const uint32_t w = c.q + li;
+  c.b_base = c.q;
+  c.b_n = n;
+  c.b_val = c.wsrc[w < c.wlast ? w : c.wlast];
+  c.q += n;
+  c.ab0 = c.ring_addr + 4u * (c.rp & (kRing - 1));
+}
+
+// End of a half-iteration: land the older request in the ring (its slots
+// hold words already consumed) and shift the newer one down.
+__device__ __forceinline__ void half_end(Chain& c, uint32_t li, uint32_t ab) {
+  c.rp += (ab - c.ab0) >> 2;
+  if (li < c.a_n) ring_put(c.ring, c.a_base + li, c.a_val);
+  const uint32_t landed = c.a_base + c.a_n;
+  c.fe = c.fe > landed ? c.fe : landed;
+  c.a_base = c.b_base;
+  c.a_n = c.b_n;
+  c.a_val = c.b_val;
+}
+
+// mask[lane] ? if1 : if0, as one v_cndmask. Written as an instruction so
+// that the compiler keeps the step branch-free instead of turning the
+// select back into a branch around the ring read.
+__device__ __forceinline__ uint32_t lane_select(unsigned long long mask, uint32_t if0, uint32_t if1) {
+  uint32_t r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if0), "v"(if1), "s"(mask));
+  return r;
+}
+
+// One symbol of one stream, without branches: every lane reads a ring word
+// at its refill address and keeps it only if it refills.
+__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& ab, uint32_t& out, int k,
+                                              uint32_t half_shift, const uint8_t* s_len, const uint8_t* s_sym) {
+  const bool refill = pos > 64u - kLimit;
+  const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
+  const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
+  const uint32_t c_lo = static_cast<uint32_t>(__popc(m_lo)), c_hi = static_cast<uint32_t>(__popc(m_hi));
+  // Refilling lanes below this one in its half: the wave-wide count, minus
+  // the lower half's refills for lanes of the upper half.
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u)) -
+                         __builtin_amdgcn_ubfe(c_lo << 16, half_shift, 16u);
+  const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(ab + 4u * below);
+  const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
+  const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
+  pos = lane_select(mask, pos, pos - 32u);
+  buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
+  ab += __builtin_amdgcn_ubfe((c_lo << 2) | (c_hi << 18), half_shift, 16u);
+  const uint32_t idx = static_cast<uint32_t>(buf >> (pos & 63u)) & (XP_LUT_BYTES - 1);
+  pos += s_len[idx];
+  out |= static_cast<uint32_t>(s_sym[idx]) << (8 * (k & 3));
 }
 
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   __shared__ uint8_t s_len[XP_LUT_BYTES];
   __shared__ uint8_t s_sym[XP_LUT_BYTES];
-  __shared__ uint32_t s_words[kGroupsPerBlock][kCapWords];
+  __shared__ uint32_t s_ring[kGroupsPerBlock][kRingPad];
 
   const int j = blockIdx.x / a.blocks_per_row;
   int r = blockIdx.x % a.blocks_per_row;
   const int name = r < a.names[0].blocks ? 0 : 1;
   if (name == 1) r -= a.names[0].blocks;
-  const NameDev& nm = a.names[name];
+  const NameDev nm = a.names[name];
 
   // Which expert, and whether it needs expanding (codec.py:263-277).
   const int64_t e = a.todo[j];
@@ -134,40 +190,138 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 
   const int wave = tid >> 6, lane = tid & 63;
   const bool upper = lane >= 32;
-  const int li = lane & 31;
-  const int gl = wave * 2 + (upper ? 1 : 0);  // group slot within the block
-  const int g = r * kGroupsPerBlock + gl;
-  const bool valid = g < nm.G;
-
+  const uint32_t li = lane & 31;
+  const uint32_t half_shift = upper ? 16u : 0u;
   const int G = nm.G;
+  const int msteps = a.chunk / 8;
   const uint32_t* rec = reinterpret_cast<const uint32_t*>(nm.stg + int64_t(j) * nm.pitch);
-  const int64_t nib_words = nm.N / 8;
-  const int64_t huff_off = (G + 1) + nib_words;                 // in words
-  const int64_t maxw = nm.pitch / 4 - huff_off;                 // Huffman words that fit in the record
-  int64_t gs = 0, ge = 0;
-  if (valid && maxw > 0) {
-    gs = rec[g];
-    ge = rec[g + 1];
-    gs = gs < 0 ? 0 : (gs > maxw ? maxw : gs);
-    ge = ge < gs ? gs : (ge > maxw ? maxw : ge);
-  }
-  const int64_t count = ge - gs;
-  const uint32_t* huff = rec + huff_off + gs;
+  const int64_t huff_off = (G + 1) + nm.N / 8;  // in words
+  const int64_t maxw = nm.pitch / 4 - huff_off;
 
-  // Stage the group's words in LDS when both groups of the wave fit.
-  const bool fits = !valid || count <= kCapWords;
-  const bool lds_mode = __ballot(!fits) == 0;
-  if (lds_mode && valid)
-    for (int64_t i = li; i < count; i += 32) s_words[gl][i] = huff[i];
+  Chain ch[kChains];
+  bool valid[kChains];
+  uint2* out[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) {
+    const int gl = wave * kGroupsPerWave + 2 * c + (upper ? 1 : 0);
+    int g = r * kGroupsPerBlock + gl;
+    valid[c] = g < G;
+    if (!valid[c]) g = G - 1;  // a spare stream repeats the last group and stores nothing
+    int64_t gs = 0, ge = 0;
+    if (maxw > 0) {
+      gs = rec[g];
+      ge = rec[g + 1];
+      gs = gs < 0 ? 0 : (gs > maxw ? maxw : gs);
+      ge = ge < gs ? gs : (ge > maxw ? maxw : ge);
+    }
+    Chain& h = ch[c];
+    h.count = static_cast<uint32_t>(ge - gs);
+    h.wsrc = h.count ? rec + huff_off + gs : rec;
+    h.wlast = h.count ? h.count - 1 : 0;
+    h.ring = s_ring[gl];
+    h.ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(h.ring));
+    h.nib = rec + (G + 1) + (int64_t(g) * msteps) * 32 + li;
+    h.buf = 0;
+    h.pos = 64u;  // nothing loaded: the first symbol refills every lane
+    h.rp = 0;
+    h.a_n = h.b_n = 0;
+    h.a_base = h.b_base = h.a_val = h.b_val = 0;
+    out[c] = reinterpret_cast<uint2*>(nm.dst + drow * nm.N + (int64_t(g) * 32 + li) * a.chunk);
+  }
+  // Initial fill of both rings: the first kRing words (8 loads per lane each).
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) {
+    Chain& h = ch[c];
+    const uint32_t fill = h.count < kRing ? h.count : kRing;
+    uint32_t v[kRing / 32];
+#pragma unroll
+    for (uint32_t i = 0; i < kRing / 32; ++i) {
+      const uint32_t w = li + 32 * i;
+      v[i] = h.wsrc[w < h.wlast ? w : h.wlast];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kRing / 32; ++i) {
+      const uint32_t w = li + 32 * i;
+      h.ring[w] = v[i];
+      if (w < kMirror) h.ring[w + kRing] = v[i];
+    }
+    h.fe = h.q = fill;
+    h.x_next = h.nib[0];
+  }
   __syncthreads();
 
-  const uint32_t* nib = rec + (G + 1) + (int64_t(g) * (a.chunk / 8)) * 32 + li;
-  uint2* out = reinterpret_cast<uint2*>(nm.dst + drow * nm.N + (int64_t(g) * 32 + li) * a.chunk);
-  const int msteps = a.chunk / 8;
-  if (lds_mode)
-    decode_lanes<true>(s_words[gl], count, nib, out, msteps, valid, upper, s_len, s_sym);
-  else
-    decode_lanes<false>(huff, count, nib, out, msteps, valid, upper, s_len, s_sym);
+  // Output: a lane's chunk is 512 contiguous bytes, produced 8 bytes per
+  // iteration. Four iterations (32 bytes, one aligned 32-byte piece) are
+  // gathered in registers and written as two 16-byte stores at the start of
+  // the next four, after that iteration's loads are issued; single 8-byte
+  // stores would each cost a partial-sector write. The registers are first
+  // rewritten at the end of that iteration, well after the stores issued.
+  uint4 ob[kChains][2];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) ob[c][0] = ob[c][1] = make_uint4(0, 0, 0, 0);
+  for (int m0 = 0; m0 < msteps; m0 += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int m = m0 + u;
+      uint2 o[kChains];
+#pragma unroll
+      for (int c = 0; c < kChains; ++c) {
+        const uint32_t x = ch[c].x_next;
+        ch[c].x_next = ch[c].nib[(m + 1 < msteps ? m + 1 : m) * 32];
+        o[c] = nibble_template(x);
+      }
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint32_t ab[kChains];
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) {
+          half_begin(ch[c], li);
+          ab[c] = ch[c].ab0;
+        }
+        if (u == 0 && half == 0 && m0 > 0) {
+#pragma unroll
+          for (int c = 0; c < kChains; ++c)
+            if (valid[c]) {
+              uint4* dst = reinterpret_cast<uint4*>(out[c] + (m0 - 4));
+              dst[0] = ob[c][0];
+              dst[1] = ob[c][1];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < static_cast<int>(kHalf); ++k) {
+#pragma unroll
+          for (int c = 0; c < kChains; ++c) {
+            if (half == 0)
+              decode_symbol(ch[c].buf, ch[c].pos, ab[c], o[c].x, k, half_shift, s_len, s_sym);
+            else
+              decode_symbol(ch[c].buf, ch[c].pos, ab[c], o[c].y, k, half_shift, s_len, s_sym);
+          }
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) half_end(ch[c], li, ab[c]);
+      }
+#pragma unroll
+      for (int c = 0; c < kChains; ++c) {
+        uint4& q = ob[c][u >> 1];
+        if (u & 1) {
+          q.z = o[c].x;
+          q.w = o[c].y;
+        } else {
+          q.x = o[c].x;
+          q.y = o[c].y;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+    if (valid[c] && msteps > 0) {
+      uint4* dst = reinterpret_cast<uint4*>(out[c] + (msteps - 4));
+      dst[0] = ob[c][0];
+      dst[1] = ob[c][1];
+    }
 }
 
 }  // namespace
@@ -182,7 +336,7 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
                    const int64_t* skip, int64_t chunk, void* stream) {
   XP_REQUIRE(K >= 0 && K <= (1 << 20), "xp_decode_rows: K=%lld", (long long)K);
   XP_REQUIRE(num_names >= 1 && num_names <= 2 && names, "xp_decode_rows: %d names (1 or 2)", num_names);
-  XP_REQUIRE(chunk >= 8 && chunk % 8 == 0 && chunk <= 4096, "xp_decode_rows: chunk=%lld (multiple of 8)",
+  XP_REQUIRE(chunk >= 32 && chunk % 32 == 0 && chunk <= 4096, "xp_decode_rows: chunk=%lld (multiple of 32)",
              (long long)chunk);
   XP_REQUIRE(num_experts >= 1, "xp_decode_rows: num_experts=%lld", (long long)num_experts);
   if (K == 0) return XP_OK;
@@ -208,7 +362,8 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
     XP_REQUIRE(s.pitch % 4 == 0 && s.pitch >= 4 * (G + 1) + s.row_bytes / 2,
                "xp_decode_rows: name %d pitch %lld cannot hold the record header", n, (long long)s.pitch);
     XP_REQUIRE(s.stg && s.dst, "xp_decode_rows: name %d has a null buffer", n);
-    XP_REQUIRE(aligned16(s.stg) && aligned16(s.dst), "xp_decode_rows: name %d buffers must be 16-byte aligned", n);
+    XP_REQUIRE(aligned16(s.stg) && aligned16(s.dst) && s.pitch % 16 == 0,
+               "xp_decode_rows: name %d buffers and pitch must be 16-byte aligned", n);
     a.names[n] = NameDev{static_cast<const uint8_t*>(s.stg),
                          s.pitch,
                          s.stg_rows,

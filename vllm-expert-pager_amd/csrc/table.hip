@@ -149,7 +149,7 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
   // different threads touch different elements.
   for (int r = tid; r < M; r += kThreads) {
     const int v = lds.order[r], e = lds.miss_e[r], old = lds.occ[v];
-    if (old >= 0) t.slot_of[old] = -1;
+    if (old >= 0 && old < E) t.slot_of[old] = -1;
     t.slot_of[e] = v;
     t.expert_in[v] = e;
   }
@@ -163,7 +163,7 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
     const int64_t mapped = n ? slot : -1;
     if (map64) map64[e] = mapped;
     if (map32) map32[e] = static_cast<int32_t>(mapped);
-    if (n) t.last_used[slot] = step;
+    if (n && slot >= 0 && slot < S) t.last_used[slot] = step;
     lds.fin[e] = static_cast<int16_t>(r >= 0 ? lds.order[r] : lds.cur[e]);
   }
   if (todo)
@@ -171,7 +171,7 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
   __syncthreads();
   for (int r = tid; r < M; r += kThreads) {
     const int old = lds.occ[lds.order[r]];
-    if (old >= 0) lds.fin[old] = -1;
+    if (old >= 0 && old < E) lds.fin[old] = -1;
   }
   if (slot_out && slot_final) {
     __syncthreads();
@@ -469,14 +469,12 @@ int xp_table_seed(const xp_table* ram, const xp_table* vram, const void* topk, i
   XP_REQUIRE(ram->num_experts == vram->num_experts, "xp_table_seed: expert counts differ");
   XP_REQUIRE(vram->num_slots <= ram->num_slots, "xp_table_seed: VRAM slots (%lld) exceed RAM slots (%lld)",
              (long long)vram->num_slots, (long long)ram->num_slots);
+  XP_REQUIRE(ram->num_slots <= ram->num_experts, "xp_table_seed: %lld RAM slots exceed %lld experts",
+             (long long)ram->num_slots, (long long)ram->num_experts);
   XP_REQUIRE(need != nullptr, "xp_table_seed: null need mask");
   const size_t smem = sizeof(SeedLds);
-  static bool attr_set = false;
-  if (!attr_set) {
-    XP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
-    attr_set = true;
-  }
+  XP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(seed_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(smem)));
   hipLaunchKernelGGL(seed_kernel, dim3(1), dim3(kThreads), smem, as_stream(stream), to_dev(ram), to_dev(vram),
                      GlobalIds{topk, topk_elem_bytes}, n, need);
   return check_launch("seed_kernel");

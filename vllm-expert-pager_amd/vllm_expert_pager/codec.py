@@ -105,6 +105,11 @@ def decode_rows(
     skip_t = None if skip is None else skip.to(torch.int64).contiguous()
     lut = lut.contiguous()
     n = len(dst)
+    E = dst_row.shape[0]
+    if lut.numel() < E * n * LUT_BYTES:
+        raise ValueError(f"lut has {lut.numel()} B, needs {E} x {n} x {LUT_BYTES}")
+    if skip_t is not None and skip_t.shape[0] < todo.shape[0]:
+        raise ValueError("skip must have at least as many entries as todo")
     names = (nat.XpDecodeName * n)()
     for i in range(n):
         s, d = staging[i], dst[i]

@@ -111,6 +111,11 @@ def gather_rows(
             raise ValueError("staging rows must have the RAM tier's pitch")
     elif tuple(P) != tuple(W):
         raise ValueError("uncompressed RAM rows must have the slab's row size")
+    for i in range(n):
+        if scale[i].shape[0] < E:
+            raise ValueError(f"scale[{i}] has {scale[i].shape[0]} rows, fewer than the {E} experts")
+        if scale_dst[i].shape[0] < dst[i].shape[0]:
+            raise ValueError(f"scale_dst[{i}] has fewer rows than dst[{i}]")
     names = (nat.XpGatherName * n)()
     for i in range(n):
         sp, srows, spitch = srcs[i]
