@@ -1,0 +1,192 @@
+"""CPU tests of the SSD request server (host C++ in libxp.so).
+
+The ring protocol is plain memory, so a Python thread plays the GPU: it
+writes a request slot, publishes its seq, and polls `done`. Covers in-order
+serving, the worker pool, read failures that still release the waiter, the
+re-publish and idle resend of `done`, gaps in seq counted as missed, and the
+test delay (the behaviours of store.py:83-308 and tests/test_store.py).
+"""
+
+import ctypes
+import os
+import time
+
+import numpy as np
+import pytest
+
+RING, BLOCK = 4, 64
+L, E, R, W = 2, 40, 8, 2
+PITCH = (4096, 8192)
+RECORD = sum(PITCH)
+
+
+def _lib():
+    from vllm_expert_pager import _native
+
+    return _native.lib()
+
+
+def aligned(nbytes, dtype=np.uint8):
+    raw = np.zeros(nbytes + 4096, np.uint8)
+    off = (-raw.ctypes.data) % 4096
+    return raw[off : off + nbytes].view(dtype)
+
+
+def pattern(layer, e, name):
+    return np.full(PITCH[name] // 4, layer * 1000 + e * 10 + name, np.int32)
+
+
+class Server:
+    def __init__(self, path, nworkers=7):
+        self.lib = _lib()
+        with open(path, "wb") as f:
+            for layer in range(L):
+                for e in range(E):
+                    f.write(pattern(layer, e, 0).tobytes() + pattern(layer, e, 1).tobytes())
+        self.fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+        self.rows = L * R + 2 * W
+        self.req = aligned(8 * (2 + RING * (2 + 2 * BLOCK)), np.int64)
+        self.done = aligned(4096, np.int64)[:1]
+        self.pinned = [aligned(self.rows * p).view(np.int32).reshape(self.rows, -1) for p in PITCH]
+        ptrs = (ctypes.c_void_p * 2)(*(a.ctypes.data for a in self.pinned))
+        pitch = (ctypes.c_long * 2)(*PITCH)
+        self.h = self.lib.ssd_start(self.fd, self.req.ctypes.data, self.done.ctypes.data, RING, BLOCK, L, E,
+                                    self.rows, RECORD, 2, ptrs, pitch, nworkers)
+        assert self.h
+        self.seq = 0
+
+    def publish(self, layer, experts, rows, seq=None):
+        seq = self.seq + 1 if seq is None else seq
+        self.seq = seq
+        slot = 2 + (seq % RING) * (2 + 2 * BLOCK)
+        self.req[slot + 2 : slot + 2 + BLOCK] = -1
+        self.req[slot + 2 + BLOCK : slot + 2 + 2 * BLOCK] = -1
+        self.req[slot + 2 : slot + 2 + len(experts)] = experts
+        self.req[slot + 2 + BLOCK : slot + 2 + BLOCK + len(rows)] = rows
+        self.req[slot + 1] = layer
+        self.req[slot] = seq  # published last (x86 stores are not reordered)
+        return seq
+
+    def wait(self, seq, timeout=10.0):
+        t0 = time.time()
+        while int(self.done[0]) < seq:
+            assert time.time() - t0 < timeout, f"done stuck at {int(self.done[0])} < {seq}"
+            time.sleep(0.001)
+
+    def stats(self):
+        f, r, m = ctypes.c_long(), ctypes.c_long(), ctypes.c_long()
+        io = ctypes.c_double()
+        self.lib.ssd_stats(self.h, ctypes.byref(f), ctypes.byref(r), ctypes.byref(io), ctypes.byref(m))
+        return f.value, r.value, io.value, m.value
+
+    def error(self):
+        e = self.lib.ssd_error(self.h)
+        return None if e is None else e.decode()
+
+    def close(self):
+        if self.h:
+            self.lib.ssd_stop(self.h)
+            self.h = None
+            os.close(self.fd)
+
+
+@pytest.fixture
+def server(tmp_path):
+    s = Server(str(tmp_path / "paging.bin"))
+    yield s
+    s.close()
+
+
+def test_serves_requests_in_order(server):
+    for i in range(12):
+        layer = i % L
+        experts = [(3 * i) % E, (3 * i + 1) % E]
+        rows = [layer * R + (i % R), layer * R + ((i + 1) % R)]
+        seq = server.publish(layer, experts, rows)
+        server.wait(seq)
+        for e, row in zip(experts, rows):
+            for n in range(2):
+                np.testing.assert_array_equal(server.pinned[n][row], pattern(layer, e, n))
+    f, r, io, missed = server.stats()
+    assert (f, r, missed) == (12, 24, 0) and io > 0
+    assert server.error() is None
+
+
+def test_many_jobs_in_one_request(server):
+    """More reads than threads in one request; done is written once all are in."""
+    seq = server.publish(1, list(range(20, 36)), list(range(16)))
+    server.wait(seq)
+    for k in range(16):
+        for n in range(2):
+            np.testing.assert_array_equal(server.pinned[n][k], pattern(1, 20 + k, n))
+    assert server.stats()[:2] == (1, 16)
+
+
+def test_read_failure_still_releases(server):
+    seq = server.publish(1, [4, 5], [10**6, 0])
+    server.wait(seq)
+    assert "outside the RAM tier" in server.error()
+    np.testing.assert_array_equal(server.pinned[0][0], pattern(1, 5, 0))
+    seq = server.publish(1, [E + 3], [0])
+    server.wait(seq)
+    assert "outside the RAM tier" in server.error()  # the first failure is kept
+
+
+def test_expert_out_of_range(tmp_path):
+    s = Server(str(tmp_path / "p.bin"))
+    try:
+        s.wait(s.publish(5, [1], [0]))
+        assert "out of range" in s.error()
+    finally:
+        s.close()
+
+
+def test_gap_in_seq_counts_missed(server):
+    server.wait(server.publish(0, [1], [0]))
+    # seqs 2..5 were given up by the GPU before the host saw them; seq 6
+    # lands in the slot the host watches (6 % RING == 2 % RING).
+    server.wait(server.publish(0, [2], [1], seq=6))
+    assert server.stats()[3] == 4
+    np.testing.assert_array_equal(server.pinned[0][1], pattern(0, 2, 0))
+
+
+def test_done_is_resent_when_the_republish_count_moves(server):
+    seq = server.publish(0, [3], [0])
+    server.wait(seq)
+    server.done[0] = 0
+    server.req[0] += 1
+    server.wait(seq, timeout=2.0)
+
+
+def test_done_is_resent_after_idling(server):
+    seq = server.publish(0, [3], [0])
+    server.wait(seq)
+    server.done[0] = 0
+    server.wait(seq, timeout=5.0)
+
+
+def test_test_delay_holds_requests(server):
+    server.lib.ssd_test_delay(server.h, 0.3)
+    t0 = time.time()
+    server.wait(server.publish(0, [3], [0]))
+    assert time.time() - t0 >= 0.29
+    server.lib.ssd_test_delay(server.h, 0.0)
+
+
+def test_stop_while_delaying(tmp_path):
+    s = Server(str(tmp_path / "p.bin"))
+    s.lib.ssd_test_delay(s.h, 60.0)
+    s.publish(0, [1], [0])
+    time.sleep(0.05)
+    t0 = time.time()
+    s.close()
+    assert time.time() - t0 < 5.0
+
+
+def test_start_rejects_bad_arguments(tmp_path):
+    lib = _lib()
+    req = aligned(8 * 64, np.int64)
+    done = aligned(4096, np.int64)
+    ptrs = (ctypes.c_void_p * 5)()
+    pitch = (ctypes.c_long * 5)()
+    assert not lib.ssd_start(0, req.ctypes.data, done.ctypes.data, RING, BLOCK, 1, 1, 1, 4096, 5, ptrs, pitch, 1)

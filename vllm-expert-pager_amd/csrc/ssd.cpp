@@ -17,6 +17,12 @@
 //
 // Exported with the reference's C ABI (store.py:253-308) so the Python side
 // binds it the same way.
+//
+// Reads go straight into the pinned rows when the kernel accepts them as an
+// O_DIRECT target. Memory from the GPU driver's pinned allocator may not be
+// (preadv fails with EFAULT); then every thread reads into its own aligned
+// bounce buffer with O_DIRECT and copies the record into the rows, which
+// still keeps the page cache from holding a second copy.
 #include <sched.h>
 #include <sys/uio.h>
 #include <unistd.h>
@@ -29,6 +35,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <thread>
@@ -68,6 +76,7 @@ struct ssd_t {
   std::atomic<bool> failing{false};
   char err[512] = {0};
   std::atomic<long long> delay_ns{0};
+  std::atomic<bool> direct{true};  // preadv straight into the pinned rows works
 
   // Job board of the request being served.
   std::mutex mu;
@@ -81,6 +90,7 @@ struct ssd_t {
   std::thread server;
 
   void fail(const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+  long read_iov(const iovec* iov, int n, off_t off, int* err);
   void read_job(long layer_, long e, long row);
   void drain_jobs();
   void worker_loop();
@@ -97,29 +107,17 @@ void ssd_t::fail(const char* fmt, ...) {
   failed.store(1, std::memory_order_release);
 }
 
-void ssd_t::read_job(long layer_, long e, long row) {
-  if (layer_ < 0 || layer_ >= L || e < 0 || e >= E) {
-    fail("expert %ld of layer %ld is out of range", e, layer_);
-    return;
-  }
-  if (row < 0 || row >= rows) {
-    fail("row %ld for expert %ld of layer %ld is outside the RAM tier of %ld rows", row, e, layer_, rows);
-    return;
-  }
-  iovec iov[kMaxNames];
-  for (int i = 0; i < names; ++i) {
-    iov[i].iov_base = pinned[i] + row * pitch[i];
-    iov[i].iov_len = static_cast<size_t>(pitch[i]);
-  }
-  const off_t off = static_cast<off_t>(layer_ * E + e) * record_bytes;
-  long got = 0;
-  // O_DIRECT preadv may return short on signals; continue until the record
-  // is complete or an error/EOF shows up.
-  while (got < record_bytes) {
+// preadv until the iovecs are full, EOF or an error; returns the bytes read
+// and the errno of a failure in *err.
+long ssd_t::read_iov(const iovec* iov, int n, off_t off, int* err) {
+  long got = 0, total = 0;
+  for (int i = 0; i < n; ++i) total += static_cast<long>(iov[i].iov_len);
+  *err = 0;
+  while (got < total) {
     iovec part[kMaxNames];
     int np = 0;
     long skip = got;
-    for (int i = 0; i < names; ++i) {
+    for (int i = 0; i < n; ++i) {
       if (skip >= static_cast<long>(iov[i].iov_len)) {
         skip -= static_cast<long>(iov[i].iov_len);
         continue;
@@ -129,16 +127,84 @@ void ssd_t::read_job(long layer_, long e, long row) {
       skip = 0;
       ++np;
     }
-    const ssize_t n = preadv(fd, part, np, off + got);
-    if (n < 0) {
+    const ssize_t r = preadv(fd, part, np, off + got);
+    if (r < 0) {
       if (errno == EINTR) continue;
-      fail("preadv of expert %ld of layer %ld failed: %s", e, layer_, strerror(errno));
+      *err = errno;
+      return got;
+    }
+    if (r == 0) break;
+    got += r;
+  }
+  return got;
+}
+
+namespace {
+struct Bounce {
+  void* p = nullptr;
+  size_t n = 0;
+  ~Bounce() { std::free(p); }
+  uint8_t* get(size_t bytes) {
+    if (n < bytes) {
+      std::free(p);
+      p = nullptr;
+      n = 0;
+      if (posix_memalign(&p, 4096, bytes) != 0) return nullptr;
+      n = bytes;
+    }
+    return static_cast<uint8_t*>(p);
+  }
+};
+thread_local Bounce t_bounce;
+}  // namespace
+
+void ssd_t::read_job(long layer_, long e, long row) {
+  if (layer_ < 0 || layer_ >= L || e < 0 || e >= E) {
+    fail("expert %ld of layer %ld is out of range", e, layer_);
+    return;
+  }
+  if (row < 0 || row >= rows) {
+    fail("row %ld for expert %ld of layer %ld is outside the RAM tier of %ld rows", row, e, layer_, rows);
+    return;
+  }
+  const off_t off = static_cast<off_t>(layer_ * E + e) * record_bytes;
+  int err = 0;
+  long got;
+  if (direct.load(std::memory_order_relaxed)) {
+    iovec iov[kMaxNames];
+    for (int i = 0; i < names; ++i) {
+      iov[i].iov_base = pinned[i] + row * pitch[i];
+      iov[i].iov_len = static_cast<size_t>(pitch[i]);
+    }
+    got = read_iov(iov, names, off, &err);
+    if (err != EFAULT) {
+      if (err) fail("preadv of expert %ld of layer %ld failed: %s", e, layer_, strerror(err));
+      else if (got != record_bytes)
+        fail("short read: %ld of %ld B for expert %ld of layer %ld", got, record_bytes, e, layer_);
       return;
     }
-    if (n == 0) break;
-    got += n;
+    direct.store(false, std::memory_order_relaxed);  // the rows cannot be an O_DIRECT target
   }
-  if (got != record_bytes) fail("short read: %ld of %ld B for expert %ld of layer %ld", got, record_bytes, e, layer_);
+  uint8_t* b = t_bounce.get(static_cast<size_t>(record_bytes));
+  if (!b) {
+    fail("cannot allocate a %ld B read buffer", record_bytes);
+    return;
+  }
+  iovec one{b, static_cast<size_t>(record_bytes)};
+  got = read_iov(&one, 1, off, &err);
+  if (err) {
+    fail("preadv of expert %ld of layer %ld failed: %s", e, layer_, strerror(err));
+    return;
+  }
+  if (got != record_bytes) {
+    fail("short read: %ld of %ld B for expert %ld of layer %ld", got, record_bytes, e, layer_);
+    return;
+  }
+  long pos = 0;
+  for (int i = 0; i < names; ++i) {
+    std::memcpy(pinned[i] + row * pitch[i], b + pos, static_cast<size_t>(pitch[i]));
+    pos += pitch[i];
+  }
 }
 
 // Take jobs of the current request until none is left (server and workers).
