@@ -263,44 +263,59 @@ void ssd_test_delay(ssd_t* s, double seconds);
 
 /* ---- MoE expert compute on the slab (prefill overflow and decode) ----
  * These replace the vLLM fused fp8 MoE the reference hands expert_map to
- * (super().forward_modular, experts.py:579-604) and its moe_sum intercept
- * (experts.py:546-556). Weights are fp8 e4m3 (OCP) with 128x128 fp32 block
- * scales; activations are quantised per token and 128-column group.
- *   w13 slab: [slots][2I][H] fp8, scale [slots][2I/128][H/128] fp32
- *   w2  slab: [slots][H][I]  fp8, scale [slots][H/128][I/128]  fp32
+ * (super().forward_modular in _expert_pager_run, experts.py:579-604) and its
+ * moe_sum intercept (collect, experts.py:538-556). Weights are fp8 e4m3 (OCP)
+ * with 128x128 fp32 block scales; activations are quantised per token and
+ * 128-column group.
+ *   w13 slab: [slots][2I][H] fp8 (gate rows, then up rows),
+ *             scale [slots][2I/128][H/128] fp32
+ *   w2  slab: [slots][H][I] fp8, scale [slots][H/128][I/128] fp32
+ * A pair is p = t*topk + k. Each listed pair's contribution is computed from
+ * its own token and expert alone, so splitting the experts over several
+ * expert_maps (chunks) writes the same bits as one call over all of them.
  */
 
-/* Quantise x[T][H] (bf16) to fp8 xq[T][H] and scales xs[T][H/128] (fp32).
- * H multiple of 128. */
+/* Quantise x[T][H] (bf16) to fp8 xq[T][H] and scales xs[T][H/128] (fp32):
+ * s = max(amax, 1e-10) / 448, q = rne(clamp(x / s, -448, 448)).
+ * H is a multiple of 128; x and xq 16-byte aligned. */
 int xp_quant_tokens(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq,
                     float* xs, void* stream);
 
-/* Route (token, k) pairs to slab slots: for every pair whose expert e has
- * expert_map[e] >= 0 (ids < 0 or >= E are skipped), list the pair under that
- * slot. Writes counts[slots] and pairs[slots][cap] (pair = t*topk + k, in
- * ascending pair order). cap = max pairs per slot kept (T*topk covers all).
- * Returns XP_E_LIMIT via the device flag overflow[0] != 0 if a slot had more
- * than cap pairs. */
+/* Upper bound on the tiles route can produce for `npairs` pairs over
+ * `slots` slots; size `tiles` as 1 + 2 * bound ints. */
+int64_t xp_moe_max_tiles(int64_t npairs, int64_t slots);
+
+/* List the pairs whose expert e (0 <= e < num_experts) has
+ * 0 <= expert_map[e] < slots under that slot, in CSR form:
+ * offsets[slots + 1], pairs[offsets[s] .. offsets[s+1]) (any order within a
+ * slot; pairs holds up to T*topk entries), and tiles[0] = tile count followed
+ * by (slot, first position) per tile of at most 64 pairs. slots <= 1024. */
 int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T,
                  int64_t topk, const int32_t* expert_map, int64_t num_experts,
-                 int64_t slots, int64_t cap, int32_t* counts, int32_t* pairs,
-                 int32_t* overflow, void* stream);
+                 int64_t slots, int32_t* offsets, int32_t* pairs,
+                 int32_t* tiles, void* stream);
 
-/* Expert FFN for every listed pair: out[pair][H] (bf16) =
- * topk_weight[pair] * (w2 . q(silu(gate) * up)), gate/up from w13 . xq.
- * act/acts are workspaces [T*topk][I] fp8 and [T*topk][I/128] fp32.
- * Pairs that are not listed are not written. */
+/* Expert FFN of every routed pair, on the slab slot route chose:
+ *   h = w13 . xq (block-scaled, fp32), gate = bf16(h[:I]), up = bf16(h[I:])
+ *   a = bf16(silu(gate) * up), quantised like xp_quant_tokens into
+ *       act[pair][I] fp8 / acts[pair][I/128] fp32 (workspaces)
+ *   out[pair][H] = bf16(topk_weight[pair] * (w2 . a)) (bf16 bits)
+ * topk_weight is fp32 [T*topk]. Pairs that were not routed are not written.
+ * H and I are multiples of 128; fp8 buffers and out 16-byte aligned. */
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T,
                    int64_t topk, const float* topk_weight, int64_t H,
                    int64_t I, const uint8_t* w13, const float* w13_scale,
                    const uint8_t* w2, const float* w2_scale, int64_t slots,
-                   int64_t cap, const int32_t* counts, const int32_t* pairs,
-                   uint8_t* act, float* acts, uint16_t* out, void* stream);
+                   const int32_t* offsets, const int32_t* pairs,
+                   const int32_t* tiles, uint8_t* act, float* acts,
+                   uint16_t* out, void* stream);
 
-/* out[t][H] = bf16(sum_k fp32(contrib[t*topk + k][H])), summed in k order.
- * The single top-k combine (experts.py:479-487). */
+/* The single top-k combine (moe_sum after collect, experts.py:546-552):
+ * out[t][H] = bf16(sum over k ascending of fp32(contrib[t*topk + k])),
+ * skipping pairs whose id is outside [0, num_experts). */
 int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk,
-                    int64_t H, uint16_t* out, void* stream);
+                    int64_t H, const void* topk_ids, int topk_elem_bytes,
+                    int64_t num_experts, uint16_t* out, void* stream);
 
 #ifdef __cplusplus
 }

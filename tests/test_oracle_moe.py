@@ -1,0 +1,128 @@
+"""Pins of the MoE oracle (oracle/moe_ref.py) on the CPU.
+
+vLLM's fused fp8 MoE is not part of the reference tree and no reference
+test exercises it, so the oracle is pinned by what the format and the
+mathematics fix: the e4m3fn code table, round-to-nearest-even, closed forms
+of the quantisation and of a one-hot token, invariances, exact sums.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as M
+
+
+def test_fp8_table_matches_torch():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).float().numpy().astype(np.float64)
+    ours = M.fp8_values()
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ours[ok], ref[ok])
+    assert ours[0x7E] == 448.0 and ours[0x01] == 2.0**-9 and ours[0x08] == 2.0**-6
+
+
+@pytest.mark.parametrize(
+    "value, code",
+    [
+        (1.0625, 0x38),  # tie between 1.0 (even) and 1.125 -> 1.0
+        (1.1875, 0x3A),  # tie between 1.125 and 1.25 (even) -> 1.25
+        (448.0, 0x7E),
+        (-448.0, 0xFE),
+        (2.0**-9, 0x01),
+        (2.0**-10, 0x00),  # half the smallest subnormal: tie to even 0
+        (3 * 2.0**-10, 0x02),  # tie between 1 and 2 subnormal units -> 2
+        (0.0, 0x00),
+    ],
+)
+def test_to_fp8_rounding(value, code):
+    assert int(M.to_fp8(np.array([value], np.float32))[0]) == code
+
+
+def test_quant_groups_closed_form():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((3, 256)).astype(np.float32)
+    x[1, :128] = 0.0
+    q, s = M.quant_groups(x)
+    assert s.shape == (3, 2)
+    vals = M.fp8_values()[q]
+    for t in range(3):
+        for g in range(2):
+            blk = x[t, 128 * g : 128 * (g + 1)]
+            amax = np.float32(np.abs(blk).max())
+            if amax == 0:
+                assert s[t, g] == np.float32(1e-10) / np.float32(448) and not q[t, 128 * g : 128 * (g + 1)].any()
+                continue
+            assert s[t, g] == amax / np.float32(448)
+            i = int(np.abs(blk).argmax())
+            assert abs(vals[t, 128 * g + i]) == 448.0
+            # every value is within half an fp8 step of x / s
+            err = np.abs(vals[t, 128 * g : 128 * (g + 1)] - blk / s[t, g])
+            assert (err <= np.maximum(np.abs(blk / s[t, g]) / 16, 2.0**-10) + 1e-6).all()
+
+
+def _experts(E=3, H=256, I=128, seed=1):
+    return M.random_experts(np.random.default_rng(seed), E, H, I)
+
+
+def test_expert_ffn_one_hot_closed_form():
+    """x = c * e_i makes h column i of w13; w2 = a permutation picks activation entries."""
+    E, H, I, c, i = 2, 256, 128, 1.5, 37
+    w13, w13s, _, _ = _experts(E, H, I)
+    # w2[e][h][n] = 1.0 at n = (h + 5e) % I, scale 1
+    w2 = np.zeros((E, H, I), np.uint8)
+    for e in range(E):
+        w2[e, np.arange(H), (np.arange(H) + 5 * e) % I] = 0x38
+    w2s = np.ones((E, H // 128, I // 128), np.float32)
+    x = np.zeros((2, H), np.float32)
+    x[:, i] = c
+    ids = np.array([[0], [1]])
+    tw = np.array([[0.5], [2.0]], np.float32)
+    got = M.expert_ffn(x, tw, ids, w13, w13s, w2, w2s)
+    v = M.fp8_values()
+    for t, e in enumerate((0, 1)):
+        col = v[w13[e][:, i]] * np.repeat(w13s[e][:, i // 128], 128)  # dequantised column i
+        h = (c * col).astype(np.float32)
+        gate, up = M.bf16(h[:I]), M.bf16(h[I:])
+        with np.errstate(over="ignore"):
+            a = M.bf16((gate / (np.float32(1) + np.exp(-gate))).astype(np.float32) * up)
+        aq, as_ = M.quant_groups(a[None, :])
+        ad = v[aq[0]] * np.repeat(as_[0].astype(np.float64), 128)
+        y = ad[(np.arange(H) + 5 * e) % I].astype(np.float32)
+        assert np.array_equal(got[t], M.bf16(y * tw[t, 0]))
+
+
+def test_expert_ffn_invariances():
+    rng = np.random.default_rng(2)
+    E, H, I, T, K = 4, 256, 128, 5, 2
+    w13, w13s, w2, w2s = _experts(E, H, I, seed=3)
+    x = M.bf16(rng.standard_normal((T, H)).astype(np.float32))
+    ids = np.stack([rng.permutation(E)[:K] for _ in range(T)])
+    tw = rng.random((T, K)).astype(np.float32)
+    base = M.fused_moe_ref(x, tw, ids, w13, w13s, w2, w2s)
+    # relabel the experts
+    perm = rng.permutation(E)
+    inv = np.argsort(perm)
+    relabelled = M.fused_moe_ref(x, tw, perm[ids], w13[inv], w13s[inv], w2[inv], w2s[inv])
+    assert np.array_equal(base, relabelled)
+    # routed weights times a power of two scale the output exactly
+    assert np.array_equal(M.fused_moe_ref(x, 4 * tw, ids, w13, w13s, w2, w2s), 4 * base)
+    # a token's output does not depend on the other tokens
+    sub = M.fused_moe_ref(x[2:4], tw[2:4], ids[2:4], w13, w13s, w2, w2s)
+    assert np.array_equal(sub, base[2:4])
+    # an id outside [0, E) contributes nothing
+    ids2 = ids.copy()
+    ids2[0, 1] = -1
+    c = M.expert_ffn(x, tw, ids2, w13, w13s, w2, w2s)
+    assert not c[1].any()
+
+
+def test_topk_sum_exact_and_skips_invalid():
+    T, K, H = 3, 4, 8
+    c = np.arange(T * K * H, dtype=np.float32).reshape(T * K, H) % 7 - 3
+    ids = np.array([[0, 1, 2, 3], [1, -1, 2, 9], [3, 3, 0, 1]])
+    got = M.topk_sum(c, ids, 4)
+    cc = c.reshape(T, K, H)
+    ok = ((ids >= 0) & (ids < 4))[:, :, None]
+    assert np.array_equal(got, (cc * ok).sum(axis=1))

@@ -1,0 +1,565 @@
+// Expert FFN on the slab for the prefill overflow path (and decode):
+// fp8 e4m3 weights with 128x128 fp32 block scales, activations quantised to
+// fp8 per token and 128-column group, MFMA fp8 grouped GEMMs, fused SiLU*up,
+// and the single top-k combine.
+//
+// The reference hands expert_map to vLLM's fused fp8 MoE and intercepts its
+// moe_sum so the top-k sum runs once over all chunks (experts.py:455-604).
+// Here every (token, k) pair's expert output is computed independently of
+// the other rows of its tile (an MFMA output element depends only on its own
+// A row and B column), written once into a persistent buffer, and summed in
+// k order in fp32 with one bf16 rounding at the end -- so a chunked run and
+// a one-shot run give the same bits.
+//
+// Numerics of one pair follow the rounding sequence of a w8a8 block-fp8 MoE:
+// x -> fp8 per 128-group (scale = max(amax, 1e-10) / 448, q = clamp(x / s));
+// h = sum over K blocks of (xq . wq) * sx * sw in fp32; gate, up -> bf16;
+// a = bf16(silu(gate) * up); a -> fp8 per 128-group; y likewise with w2;
+// contribution = bf16(y * routed weight).
+//
+// Work decomposition: route lists the pairs of each slab slot in CSR form
+// and cuts them into tiles of 64 pairs of one slot; a GEMM workgroup takes
+// one tile and 128 output columns. Launch grids are sized from the shapes
+// alone (a bound on the tile count), so the sequence is graph-capturable;
+// workgroups past the live tile count exit at once.
+#include <hip/hip_bf16.h>
+
+#include "common.h"
+
+namespace xp {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBM = 64;          // pairs per tile
+constexpr int kBN = 128;         // output columns per workgroup (one quant group for GEMM1)
+constexpr int kKB = 128;         // K block = scale block = one MFMA K
+constexpr int kThreads = 256;    // 4 waves, split along N (32 columns each)
+constexpr int kRowPitch = 144;   // LDS bytes per staged A row (128 + 16 against bank conflicts)
+constexpr int kRouteThreads = 1024;
+constexpr int kMaxRouteSlots = 1024;
+constexpr float kFp8Max = 448.0f;
+constexpr float kEps = 1e-10f;
+
+__device__ __forceinline__ float bf16_round(float v) { return __bfloat162float(__float2bfloat16(v)); }
+
+__device__ __forceinline__ uint32_t bf16_bits(float v) {
+  __hip_bfloat16 b = __float2bfloat16(v);
+  return static_cast<uint32_t>(*reinterpret_cast<uint16_t*>(&b));
+}
+
+__device__ __forceinline__ float bf16_value(uint32_t u16) { return __uint_as_float(u16 << 16); }
+
+// fp32 -> fp8 e4m3 (OCP), round to nearest even; callers clamp to +-448.
+__device__ __forceinline__ uint32_t to_fp8(float v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(v, v, 0, false)) & 0xffu;
+}
+
+__device__ __forceinline__ float quant_scale(float amax) { return fmaxf(amax, kEps) / kFp8Max; }
+
+__device__ __forceinline__ float clamp_fp8(float v) { return fminf(fmaxf(v, -kFp8Max), kFp8Max); }
+
+// 16x16 output tile = A[16][128] . B[128][16] in fp8 e4m3. Lane l = 16q + j
+// supplies 32 bytes of A row j and of B column j at K offset 32q; the
+// instruction maps the bytes of A and B to K in the same way, so the dot
+// products are those of the plain layout. Lane l receives C[4q + r][j].
+// Zero scale operands select the unscaled instruction.
+__device__ __forceinline__ f32x4 mfma_k128(const u32x4 (&a)[2], const u32x4 (&b)[2]) {
+  const i32x8 av = {static_cast<int>(a[0].x), static_cast<int>(a[0].y), static_cast<int>(a[0].z),
+                    static_cast<int>(a[0].w), static_cast<int>(a[1].x), static_cast<int>(a[1].y),
+                    static_cast<int>(a[1].z), static_cast<int>(a[1].w)};
+  const i32x8 bv = {static_cast<int>(b[0].x), static_cast<int>(b[0].y), static_cast<int>(b[0].z),
+                    static_cast<int>(b[0].w), static_cast<int>(b[1].x), static_cast<int>(b[1].y),
+                    static_cast<int>(b[1].z), static_cast<int>(b[1].w)};
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, zero, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ void load32(const uint8_t* p, u32x4 (&v)[2]) {
+  v[0] = *reinterpret_cast<const u32x4*>(p);
+  v[1] = *reinterpret_cast<const u32x4*>(p + 16);
+}
+
+// ---- token quantisation: one workgroup per token, 16 lanes per group ----
+__global__ void __launch_bounds__(256) quant_tokens_kernel(const uint16_t* __restrict__ x, int64_t H,
+                                                           uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const int64_t t = blockIdx.x;
+  const uint16_t* row = x + t * H;
+  for (int64_t c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(row + c0);
+    float v[8];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_value(raw[i] & 0xffffu);
+      v[2 * i + 1] = bf16_value(raw[i] >> 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+    const float s = quant_scale(amax);
+    uint32_t q0 = 0, q1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q0 |= to_fp8(clamp_fp8(v[i] / s)) << (8 * i);
+      q1 |= to_fp8(clamp_fp8(v[4 + i] / s)) << (8 * i);
+    }
+    *reinterpret_cast<uint2*>(xq + t * H + c0) = make_uint2(q0, q1);
+    if ((threadIdx.x & 15) == 0) xs[t * (H / kKB) + c0 / kKB] = s;
+  }
+}
+
+// Exclusive scan of two counters over a 1024-thread workgroup.
+__device__ __forceinline__ int2 block_scan2(int a, int b, int2* s_tot, int2* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int ia = a, ib = b;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int ya = __shfl_up(ia, off, 64), yb = __shfl_up(ib, off, 64);
+    if (lane >= off) {
+      ia += ya;
+      ib += yb;
+    }
+  }
+  if (lane == 63) s_tot[wave] = make_int2(ia, ib);
+  __syncthreads();
+  int2 base = make_int2(0, 0), all = make_int2(0, 0);
+  for (int w = 0; w < kRouteThreads / 64; ++w) {
+    const int2 v = s_tot[w];
+    if (w < wave) {
+      base.x += v.x;
+      base.y += v.y;
+    }
+    all.x += v.x;
+    all.y += v.y;
+  }
+  *total = all;
+  return make_int2(base.x + ia - a, base.y + ib - b);
+}
+
+// ---- routing: CSR lists of the pairs of each slab slot, and the tiles ----
+// offsets[slots + 1]; pairs[offsets[s] .. offsets[s+1]) = pair ids t*topk + k
+// of slot s (in no particular order); tiles[0] = live tile count, then
+// (slot, first pair position) per tile.
+__global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, int eb, int64_t npairs,
+                                                              const int32_t* __restrict__ expert_map, int E,
+                                                              int slots, int32_t* __restrict__ offsets,
+                                                              int32_t* __restrict__ pairs,
+                                                              int32_t* __restrict__ tiles) {
+  __shared__ int s_cnt[kMaxRouteSlots];
+  __shared__ int2 s_tot[kRouteThreads / 64];
+  const int tid = threadIdx.x;
+  if (tid < slots) s_cnt[tid] = 0;
+  __syncthreads();
+  for (int64_t p = tid; p < npairs; p += kRouteThreads) {
+    const int64_t e = load_id(ids, eb, p);
+    const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
+    if (s >= 0 && s < slots) atomicAdd(&s_cnt[s], 1);
+  }
+  __syncthreads();
+  const int c = tid < slots ? s_cnt[tid] : 0;
+  const int nt = (c + kBM - 1) / kBM;
+  int2 total;
+  const int2 off = block_scan2(c, nt, s_tot, &total);
+  if (tid < slots) {
+    offsets[tid] = off.x;
+    s_cnt[tid] = off.x;  // becomes the scatter cursor
+    for (int i = 0; i < nt; ++i) {
+      tiles[1 + 2 * (off.y + i)] = tid;
+      tiles[2 + 2 * (off.y + i)] = off.x + i * kBM;
+    }
+  }
+  if (tid == 0) {
+    offsets[slots] = total.x;
+    tiles[0] = total.y;
+  }
+  __syncthreads();
+  for (int64_t p = tid; p < npairs; p += kRouteThreads) {
+    const int64_t e = load_id(ids, eb, p);
+    const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
+    if (s >= 0 && s < slots) pairs[atomicAdd(&s_cnt[s], 1)] = static_cast<int32_t>(p);
+  }
+}
+
+struct Tile {
+  int slot, first, count;
+};
+
+__device__ __forceinline__ bool load_tile(const int32_t* tiles, const int32_t* offsets, Tile& t) {
+  const int i = blockIdx.y;
+  if (i >= tiles[0]) return false;
+  t.slot = tiles[1 + 2 * i];
+  t.first = tiles[2 + 2 * i];
+  const int end = offsets[t.slot + 1];
+  t.count = end - t.first < kBM ? end - t.first : kBM;
+  return true;
+}
+
+// Stage K block kb of the tile's A rows into LDS ([kBM][kRowPitch] bytes)
+// and their scales: 4 threads x 32 bytes per row.
+__device__ __forceinline__ void stage_a(const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t lda,
+                                        int kblocks, const int* s_row, int kb, uint8_t* s_a, float* s_sa) {
+  const int r = threadIdx.x >> 2, part = threadIdx.x & 3;
+  const int64_t row = s_row[r];
+  u32x4 v[2];
+  load32(A + row * lda + kb * kKB + part * 32, v);
+  u32x4* dst = reinterpret_cast<u32x4*>(s_a + r * kRowPitch + part * 32);
+  dst[0] = v[0];
+  dst[1] = v[1];
+  if (part == 0) s_sa[r] = As[row * kblocks + kb];
+}
+
+__device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4 (&a)[2]) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(s_a + row * kRowPitch + 32 * q);
+  a[0] = p[0];
+  a[1] = p[1];
+}
+
+// Tile rows: the pair of each row (-1 for padding) and the A row it reads
+// (padding rows repeat the tile's first pair, so every load stays inside
+// the operand).
+__device__ __forceinline__ void tile_rows(const Tile& tile, const int32_t* pairs, int div, int* s_pair, int* s_row) {
+  const int tid = threadIdx.x;
+  if (tid < kBM) {
+    const int p = pairs[tile.first + (tid < tile.count ? tid : 0)];
+    s_pair[tid] = tid < tile.count ? p : -1;
+    s_row[tid] = p / div;
+  }
+}
+
+// GEMM1: gate/up for 128 activation columns, SiLU*up, per-pair fp8
+// quantisation of the activation. grid = (I / 128, tile bound).
+__global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                         int64_t H, int64_t I, int topk,
+                                                         const uint8_t* __restrict__ w13,
+                                                         const float* __restrict__ w13_scale,
+                                                         const int32_t* __restrict__ offsets,
+                                                         const int32_t* __restrict__ pairs,
+                                                         const int32_t* __restrict__ tiles,
+                                                         uint8_t* __restrict__ act, float* __restrict__ acts) {
+  __shared__ int s_row[kBM];
+  __shared__ int s_pair[kBM];
+  __shared__ float s_sa[kBM];
+  __shared__ float s_amax[4][kBM];
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[kBM * kRowPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t s_q[kBM * kBN];
+
+  Tile tile;
+  if (!load_tile(tiles, offsets, tile)) return;
+  const int n0 = blockIdx.x * kBN;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const int KB = static_cast<int>(H / kKB);
+
+  tile_rows(tile, pairs, topk, s_pair, s_row);
+  __syncthreads();
+
+  // B rows of this lane: gate rows n0 + 32*wave + 16t + j and the up rows I below them.
+  const uint8_t* wrow[4];
+  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t n = n0 + 32 * wave + 16 * t + j;
+    wrow[t] = wslot + n * H + 32 * q;
+    wrow[2 + t] = wslot + (I + n) * H + 32 * q;
+  }
+  const float* sw_gate = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + n0 / kKB) * KB;
+  const float* sw_up = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + n0) / kKB) * KB;
+
+  f32x4 acc[4][4];  // [row subtile][gate t0, gate t1, up t0, up t1]
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int si = 0; si < 4; ++si) acc[mi][si] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 bnext[4][2];
+#pragma unroll
+  for (int si = 0; si < 4; ++si) load32(wrow[si], bnext[si]);
+  for (int kb = 0; kb < KB; ++kb) {
+    __syncthreads();  // the previous K block's LDS rows are consumed
+    stage_a(xq, xs, H, KB, s_row, kb, s_a, s_sa);
+    u32x4 b[4][2];
+#pragma unroll
+    for (int si = 0; si < 4; ++si) {
+      b[si][0] = bnext[si][0];
+      b[si][1] = bnext[si][1];
+    }
+    if (kb + 1 < KB) {
+#pragma unroll
+      for (int si = 0; si < 4; ++si) load32(wrow[si] + (kb + 1) * kKB, bnext[si]);
+    }
+    const float sg = sw_gate[kb], su = sw_up[kb];
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      u32x4 a[2];
+      read_a(s_a, 16 * mi + j, q, a);
+      float sa[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sa[r] = s_sa[16 * mi + 4 * q + r];
+#pragma unroll
+      for (int si = 0; si < 4; ++si) {
+        const f32x4 part = mfma_k128(a, b[si]);
+        const float swv = si < 2 ? sg : su;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mi][si][r] += part[r] * sa[r] * swv;
+      }
+    }
+  }
+
+  // a = bf16(silu(bf16 gate) * bf16 up); row amax over the 128 columns
+  // (16 lanes x 2 subtiles per wave, then the 4 waves); fp8 quantisation.
+  float av[4][2][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float g = bf16_round(acc[mi][t][r]);
+        const float u = bf16_round(acc[mi][2 + t][r]);
+        av[mi][t][r] = bf16_round(g / (1.0f + expf(-g)) * u);
+      }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float m = fmaxf(fabsf(av[mi][0][r]), fabsf(av[mi][1][r]));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      if (j == 0) s_amax[wave][16 * mi + 4 * q + r] = m;
+    }
+  __syncthreads();
+  if (tid < kBM) {
+    const float m = fmaxf(fmaxf(s_amax[0][tid], s_amax[1][tid]), fmaxf(s_amax[2][tid], s_amax[3][tid]));
+    s_sa[tid] = quant_scale(m);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mi + 4 * q + r;
+      const float s = s_sa[row];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        s_q[row * kBN + 32 * wave + 16 * t + j] = static_cast<uint8_t>(to_fp8(clamp_fp8(av[mi][t][r] / s)));
+    }
+  __syncthreads();
+  {
+    const int row = tid >> 2, part = tid & 3;
+    const int p = s_pair[row];
+    if (p >= 0) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(s_q + row * kBN + part * 32);
+      u32x4* dst = reinterpret_cast<u32x4*>(act + static_cast<int64_t>(p) * I + n0 + part * 32);
+      dst[0] = src[0];
+      dst[1] = src[1];
+      if (part == 0) acts[static_cast<int64_t>(p) * (I / kKB) + n0 / kKB] = s_sa[row];
+    }
+  }
+}
+
+// GEMM2: down projection of 128 output columns times the routed weight,
+// bf16 rows per pair. grid = (H / 128, tile bound).
+__global__ void __launch_bounds__(kThreads) gemm2_kernel(const uint8_t* __restrict__ act, const float* __restrict__ acts,
+                                                         int64_t H, int64_t I, const float* __restrict__ topk_weight,
+                                                         const uint8_t* __restrict__ w2,
+                                                         const float* __restrict__ w2_scale,
+                                                         const int32_t* __restrict__ offsets,
+                                                         const int32_t* __restrict__ pairs,
+                                                         const int32_t* __restrict__ tiles,
+                                                         uint16_t* __restrict__ out) {
+  __shared__ int s_row[kBM];
+  __shared__ int s_pair[kBM];
+  __shared__ float s_sa[kBM];
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[kBM * kRowPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t s_o[kBM * kBN];
+
+  Tile tile;
+  if (!load_tile(tiles, offsets, tile)) return;
+  const int n0 = blockIdx.x * kBN;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const int KB = static_cast<int>(I / kKB);
+
+  tile_rows(tile, pairs, 1, s_pair, s_row);
+  __syncthreads();
+
+  const uint8_t* wrow[2];
+  const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) wrow[t] = wslot + static_cast<int64_t>(n0 + 32 * wave + 16 * t + j) * I + 32 * q;
+  const float* sw = w2_scale + (static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB;
+
+  f32x4 acc[4][2];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 bnext[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) load32(wrow[t], bnext[t]);
+  for (int kb = 0; kb < KB; ++kb) {
+    __syncthreads();
+    stage_a(act, acts, I, KB, s_row, kb, s_a, s_sa);
+    u32x4 b[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      b[t][0] = bnext[t][0];
+      b[t][1] = bnext[t][1];
+    }
+    if (kb + 1 < KB) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) load32(wrow[t] + (kb + 1) * kKB, bnext[t]);
+    }
+    const float swv = sw[kb];
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      u32x4 a[2];
+      read_a(s_a, 16 * mi + j, q, a);
+      float sa[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sa[r] = s_sa[16 * mi + 4 * q + r];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const f32x4 part = mfma_k128(a, b[t]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mi][t][r] += part[r] * sa[r] * swv;
+      }
+    }
+  }
+
+  __syncthreads();  // s_sa is reused for the routed weights
+  if (tid < kBM) s_sa[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
+  __syncthreads();
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mi + 4 * q + r;
+      const float wgt = s_sa[row];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        s_o[row * kBN + 32 * wave + 16 * t + j] = static_cast<uint16_t>(bf16_bits(acc[mi][t][r] * wgt));
+    }
+  __syncthreads();
+  // 256 bytes per row: 16 threads x 16 bytes, 16 rows per pass.
+  for (int row = tid >> 4; row < kBM; row += kThreads / 16) {
+    const int p = s_pair[row];
+    if (p < 0) continue;
+    const int col = (tid & 15) * 8;
+    *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
+        *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
+  }
+}
+
+// out[t] = bf16(sum over k of contrib[t*topk + k]) in fp32, k ascending,
+// over the pairs whose id is a valid expert.
+__global__ void __launch_bounds__(256) topk_sum_kernel(const uint16_t* __restrict__ contrib, int64_t H, int topk,
+                                                       const void* ids, int eb, int E, uint16_t* __restrict__ out) {
+  const int64_t t = blockIdx.y;
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
+  if (c >= H) return;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < topk; ++k) {
+    const int64_t p = t * topk + k;
+    const int64_t e = load_id(ids, eb, p);
+    if (e < 0 || e >= E) continue;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(contrib + p * H + c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[2 * i] += bf16_value(v[i] & 0xffffu);
+      s[2 * i + 1] += bf16_value(v[i] >> 16);
+    }
+  }
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = bf16_bits(s[2 * i]) | (bf16_bits(s[2 * i + 1]) << 16);
+  *reinterpret_cast<u32x4*>(out + t * H + c) = o;
+}
+
+}  // namespace
+}  // namespace xp
+
+using namespace xp;
+
+extern "C" {
+
+int64_t xp_moe_max_tiles(int64_t npairs, int64_t slots) {
+  if (npairs <= 0 || slots <= 0) return 0;
+  return (npairs + kBM - 1) / kBM + (slots < npairs ? slots : npairs);
+}
+
+int xp_quant_tokens(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq, float* xs, void* stream) {
+  XP_REQUIRE(T >= 0 && T <= INT32_MAX && H > 0 && H % kKB == 0,
+             "xp_quant_tokens: T=%lld, H=%lld (H must be a positive multiple of %d)", (long long)T, (long long)H,
+             kKB);
+  if (T == 0) return XP_OK;
+  XP_REQUIRE(x && xq && xs && aligned16(x) && aligned16(xq), "xp_quant_tokens: null or misaligned buffer");
+  hipLaunchKernelGGL(quant_tokens_kernel, dim3(static_cast<unsigned>(T)), dim3(256), 0, as_stream(stream), x, H, xq,
+                     xs);
+  return check_launch("quant_tokens_kernel");
+}
+
+int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T, int64_t topk, const int32_t* expert_map,
+                 int64_t num_experts, int64_t slots, int32_t* offsets, int32_t* pairs, int32_t* tiles, void* stream) {
+  XP_REQUIRE(topk_elem_bytes == 4 || topk_elem_bytes == 8, "xp_moe_route: id size %d", topk_elem_bytes);
+  XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX, "xp_moe_route: T=%lld, topk=%lld", (long long)T,
+             (long long)topk);
+  XP_REQUIRE(slots >= 1 && slots <= kMaxRouteSlots, "xp_moe_route: %lld slots (at most %d)", (long long)slots,
+             kMaxRouteSlots);
+  XP_REQUIRE(num_experts >= 1 && num_experts <= INT32_MAX, "xp_moe_route: %lld experts", (long long)num_experts);
+  XP_REQUIRE(expert_map && offsets && pairs && tiles && (T == 0 || topk_ids), "xp_moe_route: null argument");
+  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, as_stream(stream), topk_ids, topk_elem_bytes,
+                     T * topk, expert_map, static_cast<int>(num_experts), static_cast<int>(slots), offsets, pairs,
+                     tiles);
+  return check_launch("route_kernel");
+}
+
+int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
+                   int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
+                   int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, uint8_t* act,
+                   float* acts, uint16_t* out, void* stream) {
+  XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0,
+             "xp_moe_experts: H=%lld and I=%lld must be positive multiples of %d", (long long)H, (long long)I, kBN);
+  XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX && slots >= 1 && slots <= kMaxRouteSlots,
+             "xp_moe_experts: T=%lld, topk=%lld, slots=%lld", (long long)T, (long long)topk, (long long)slots);
+  if (T == 0) return XP_OK;
+  XP_REQUIRE(xq && xs && topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && act &&
+                 acts && out,
+             "xp_moe_experts: null argument");
+  XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(act) && aligned16(out),
+             "xp_moe_experts: fp8 and output buffers must be 16-byte aligned");
+  const int64_t bound = xp_moe_max_tiles(T * topk, slots);
+  XP_REQUIRE(bound <= 65535, "xp_moe_experts: %lld tiles exceed the launch grid", (long long)bound);
+  hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(I / kBN), static_cast<unsigned>(bound)), dim3(kThreads),
+                     0, as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles,
+                     act, acts);
+  const int rc = check_launch("gemm1_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(H / kBN), static_cast<unsigned>(bound)), dim3(kThreads),
+                     0, as_stream(stream), act, acts, H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, out);
+  return check_launch("gemm2_kernel");
+}
+
+int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk, int64_t H, const void* topk_ids,
+                    int topk_elem_bytes, int64_t num_experts, uint16_t* out, void* stream) {
+  XP_REQUIRE(T >= 0 && T <= 65535 && topk >= 1 && H > 0 && H % 8 == 0,
+             "xp_moe_topk_sum: T=%lld (at most 65535), topk=%lld, H=%lld (a multiple of 8)", (long long)T,
+             (long long)topk, (long long)H);
+  XP_REQUIRE(topk_elem_bytes == 4 || topk_elem_bytes == 8, "xp_moe_topk_sum: id size %d", topk_elem_bytes);
+  if (T == 0) return XP_OK;
+  XP_REQUIRE(contrib && out && topk_ids && aligned16(contrib) && aligned16(out),
+             "xp_moe_topk_sum: null or misaligned buffer");
+  const unsigned bx = static_cast<unsigned>((H / 8 + 255) / 256);
+  hipLaunchKernelGGL(topk_sum_kernel, dim3(bx, static_cast<unsigned>(T)), dim3(256), 0, as_stream(stream), contrib, H,
+                     static_cast<int>(topk), topk_ids, topk_elem_bytes, static_cast<int>(num_experts), out);
+  return check_launch("topk_sum_kernel");
+}
+
+}  // extern "C"

@@ -104,9 +104,10 @@ _SIGNATURES = {
     "ssd_error": (ctypes.c_char_p, [_P]),
     "ssd_test_delay": (None, [_P, ctypes.c_double]),
     "xp_quant_tokens": (_I, [_P, _L, _L, _P, _P, _P]),
-    "xp_moe_route": (_I, [_P, _I, _L, _L, _P, _L, _L, _L, _P, _P, _P, _P]),
-    "xp_moe_experts": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _L, _P, _P, _P, _P, _P, _P]),
-    "xp_moe_topk_sum": (_I, [_P, _L, _L, _L, _P, _P]),
+    "xp_moe_max_tiles": (_L, [_L, _L]),
+    "xp_moe_route": (_I, [_P, _I, _L, _L, _P, _L, _L, _P, _P, _P, _P]),
+    "xp_moe_experts": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P, _P, _P]),
+    "xp_moe_topk_sum": (_I, [_P, _L, _L, _L, _P, _I, _L, _P, _P]),
 }
 
 _lib = None
