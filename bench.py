@@ -28,6 +28,7 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP8_PEAK_TFLOPS = 5000.0  # dense fp8 MFMA, MI355X
 SHAPES = ((1024, 2048), (2048, 512))  # w13, w2 (rows, cols) of fp8
 PITCH_RATIO = 0.89
 
@@ -76,6 +77,19 @@ def algorithmic_bytes(stg: list[np.ndarray], n_bytes: list[int], chunk: int = 51
         words = s[:, 4 * G : 4 * G + 4].view(np.int32).astype(np.int64).reshape(-1)  # gstart[G]
         total += int(((4 * (G + 1) + n // 2 + 512 + n) * s.shape[0]) + 4 * words.sum())
     return total
+
+
+def decode_traffic(rows: int):
+    """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the same counters on a plain device copy), read from the committed profile
+    summary of the same workload; None when there is none for this row count."""
+    path = os.path.join(ROOT, "profiles", f"decode_traffic_{rows}rows.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
 
 
 def bench_decode(args, dev, cores):
@@ -265,6 +279,101 @@ def bench_acquire(args, dev):
     return {"us_per_layer": round(us_layer, 3)}
 
 
+def bench_moe(args, dev):
+    """Expert FFN of one prefill layer: 2048 tokens x top-8 over 256 experts.
+
+    Experts are w13 fp8 1024x2048 + w2 fp8 2048x512 with 128x128 block
+    scales, tokens bf16 ~N(0,1), softmax gate weights over the top 8 of
+    random logits (near-uniform coverage). Times the two GEMM launches over
+    a 256-slot slab (one-shot), the whole layer (quantise, route, GEMMs,
+    top-k sum), and the overflow path's compute over four 64-row chunks,
+    which must give the one-shot bits.
+    """
+    from vllm_expert_pager import moe
+
+    E, H, I, T, topk, W = 256, 2048, 512, 2048, 8, 64
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def quantised(n, k):
+        q = torch.empty((E, n, k), dtype=torch.uint8, device=dev)
+        s = torch.empty((E, n // 128, k // 128), dtype=torch.float32, device=dev)
+        for e in range(E):
+            w = torch.randn((n, k), generator=g, device=dev) * 0.02
+            b = w.view(n // 128, 128, k // 128, 128)
+            se = (b.abs().amax(dim=(1, 3)) / 448.0).clamp_min(1e-10)
+            q[e] = (b / se[:, None, :, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).view(n, k)
+            s[e] = se
+        return q, s
+
+    w13, w13s = quantised(2 * I, H)
+    w2, w2s = quantised(H, I)
+    x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    top, ids = torch.randn((T, E), generator=g, device=dev).topk(topk, dim=1)
+    tw = torch.softmax(top, dim=1).float().contiguous()
+    xq, xs = moe.quant_tokens(x)
+    emap = torch.arange(E, dtype=torch.int32, device=dev)
+    r = moe.route(ids, emap, E)
+    contrib = torch.zeros((T * topk, H), dtype=torch.bfloat16, device=dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, reps):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    reps = max(3, args.moe_steps)
+    ms_gemm = timed(lambda: moe.run_experts(xq, xs, tw, w13, w13s, w2, w2s, r, contrib), reps)
+    one = moe.topk_sum(contrib, ids, E)
+    ms_layer = timed(lambda: moe.fused_moe(x, tw, ids, w13, w13s, w2, w2s), reps)
+
+    chunk_maps = []
+    for k in range(E // W):
+        m = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        m[k * W : (k + 1) * W] = torch.arange(W, dtype=torch.int32, device=dev)
+        chunk_maps.append(m)
+    contrib2 = torch.zeros_like(contrib)
+
+    def chunked():
+        xq2, xs2 = moe.quant_tokens(x)
+        for k, m in enumerate(chunk_maps):
+            rk = moe.route(ids, m, W)
+            sl = slice(k * W, (k + 1) * W)
+            moe.run_experts(xq2, xs2, tw, w13[sl], w13s[sl], w2[sl], w2s[sl], rk, contrib2)
+        return moe.topk_sum(contrib2, ids, E)
+
+    ms_chunked = timed(chunked, reps)
+    two = chunked()
+    exact = bool(torch.equal(one.view(torch.int16), two.view(torch.int16)))
+    if not exact:
+        raise SystemExit("chunked expert FFN differs from the one-shot run")
+    pairs = T * topk
+    flops = 2.0 * pairs * (2 * I * H + H * I)
+    weight_bytes = E * (2 * I * H + H * I) + 4 * (w13s.numel() + w2s.numel())
+    # Minimum HBM traffic of the two GEMMs: weights once, tokens once, the
+    # fp8 activation written and read, the bf16 contributions written.
+    alg_bytes = weight_bytes + T * H + 4 * T * H // 128 + 2 * pairs * I + 2 * pairs * H
+    tflops = flops / (ms_gemm * 1e-3) / 1e12
+    out = {
+        "workload": f"{T} tokens x top-{topk} over {E} experts (w13 2x{I}x{H}, w2 {H}x{I} fp8, 128x128 scales)",
+        "ms_gemm": round(ms_gemm, 4),
+        "tflops": round(tflops, 1),
+        "mfma_frac": round(tflops / MFMA_FP8_PEAK_TFLOPS, 4),
+        "hbm_gbps": round(alg_bytes / (ms_gemm * 1e-3) / 1e9, 1),
+        "hbm_frac": round(alg_bytes / (ms_gemm * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "ms_layer_one_shot": round(ms_layer, 4),
+        "ms_layer_chunked_4x64": round(ms_chunked, 4),
+        "chunked_bit_exact": exact,
+    }
+    log(f"moe: {out}")
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -274,7 +383,12 @@ def main() -> None:
     ap.add_argument("--cpu-rows", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gather-steps", type=int, default=10)
+    ap.add_argument("--moe-steps", type=int, default=5)
     ap.add_argument("--only-decode", action="store_true")
+    ap.add_argument("--only-moe", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="after the decode leg, copy this many MiB device to device three times "
+                         "(the plain copy that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -289,11 +403,25 @@ def main() -> None:
     torch.cuda.set_device(dev)
     cores = len(os.sched_getaffinity(0))
 
+    if args.only_moe:
+        print(json.dumps({"moe": bench_moe(args, dev)}), flush=True)
+        return
     dec = bench_decode(args, dev, cores)
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        a = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        for _ in range(3):
+            torch.bitwise_not(a, out=b)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 device copies and 3 elementwise passes of {args.copy_probe_mib} MiB")
     extras = {}
     if not args.only_decode:
         extras["gather"] = bench_gather(args, dev)
         extras["acquire"] = bench_acquire(args, dev)
+        extras["moe"] = bench_moe(args, dev)
     line = {
         "metric": "Huffman decode GB/s (% HBM peak); gather GB/s; acquire us/layer; decode tok/s",
         "value": round(dec["gbps"], 2),
@@ -320,7 +448,7 @@ def main() -> None:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": decode_traffic(args.rows),
         },
         "cpu_baseline": dec["cpu"],
         "decode_raw_output_gbps": round(dec["raw_gbps"], 2),
