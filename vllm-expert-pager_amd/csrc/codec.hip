@@ -10,9 +10,10 @@
 // its half of the wave ballot (mbcnt) -- exactly the encoder's
 // (symbol index, lane) word order.
 //
-// Memory: the group's Huffman words stream through a 512-word ring in LDS
-// (plus a mirror of its head, so an iteration's reads never wrap), filled
-// with coalesced loads issued one 8-symbol iteration ahead of use; the
+// Memory: the group's Huffman words stream through a 256-word ring in LDS
+// (plus a 160-word mirror of its head, so a half-iteration's reads never
+// wrap), filled with coalesced 32-word loads issued one half-iteration (4
+// symbols) ahead of use; the
 // 512-entry LUT is split into a length table and a pre-shifted exponent
 // table in LDS; the sign/mantissa nibbles arrive as coalesced 32-bit words
 // (8 values each), prefetched an iteration ahead.
