@@ -374,6 +374,202 @@ def bench_moe(args, dev):
     return out
 
 
+# ---- 40-layer decode trace with a Qwen3-MoE-shaped model ----
+
+QWEN = {"layers": 40, "hidden": 2048, "heads": 32, "kv_heads": 4, "head_dim": 128, "experts": 256,
+        "intermediate": 512, "topk": 8, "vocab": 151936, "rope_theta": 1e6, "eps": 1e-6}
+
+
+def zipf_trace(rng, steps: int, layers: int, E: int, k: int, s: float, reuse: float) -> np.ndarray:
+    """(steps, layers, k) expert ids: Zipf(s) over a per-layer permutation, k distinct per step;
+    with probability `reuse` a layer repeats its previous step's set."""
+    p = np.arange(1, E + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    perms = [rng.permutation(E) for _ in range(layers)]
+    out = np.empty((steps, layers, k), np.int32)
+    for t in range(steps):
+        for l in range(layers):
+            if t > 0 and rng.random() < reuse:
+                out[t, l] = out[t - 1, l]
+            else:
+                out[t, l] = perms[l][rng.choice(E, k, replace=False, p=p)]
+    return out
+
+
+def quantised_experts(E: int, H: int, I: int, g, dev):
+    """Synthetic block-fp8 experts on the GPU: N(0, 0.02) weights, one amax/448 scale per 128x128 block."""
+    def one(n, k):
+        q = torch.empty((E, n, k), dtype=torch.uint8, device=dev)
+        s = torch.empty((E, n // 128, k // 128), dtype=torch.float32, device=dev)
+        for e0 in range(0, E, 32):
+            w = torch.randn((min(32, E - e0), n, k), generator=g, device=dev) * 0.02
+            b = w.view(-1, n // 128, 128, k // 128, 128)
+            se = (b.abs().amax(dim=(2, 4)) / 448.0).clamp_min(1e-10)
+            q[e0 : e0 + w.shape[0]] = (b / se[:, :, None, :, None]).clamp(-448, 448).to(
+                torch.float8_e4m3fn).view(torch.uint8).view(-1, n, k)
+            s[e0 : e0 + w.shape[0]] = se
+        return q, s
+    w13, w13s = one(2 * I, H)
+    w2, w2s = one(H, I)
+    return w13, w13s, w2, w2s
+
+
+class QwenMoeDecoder:
+    """Random-init Qwen3-MoE-shaped decoder (bf16 non-expert weights) whose experts are paged.
+
+    Per layer: RMSNorm, fused QKV projection, per-head q/k RMSNorm, RoPE,
+    GQA attention over a static KV cache with a position mask, output
+    projection, RMSNorm, router (softmax over the logits of the traced
+    ids), the paged expert FFN, residuals. Final RMSNorm, LM head, greedy
+    next token. Shapes are static, so one step is captured in a hipGraph.
+    """
+
+    def __init__(self, dev, pager, layers, trace, ctx: int):
+        c = QWEN
+        self.dev, self.pager, self.layers = dev, pager, layers
+        H, nh, kv, hd = c["hidden"], c["heads"], c["kv_heads"], c["head_dim"]
+        self.H, self.nh, self.kv, self.hd, self.ctx = H, nh, kv, hd, ctx
+        g = torch.Generator(device=dev).manual_seed(11)
+        bf = {"dtype": torch.bfloat16, "device": dev}
+        rnd = lambda *shape: (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        L = len(layers)
+        self.w_qkv = [rnd((nh + 2 * kv) * hd, H) for _ in range(L)]
+        self.w_o = [rnd(H, nh * hd) for _ in range(L)]
+        self.w_router = [rnd(c["experts"], H) for _ in range(L)]
+        self.ln1 = [torch.ones(H, **bf) for _ in range(L)]
+        self.ln2 = [torch.ones(H, **bf) for _ in range(L)]
+        self.qn = [torch.ones(hd, **bf) for _ in range(L)]
+        self.kn = [torch.ones(hd, **bf) for _ in range(L)]
+        self.embed = rnd(c["vocab"], H)
+        self.lm_head = rnd(c["vocab"], H)
+        self.norm = torch.ones(H, **bf)
+        self.kcache = torch.zeros((L, kv, hd, ctx), **bf)   # K stored transposed: (kv, dim, ctx)
+        self.vcache = torch.zeros((L, kv, ctx, hd), **bf)
+        inv = 1.0 / (c["rope_theta"] ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+        ang = torch.arange(ctx, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
+        self.cos, self.sin = ang.cos(), ang.sin()
+        self.trace = trace                                   # (steps, L, k) int32 on the device
+        self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.token = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.positions = torch.arange(ctx, device=dev)
+
+    def _rms(self, x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + QWEN["eps"])).to(torch.bfloat16) * w
+
+    def _rope(self, x):  # x (heads, hd) bf16
+        cos = self.cos.index_select(0, self.pos)  # (1, hd/2)
+        sin = self.sin.index_select(0, self.pos)
+        xf = x.float()
+        a, b = xf[:, 0::2], xf[:, 1::2]
+        out = torch.empty_like(xf)
+        out[:, 0::2] = a * cos - b * sin
+        out[:, 1::2] = a * sin + b * cos
+        return out.to(torch.bfloat16)
+
+    def forward_step(self):
+        nh, kv, hd, H = self.nh, self.kv, self.hd, self.H
+        ids_all = self.trace.index_select(0, self.step).squeeze(0)  # (L, k)
+        h = self.embed.index_select(0, self.token)                  # (1, H)
+        mask = self.positions <= self.pos
+        for l, layer in enumerate(self.layers):
+            x = self._rms(h, self.ln1[l])
+            qkv = torch.nn.functional.linear(x, self.w_qkv[l])[0]
+            q = self._rope(self._rms(qkv[: nh * hd].view(nh, hd), self.qn[l]))
+            k = self._rope(self._rms(qkv[nh * hd : (nh + kv) * hd].view(kv, hd), self.kn[l]))
+            v = qkv[(nh + kv) * hd :].view(kv, hd)
+            self.kcache[l].index_copy_(2, self.pos, k.unsqueeze(2))
+            self.vcache[l].index_copy_(1, self.pos, v.unsqueeze(1))
+            qg = q.view(kv, nh // kv, hd)
+            scores = torch.matmul(qg, self.kcache[l]).float() * (hd ** -0.5)  # (kv, g, ctx)
+            scores = scores.masked_fill(~mask, float("-inf"))
+            probs = torch.softmax(scores, dim=-1).to(torch.bfloat16)
+            attn = torch.matmul(probs, self.vcache[l]).reshape(1, nh * hd)
+            h = h + torch.nn.functional.linear(attn, self.w_o[l])
+            x2 = self._rms(h, self.ln2[l])
+            logits = torch.nn.functional.linear(x2, self.w_router[l]).float()
+            ids = ids_all[l : l + 1]                                         # (1, k) traced routing
+            w = torch.softmax(logits.gather(1, ids.long()), dim=-1)          # renormalised over the top-k
+            h = h + layer.forward(x2, w, ids)
+        logits = torch.nn.functional.linear(self._rms(h, self.norm), self.lm_head)
+        # Greedy token in two single-workgroup reductions (vocab = 1187 x 128).
+        best, idx = logits.view(-1, 128).max(dim=1)
+        row = best.argmax().view(1)
+        self.token.copy_((row * 128 + idx.index_select(0, row)).clamp_(0, QWEN["vocab"] - 1))
+        self.pos.add_(1)
+        self.step.add_(1)
+
+
+def bench_model_decode(args, dev):
+    """Decode trace: 40 MoE layers x 256 experts x 3 MiB, 32 cache slots, every expert in a raw pinned
+    RAM tier, batch 1, top-8, Zipf(1.1) routing with 70% reuse of the previous step's set per layer.
+    One decode step of the whole model is one hipGraph replay."""
+    from vllm_expert_pager import pager as pg
+
+    c = QWEN
+    L, E, H, I, k = c["layers"], c["experts"], c["hidden"], c["intermediate"], c["topk"]
+    steps, warm = args.decode_steps, args.decode_warmup
+    t0 = time.time()
+    settings = pg.Settings(cache_slots=32, ram_slots=None, compress="off", working_rows=64, log_interval=0)
+    pager = pg.Pager(settings, L, E, H, I, dev)
+    layers = []
+    g = torch.Generator(device=dev).manual_seed(3)
+    for l in range(L):
+        layer = pager.add_layer()
+        w13, w13s, w2, w2s = quantised_experts(E, H, I, g, dev)
+        pager.store.write_raw_rows(layer.layer, "w13_weight", w13.view(E, -1))
+        pager.store.write_raw_rows(layer.layer, "w2_weight", w2.view(E, -1))
+        del w13, w2
+        layer.setup({pg.SCALES[0]: w13s, pg.SCALES[1]: w2s})
+        layers.append(layer)
+    torch.cuda.synchronize()
+    log(f"model: {L} layers x {E} experts loaded in {time.time() - t0:.1f}s "
+        f"(RAM tier {pager.store.rows * pager.store.record_bytes / 2**30:.1f} GiB pinned)")
+    rng = np.random.default_rng(2025)
+    trace = torch.from_numpy(zipf_trace(rng, warm + steps, L, E, k, 1.1, 0.7)).to(dev)
+    model = QwenMoeDecoder(dev, pager, layers, trace, ctx=warm + steps + 1)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        model.forward_step()  # eager step 0 (also warms the allocator)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            model.forward_step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    # Capture records without running; replays continue from step 1.
+    for _ in range(max(0, warm - 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    before = [lay.hit_rates() for lay in layers]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    after = [lay.hit_rates() for lay in layers]
+    vh = sum(a[0] - b[0] for a, b in zip(after, before))
+    vm = sum(a[1] - b[1] for a, b in zip(after, before))
+    out = {
+        "workload": f"{L}-layer decode trace, {E} experts x 3 MiB, 32 cache slots, all experts in a raw "
+                    f"pinned RAM tier, batch 1, top-{k}, Zipf(1.1) with 0.7 reuse, {steps} steps in one "
+                    "captured hipGraph per step",
+        "tok_s": round(1e3 / ms, 2),
+        "ms_per_token": round(ms, 4),
+        "us_per_layer": round(ms * 1e3 / L, 2),
+        "vram_hit_rate": round(vh / max(1, vh + vm), 4),
+        "misses_per_layer_step": round(vm / (L * steps), 3),
+        "steps": steps,
+    }
+    log(f"model decode: {out}")
+    pager.close()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -386,6 +582,9 @@ def main() -> None:
     ap.add_argument("--moe-steps", type=int, default=5)
     ap.add_argument("--only-decode", action="store_true")
     ap.add_argument("--only-moe", action="store_true")
+    ap.add_argument("--only-model", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=2000)
+    ap.add_argument("--decode-warmup", type=int, default=20)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after the decode leg, copy this many MiB device to device three times "
                          "(the plain copy that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -406,6 +605,9 @@ def main() -> None:
     if args.only_moe:
         print(json.dumps({"moe": bench_moe(args, dev)}), flush=True)
         return
+    if args.only_model:
+        print(json.dumps({"model_decode": bench_model_decode(args, dev)}), flush=True)
+        return
     dec = bench_decode(args, dev, cores)
     if args.copy_probe_mib:
         n = args.copy_probe_mib << 20
@@ -422,6 +624,7 @@ def main() -> None:
         extras["gather"] = bench_gather(args, dev)
         extras["acquire"] = bench_acquire(args, dev)
         extras["moe"] = bench_moe(args, dev)
+        extras["model_decode"] = bench_model_decode(args, dev)
     line = {
         "metric": "Huffman decode GB/s (% HBM peak); gather GB/s; acquire us/layer; decode tok/s",
         "value": round(dec["gbps"], 2),

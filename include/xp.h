@@ -295,19 +295,26 @@ int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T,
                  int64_t slots, int32_t* offsets, int32_t* pairs,
                  int32_t* tiles, void* stream);
 
+/* Bytes of the workspace xp_moe_experts needs for npairs = T*topk pairs
+ * (bf16 and fp8 activations with their scales). */
+int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I);
+
 /* Expert FFN of every routed pair, on the slab slot route chose:
  *   h = w13 . xq (block-scaled, fp32), gate = bf16(h[:I]), up = bf16(h[I:])
- *   a = bf16(silu(gate) * up), quantised like xp_quant_tokens into
- *       act[pair][I] fp8 / acts[pair][I/128] fp32 (workspaces)
+ *   a = bf16(silu(gate) * up), quantised like xp_quant_tokens per 128 columns
  *   out[pair][H] = bf16(topk_weight[pair] * (w2 . a)) (bf16 bits)
- * topk_weight is fp32 [T*topk]. Pairs that were not routed are not written.
- * H and I are multiples of 128; fp8 buffers and out 16-byte aligned. */
+ * topk_weight is fp32 [T*topk]; work is a 256-byte aligned device buffer of
+ * xp_moe_workspace_bytes(T*topk, I) bytes (no initial contents needed).
+ * Pairs that were not routed are not written. Three launches: gate/up
+ * (32 activation columns per workgroup, K split over its waves), activation
+ * quantisation, down projection. H and I are multiples of 128, at most 8192;
+ * fp8 buffers and out 16-byte aligned. */
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T,
                    int64_t topk, const float* topk_weight, int64_t H,
                    int64_t I, const uint8_t* w13, const float* w13_scale,
                    const uint8_t* w2, const float* w2_scale, int64_t slots,
                    const int32_t* offsets, const int32_t* pairs,
-                   const int32_t* tiles, uint8_t* act, float* acts,
+                   const int32_t* tiles, void* work, int64_t work_bytes,
                    uint16_t* out, void* stream);
 
 /* The single top-k combine (moe_sum after collect, experts.py:546-552):

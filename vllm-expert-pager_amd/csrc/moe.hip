@@ -18,10 +18,12 @@
 // contribution = bf16(y * routed weight).
 //
 // Work decomposition: route lists the pairs of each slab slot in CSR form
-// and cuts them into tiles of 64 pairs of one slot; a GEMM workgroup takes
-// one tile and 128 output columns. Launch grids are sized from the shapes
-// alone (a bound on the tile count), so the sequence is graph-capturable;
-// workgroups past the live tile count exit at once.
+// and cuts them into tiles of 64 pairs of one slot. gemm1 takes one tile
+// and 32 activation columns per workgroup (so a decode step of 8 pairs
+// still spreads over 128 workgroups), act_quant one tile, gemm2 one tile and
+// 128 output columns. Launch grids are sized from the shapes alone (a bound
+// on the tile count), so the sequence is graph-capturable; workgroups past
+// the live tile count exit at once.
 #include <hip/hip_bf16.h>
 
 #include "common.h"
@@ -37,7 +39,6 @@ constexpr int kBM = 64;          // pairs per tile
 constexpr int kBN = 128;         // output columns per workgroup (one quant group for GEMM1)
 constexpr int kKB = 128;         // K block = scale block = one MFMA K
 constexpr int kThreads = 256;    // 4 waves, split along N (32 columns each)
-constexpr int kRowPitch = 144;   // LDS bytes per staged A row (128 + 16 against bank conflicts)
 constexpr int kRouteThreads = 1024;
 constexpr int kMaxRouteSlots = 1024;
 constexpr float kFp8Max = 448.0f;
@@ -142,31 +143,44 @@ __device__ __forceinline__ int2 block_scan2(int a, int b, int2* s_tot, int2* tot
 
 // ---- routing: CSR lists of the pairs of each slab slot, and the tiles ----
 // offsets[slots + 1]; pairs[offsets[s] .. offsets[s+1]) = pair ids t*topk + k
-// of slot s (in no particular order); tiles[0] = live tile count, then
-// (slot, first pair position) per tile.
+// of slot s; tiles[0] = live tile count, then (slot, first pair position)
+// per tile. Each wave counts a contiguous range of pairs into its own LDS
+// histogram (no contention between waves), so a slot's list is ordered by
+// wave range; dynamic LDS = 16 * slots ints.
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, int eb, int64_t npairs,
                                                               const int32_t* __restrict__ expert_map, int E,
                                                               int slots, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ pairs,
                                                               int32_t* __restrict__ tiles) {
-  __shared__ int s_cnt[kMaxRouteSlots];
+  extern __shared__ int s_hist[];  // [16 waves][slots]
   __shared__ int2 s_tot[kRouteThreads / 64];
-  const int tid = threadIdx.x;
-  if (tid < slots) s_cnt[tid] = 0;
+  constexpr int kW = kRouteThreads / 64;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int i = tid; i < kW * slots; i += kRouteThreads) s_hist[i] = 0;
   __syncthreads();
-  for (int64_t p = tid; p < npairs; p += kRouteThreads) {
+  const int64_t per = (npairs + kW - 1) / kW;
+  const int64_t lo = wave * per, hi = lo + per < npairs ? lo + per : npairs;
+  int* hist = s_hist + wave * slots;
+  for (int64_t p = lo + lane; p < hi; p += 64) {
     const int64_t e = load_id(ids, eb, p);
     const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
-    if (s >= 0 && s < slots) atomicAdd(&s_cnt[s], 1);
+    if (s >= 0 && s < slots) atomicAdd(&hist[s], 1);
   }
   __syncthreads();
-  const int c = tid < slots ? s_cnt[tid] : 0;
+  int c = 0;
+  if (tid < slots) {
+    for (int w = 0; w < kW; ++w) {  // per-wave counts -> per-wave starts within the slot
+      const int v = s_hist[w * slots + tid];
+      s_hist[w * slots + tid] = c;
+      c += v;
+    }
+  }
   const int nt = (c + kBM - 1) / kBM;
   int2 total;
   const int2 off = block_scan2(c, nt, s_tot, &total);
   if (tid < slots) {
     offsets[tid] = off.x;
-    s_cnt[tid] = off.x;  // becomes the scatter cursor
+    for (int w = 0; w < kW; ++w) s_hist[w * slots + tid] += off.x;  // scatter cursors
     for (int i = 0; i < nt; ++i) {
       tiles[1 + 2 * (off.y + i)] = tid;
       tiles[2 + 2 * (off.y + i)] = off.x + i * kBM;
@@ -177,10 +191,10 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, i
     tiles[0] = total.y;
   }
   __syncthreads();
-  for (int64_t p = tid; p < npairs; p += kRouteThreads) {
+  for (int64_t p = lo + lane; p < hi; p += 64) {
     const int64_t e = load_id(ids, eb, p);
     const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
-    if (s >= 0 && s < slots) pairs[atomicAdd(&s_cnt[s], 1)] = static_cast<int32_t>(p);
+    if (s >= 0 && s < slots) pairs[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(p);
   }
 }
 
@@ -198,26 +212,6 @@ __device__ __forceinline__ bool load_tile(const int32_t* tiles, const int32_t* o
   return true;
 }
 
-// Stage K block kb of the tile's A rows into LDS ([kBM][kRowPitch] bytes)
-// and their scales: 4 threads x 32 bytes per row.
-__device__ __forceinline__ void stage_a(const uint8_t* __restrict__ A, const float* __restrict__ As, int64_t lda,
-                                        int kblocks, const int* s_row, int kb, uint8_t* s_a, float* s_sa) {
-  const int r = threadIdx.x >> 2, part = threadIdx.x & 3;
-  const int64_t row = s_row[r];
-  u32x4 v[2];
-  load32(A + row * lda + kb * kKB + part * 32, v);
-  u32x4* dst = reinterpret_cast<u32x4*>(s_a + r * kRowPitch + part * 32);
-  dst[0] = v[0];
-  dst[1] = v[1];
-  if (part == 0) s_sa[r] = As[row * kblocks + kb];
-}
-
-__device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4 (&a)[2]) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(s_a + row * kRowPitch + 32 * q);
-  a[0] = p[0];
-  a[1] = p[1];
-}
-
 // Tile rows: the pair of each row (-1 for padding) and the A row it reads
 // (padding rows repeat the tile's first pair, so every load stays inside
 // the operand).
@@ -230,152 +224,225 @@ __device__ __forceinline__ void tile_rows(const Tile& tile, const int32_t* pairs
   }
 }
 
-// GEMM1: gate/up for 128 activation columns, SiLU*up, per-pair fp8
-// quantisation of the activation. grid = (I / 128, tile bound).
+// Workspace of xp_moe_experts: bf16 activations, their per-32-column
+// maxima, the fp8 activations and their per-128-column scales.
+struct Work {
+  uint16_t* a16;   // [npairs][I]
+  float* amax32;   // [npairs][I/32]
+  uint8_t* act;    // [npairs][I]
+  float* acts;     // [npairs][I/128]
+};
+
+inline int64_t align256(int64_t n) { return (n + 255) & ~int64_t(255); }
+
+inline int64_t work_layout(int64_t npairs, int64_t I, Work* w, uint8_t* base) {
+  const int64_t sz[4] = {align256(npairs * I * 2), align256(npairs * (I / 32) * 4), align256(npairs * I),
+                         align256(npairs * (I / kKB) * 4)};
+  if (w) {
+    w->a16 = reinterpret_cast<uint16_t*>(base);
+    w->amax32 = reinterpret_cast<float*>(base + sz[0]);
+    w->act = base + sz[0] + sz[1];
+    w->acts = reinterpret_cast<float*>(base + sz[0] + sz[1] + sz[2]);
+  }
+  return sz[0] + sz[1] + sz[2] + sz[3];
+}
+
+constexpr int kC1 = 32;       // activation columns per gemm1 workgroup
+constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I <= 8192)
+
+// GEMM1: gate and up for 32 activation columns of one tile. The 4 waves
+// are 2 K halves x 2 column halves: wave w takes the K blocks kh, kh+2, ...
+// (kh = w / 2) of the gate and up rows of column half ch = w % 2; the second
+// K half's partial sums are added in LDS. Then a = bf16(silu(bf16 gate) *
+// bf16 up) is written as bf16 together with the maximum |a| of each row's
+// 32 columns. Only the 16-row subtiles that hold pairs are computed.
+// grid = (I / 32, tile bound).
 __global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
                                                          int64_t H, int64_t I, int topk,
                                                          const uint8_t* __restrict__ w13,
                                                          const float* __restrict__ w13_scale,
                                                          const int32_t* __restrict__ offsets,
                                                          const int32_t* __restrict__ pairs,
-                                                         const int32_t* __restrict__ tiles,
-                                                         uint8_t* __restrict__ act, float* __restrict__ acts) {
+                                                         const int32_t* __restrict__ tiles, Work work) {
   __shared__ int s_row[kBM];
   __shared__ int s_pair[kBM];
-  __shared__ float s_sa[kBM];
-  __shared__ float s_amax[4][kBM];
-  __shared__ __attribute__((aligned(16))) uint8_t s_a[kBM * kRowPitch];
-  __shared__ __attribute__((aligned(16))) uint8_t s_q[kBM * kBN];
+  __shared__ float s_xs[kBM * kMaxKB];  // token scales per row and K block; then the bf16 staging
+  __shared__ f32x4 s_red[2][4][2][64];  // [column half][row subtile][gate, up][lane]
+  __shared__ float s_m[2][kBM];         // row maxima per column half
+  __shared__ float s_sw[2][kMaxKB];     // gate and up weight scales per K block
 
   Tile tile;
   if (!load_tile(tiles, offsets, tile)) return;
-  const int n0 = blockIdx.x * kBN;
+  const int c0 = blockIdx.x * kC1;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
+  const int kh = wave >> 1, ch = wave & 1;
   const int KB = static_cast<int>(H / kKB);
+  const int nmi = (tile.count + 15) >> 4;
 
   tile_rows(tile, pairs, topk, s_pair, s_row);
   __syncthreads();
-
-  // B rows of this lane: gate rows n0 + 32*wave + 16t + j and the up rows I below them.
-  const uint8_t* wrow[4];
-  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int64_t n = n0 + 32 * wave + 16 * t + j;
-    wrow[t] = wslot + n * H + 32 * q;
-    wrow[2 + t] = wslot + (I + n) * H + 32 * q;
+  for (int i = tid; i < 16 * nmi * KB; i += kThreads) {
+    const int r = i / KB, kb = i - r * KB;
+    s_xs[i] = xs[static_cast<int64_t>(s_row[r]) * KB + kb];
   }
-  const float* sw_gate = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + n0 / kKB) * KB;
-  const float* sw_up = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + n0) / kKB) * KB;
+  {
+    // Weight scales of the gate and up rows: one 128-row block each.
+    const float* sg = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + c0 / kKB) * KB;
+    const float* su = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
+    for (int i = tid; i < 2 * KB; i += kThreads) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
+  }
+  __syncthreads();
 
-  f32x4 acc[4][4];  // [row subtile][gate t0, gate t1, up t0, up t1]
+  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
+  const int64_t n = c0 + 16 * ch + j;
+  const uint8_t* brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
+  const uint8_t* arow[4];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int si = 0; si < 4; ++si) acc[mi][si] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mi = 0; mi < 4; ++mi) arow[mi] = xq + static_cast<int64_t>(s_row[16 * mi + j]) * H + 32 * q;
 
-  u32x4 bnext[4][2];
+  f32x4 acc[4][2];
 #pragma unroll
-  for (int si = 0; si < 4; ++si) load32(wrow[si], bnext[si]);
-  for (int kb = 0; kb < KB; ++kb) {
-    __syncthreads();  // the previous K block's LDS rows are consumed
-    stage_a(xq, xs, H, KB, s_row, kb, s_a, s_sa);
-    u32x4 b[4][2];
+  for (int mi = 0; mi < 4; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // A and B of the next K block are requested before the current one is
+  // multiplied (all A rows unconditionally: padding rows point at a live
+  // row), so the in-order load counter never makes the MFMAs wait for them.
+  u32x4 a[2][4][2], b[2][2][2];
+  auto load = [&](int buf, int kb) {
 #pragma unroll
-    for (int si = 0; si < 4; ++si) {
-      b[si][0] = bnext[si][0];
-      b[si][1] = bnext[si][1];
-    }
-    if (kb + 1 < KB) {
+    for (int si = 0; si < 2; ++si) load32(brow[si] + kb * kKB, b[buf][si]);
 #pragma unroll
-      for (int si = 0; si < 4; ++si) load32(wrow[si] + (kb + 1) * kKB, bnext[si]);
-    }
-    const float sg = sw_gate[kb], su = sw_up[kb];
-    __syncthreads();
+    for (int mi = 0; mi < 4; ++mi) load32(arow[mi] + kb * kKB, a[buf][mi]);
+  };
+  auto compute = [&](int buf, int kb) {
+    const float g = s_sw[0][kb], u = s_sw[1][kb];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      u32x4 a[2];
-      read_a(s_a, 16 * mi + j, q, a);
+      if (mi >= nmi) continue;
       float sa[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sa[r] = s_sa[16 * mi + 4 * q + r];
+      for (int r = 0; r < 4; ++r) sa[r] = s_xs[(16 * mi + 4 * q + r) * KB + kb];
 #pragma unroll
-      for (int si = 0; si < 4; ++si) {
-        const f32x4 part = mfma_k128(a, b[si]);
-        const float swv = si < 2 ? sg : su;
+      for (int si = 0; si < 2; ++si) {
+        const f32x4 part = mfma_k128(a[buf][mi], b[buf][si]);
+        const float sw = si == 0 ? g : u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][si][r] += part[r] * sa[r] * swv;
+        for (int r = 0; r < 4; ++r) acc[mi][si][r] += part[r] * sa[r] * sw;
       }
+    }
+  };
+  // Branch-free prefetch: the block index is clamped at the wave's last
+  // block, so every iteration issues the same loads.
+  const int nk = (KB - kh + 1) / 2;  // K blocks kh, kh + 2, ... below KB
+  if (nk > 0) {
+    auto kidx = [&](int i) { return kh + 2 * (i < nk ? i : nk - 1); };
+    load(0, kidx(0));
+    for (int i = 0; i < nk; i += 2) {
+      load(1, kidx(i + 1));
+      compute(0, kidx(i));
+      load(0, kidx(i + 2));
+      if (i + 1 < nk) compute(1, kidx(i + 1));
     }
   }
 
-  // a = bf16(silu(bf16 gate) * bf16 up); row amax over the 128 columns
-  // (16 lanes x 2 subtiles per wave, then the 4 waves); fp8 quantisation.
-  float av[4][2][4];
+  if (kh == 1) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float g = bf16_round(acc[mi][t][r]);
-        const float u = bf16_round(acc[mi][2 + t][r]);
-        av[mi][t][r] = bf16_round(g / (1.0f + expf(-g)) * u);
+    for (int mi = 0; mi < 4; ++mi)
+      if (mi < nmi) {
+        s_red[ch][mi][0][lane] = acc[mi][0];
+        s_red[ch][mi][1][lane] = acc[mi][1];
       }
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float m = fmaxf(fabsf(av[mi][0][r]), fabsf(av[mi][1][r]));
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
-      if (j == 0) s_amax[wave][16 * mi + 4 * q + r] = m;
-    }
-  __syncthreads();
-  if (tid < kBM) {
-    const float m = fmaxf(fmaxf(s_amax[0][tid], s_amax[1][tid]), fmaxf(s_amax[2][tid], s_amax[3][tid]));
-    s_sa[tid] = quant_scale(m);
   }
   __syncthreads();
+  uint16_t* s_o = reinterpret_cast<uint16_t*>(s_xs);  // [kBM][kC1] bf16
+  if (kh == 0) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi) {
+      if (mi >= nmi) continue;
+      const f32x4 gs = acc[mi][0] + s_red[ch][mi][0][lane];
+      const f32x4 us = acc[mi][1] + s_red[ch][mi][1][lane];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mi + 4 * q + r;
-      const float s = s_sa[row];
+      for (int r = 0; r < 4; ++r) {
+        const float g = bf16_round(gs[r]), u = bf16_round(us[r]);
+        const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+        float m = fabsf(a);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        s_q[row * kBN + 32 * wave + 16 * t + j] = static_cast<uint8_t>(to_fp8(clamp_fp8(av[mi][t][r] / s)));
+        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+        const int row = 16 * mi + 4 * q + r;
+        if (j == 0) s_m[ch][row] = m;
+        s_o[row * kC1 + 16 * ch + j] = static_cast<uint16_t>(bf16_bits(a));
+      }
     }
+  }
   __syncthreads();
   {
-    const int row = tid >> 2, part = tid & 3;
+    const int row = tid >> 2, part = tid & 3;  // 64 bytes per row: 4 threads x 16 bytes
     const int p = s_pair[row];
     if (p >= 0) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(s_q + row * kBN + part * 32);
-      u32x4* dst = reinterpret_cast<u32x4*>(act + static_cast<int64_t>(p) * I + n0 + part * 32);
-      dst[0] = src[0];
-      dst[1] = src[1];
-      if (part == 0) acts[static_cast<int64_t>(p) * (I / kKB) + n0 / kKB] = s_sa[row];
+      *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + part * 8) =
+          *reinterpret_cast<const u32x4*>(s_o + row * kC1 + part * 8);
+      if (part == 0) work.amax32[static_cast<int64_t>(p) * (I / 32) + c0 / 32] = fmaxf(s_m[0][row], s_m[1][row]);
     }
   }
 }
 
+// The activations of one tile to fp8: per pair and 128-column group,
+// s = max(max |a|, 1e-10) / 448 and q = rne(clamp(a / s)). grid = (1, tile bound).
+__global__ void __launch_bounds__(kThreads) act_quant_kernel(int64_t I, const int32_t* __restrict__ offsets,
+                                                             const int32_t* __restrict__ pairs,
+                                                             const int32_t* __restrict__ tiles, Work work) {
+  __shared__ int s_p[kBM];
+  __shared__ float s_s[kBM * kMaxKB];
+  Tile tile;
+  if (!load_tile(tiles, offsets, tile)) return;
+  const int tid = threadIdx.x;
+  const int G = static_cast<int>(I / kKB);
+  if (tid < tile.count) s_p[tid] = pairs[tile.first + tid];
+  __syncthreads();
+  for (int i = tid; i < tile.count * G; i += kThreads) {
+    const int r = i / G, g = i - r * G;
+    const int64_t p = s_p[r];
+    const float* m = work.amax32 + p * (I / 32) + 4 * g;
+    const float s = quant_scale(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3])));
+    s_s[i] = s;
+    work.acts[p * G + g] = s;
+  }
+  __syncthreads();
+  const int per_row = static_cast<int>(I / 8);
+  for (int i = tid; i < tile.count * per_row; i += kThreads) {
+    const int r = i / per_row, c = (i - r * per_row) * 8;
+    const int64_t p = s_p[r];
+    const float s = s_s[r * G + c / kKB];
+    const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c);
+    uint32_t q0 = 0, q1 = 0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      q0 |= to_fp8(clamp_fp8(bf16_value(v[k] & 0xffffu) / s)) << (16 * k);
+      q0 |= to_fp8(clamp_fp8(bf16_value(v[k] >> 16) / s)) << (16 * k + 8);
+      q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + k] & 0xffffu) / s)) << (16 * k);
+      q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + k] >> 16) / s)) << (16 * k + 8);
+    }
+    *reinterpret_cast<uint2*>(work.act + p * I + c) = make_uint2(q0, q1);
+  }
+}
+
 // GEMM2: down projection of 128 output columns times the routed weight,
-// bf16 rows per pair. grid = (H / 128, tile bound).
-__global__ void __launch_bounds__(kThreads) gemm2_kernel(const uint8_t* __restrict__ act, const float* __restrict__ acts,
-                                                         int64_t H, int64_t I, const float* __restrict__ topk_weight,
+// bf16 rows per pair; each wave owns 32 columns and reads the tile's fp8
+// activations straight from memory (shared through the cache), one K block
+// ahead. grid = (H / 128, tile bound).
+__global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, const float* __restrict__ topk_weight,
                                                          const uint8_t* __restrict__ w2,
                                                          const float* __restrict__ w2_scale,
                                                          const int32_t* __restrict__ offsets,
                                                          const int32_t* __restrict__ pairs,
-                                                         const int32_t* __restrict__ tiles,
+                                                         const int32_t* __restrict__ tiles, Work work,
                                                          uint16_t* __restrict__ out) {
   __shared__ int s_row[kBM];
   __shared__ int s_pair[kBM];
-  __shared__ float s_sa[kBM];
-  __shared__ __attribute__((aligned(16))) uint8_t s_a[kBM * kRowPitch];
+  __shared__ float s_as[kBM * kMaxKB];
+  __shared__ float s_w[kBM];
+  __shared__ float s_sw[kMaxKB];        // weight scales per K block of this 128-column block
   __shared__ __attribute__((aligned(16))) uint16_t s_o[kBM * kBN];
 
   Tile tile;
@@ -384,15 +451,25 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(const uint8_t* __restri
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(I / kKB);
+  const int nmi = (tile.count + 15) >> 4;
 
   tile_rows(tile, pairs, 1, s_pair, s_row);
   __syncthreads();
+  for (int i = tid; i < 16 * nmi * KB; i += kThreads) {
+    const int r = i / KB, kb = i - r * KB;
+    s_as[i] = work.acts[static_cast<int64_t>(s_row[r]) * KB + kb];
+  }
+  if (tid < kBM) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
+  if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
+  __syncthreads();
 
-  const uint8_t* wrow[2];
   const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
+  const uint8_t* brow[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) wrow[t] = wslot + static_cast<int64_t>(n0 + 32 * wave + 16 * t + j) * I + 32 * q;
-  const float* sw = w2_scale + (static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB;
+  for (int t = 0; t < 2; ++t) brow[t] = wslot + static_cast<int64_t>(n0 + 32 * wave + 16 * t + j) * I + 32 * q;
+  const uint8_t* arow[4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) arow[mi] = work.act + static_cast<int64_t>(s_row[16 * mi + j]) * I + 32 * q;
 
   f32x4 acc[4][2];
 #pragma unroll
@@ -400,58 +477,54 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(const uint8_t* __restri
 #pragma unroll
     for (int t = 0; t < 2; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  u32x4 bnext[2][2];
+  u32x4 a[2][4][2], b[2][2][2];
+  auto load = [&](int buf, int kb) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) load32(wrow[t], bnext[t]);
-  for (int kb = 0; kb < KB; ++kb) {
-    __syncthreads();
-    stage_a(act, acts, I, KB, s_row, kb, s_a, s_sa);
-    u32x4 b[2][2];
+    for (int t = 0; t < 2; ++t) load32(brow[t] + kb * kKB, b[buf][t]);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      b[t][0] = bnext[t][0];
-      b[t][1] = bnext[t][1];
-    }
-    if (kb + 1 < KB) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t) load32(wrow[t] + (kb + 1) * kKB, bnext[t]);
-    }
-    const float swv = sw[kb];
-    __syncthreads();
+    for (int mi = 0; mi < 4; ++mi) load32(arow[mi] + kb * kKB, a[buf][mi]);
+  };
+  auto compute = [&](int buf, int kb) {
+    const float w = s_sw[kb];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      u32x4 a[2];
-      read_a(s_a, 16 * mi + j, q, a);
+      if (mi >= nmi) continue;
       float sa[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sa[r] = s_sa[16 * mi + 4 * q + r];
+      for (int r = 0; r < 4; ++r) sa[r] = s_as[(16 * mi + 4 * q + r) * KB + kb];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const f32x4 part = mfma_k128(a, b[t]);
+        const f32x4 part = mfma_k128(a[buf][mi], b[buf][t]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][t][r] += part[r] * sa[r] * swv;
+        for (int r = 0; r < 4; ++r) acc[mi][t][r] += part[r] * sa[r] * w;
       }
     }
+  };
+  auto kidx = [&](int i) { return i < KB ? i : KB - 1; };
+  load(0, 0);
+  for (int i = 0; i < KB; i += 2) {
+    load(1, kidx(i + 1));
+    compute(0, i);
+    load(0, kidx(i + 2));
+    if (i + 1 < KB) compute(1, i + 1);
   }
 
-  __syncthreads();  // s_sa is reused for the routed weights
-  if (tid < kBM) s_sa[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
-  __syncthreads();
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) {
+    if (mi >= nmi) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * mi + 4 * q + r;
-      const float wgt = s_sa[row];
+      const float wgt = s_w[row];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         s_o[row * kBN + 32 * wave + 16 * t + j] = static_cast<uint16_t>(bf16_bits(acc[mi][t][r] * wgt));
     }
+  }
   __syncthreads();
   // 256 bytes per row: 16 threads x 16 bytes, 16 rows per pass.
-  for (int row = tid >> 4; row < kBM; row += kThreads / 16) {
+  for (int row = tid >> 4; row < tile.count; row += kThreads / 16) {
     const int p = s_pair[row];
-    if (p < 0) continue;
     const int col = (tid & 15) * 8;
     *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
         *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
@@ -515,35 +588,51 @@ int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T, int64_t t
              kMaxRouteSlots);
   XP_REQUIRE(num_experts >= 1 && num_experts <= INT32_MAX, "xp_moe_route: %lld experts", (long long)num_experts);
   XP_REQUIRE(expert_map && offsets && pairs && tiles && (T == 0 || topk_ids), "xp_moe_route: null argument");
-  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, as_stream(stream), topk_ids, topk_elem_bytes,
+  const size_t lds = static_cast<size_t>(kRouteThreads / 64) * static_cast<size_t>(slots) * sizeof(int);
+  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), lds, as_stream(stream), topk_ids, topk_elem_bytes,
                      T * topk, expert_map, static_cast<int>(num_experts), static_cast<int>(slots), offsets, pairs,
                      tiles);
   return check_launch("route_kernel");
 }
 
+int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I) {
+  if (npairs <= 0 || I <= 0) return 0;
+  return work_layout(npairs, I, nullptr, nullptr);
+}
+
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
                    int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
-                   int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, uint8_t* act,
-                   float* acts, uint16_t* out, void* stream) {
-  XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0,
-             "xp_moe_experts: H=%lld and I=%lld must be positive multiples of %d", (long long)H, (long long)I, kBN);
+                   int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, void* work,
+                   int64_t work_bytes, uint16_t* out, void* stream) {
+  XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0 && H <= kKB * kMaxKB && I <= kKB * kMaxKB,
+             "xp_moe_experts: H=%lld and I=%lld must be multiples of %d, at most %d", (long long)H, (long long)I,
+             kBN, kKB * kMaxKB);
   XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX && slots >= 1 && slots <= kMaxRouteSlots,
              "xp_moe_experts: T=%lld, topk=%lld, slots=%lld", (long long)T, (long long)topk, (long long)slots);
   if (T == 0) return XP_OK;
-  XP_REQUIRE(xq && xs && topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && act &&
-                 acts && out,
+  XP_REQUIRE(xq && xs && topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && work && out,
              "xp_moe_experts: null argument");
-  XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(act) && aligned16(out),
-             "xp_moe_experts: fp8 and output buffers must be 16-byte aligned");
-  const int64_t bound = xp_moe_max_tiles(T * topk, slots);
+  XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(out) &&
+                 (reinterpret_cast<uintptr_t>(work) & 255) == 0,
+             "xp_moe_experts: fp8 and output buffers must be 16-byte aligned, the workspace 256-byte aligned");
+  const int64_t npairs = T * topk;
+  const int64_t need = xp_moe_workspace_bytes(npairs, I);
+  XP_REQUIRE(work_bytes >= need, "xp_moe_experts: workspace of %lld B, needs %lld", (long long)work_bytes,
+             (long long)need);
+  const int64_t bound = xp_moe_max_tiles(npairs, slots);
   XP_REQUIRE(bound <= 65535, "xp_moe_experts: %lld tiles exceed the launch grid", (long long)bound);
-  hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(I / kBN), static_cast<unsigned>(bound)), dim3(kThreads),
-                     0, as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles,
-                     act, acts);
-  const int rc = check_launch("gemm1_kernel");
+  Work w;
+  work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
+  const unsigned ty = static_cast<unsigned>(bound);
+  hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(I / kC1), ty), dim3(kThreads), 0, as_stream(stream), xq,
+                     xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
+  int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(H / kBN), static_cast<unsigned>(bound)), dim3(kThreads),
-                     0, as_stream(stream), act, acts, H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, out);
+  hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles, w);
+  rc = check_launch("act_quant_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(H / kBN), ty), dim3(kThreads), 0, as_stream(stream), H,
+                     I, topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
   return check_launch("gemm2_kernel");
 }
 

@@ -149,13 +149,13 @@ def run_experts(
         raise ValueError(f"routing addresses {routing.slots} slots, the slab has {S}")
     if contrib.dtype != torch.bfloat16 or tuple(contrib.shape) != (T * topk, H) or not contrib.is_contiguous():
         raise ValueError(f"contrib must be contiguous bfloat16 {(T * topk, H)}")
-    act = torch.empty((T * topk, I), dtype=torch.uint8, device=xq.device)
-    acts = torch.empty((T * topk, I // BLOCK), dtype=torch.float32, device=xq.device)
+    nbytes = int(nat.lib().xp_moe_workspace_bytes(T * topk, I))
+    work = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=xq.device)
     nat.call(
         "xp_moe_experts", _fp8_ptr(xq, "xq"), _f32(xs, "xs").data_ptr(), T, topk, tw.data_ptr(), H, I,
         _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(), _fp8_ptr(w2, "w2"),
         _f32(w2_scale, "w2_scale").data_ptr(), routing.slots, routing.offsets.data_ptr(),
-        routing.pairs.data_ptr(), routing.tiles.data_ptr(), act.data_ptr(), acts.data_ptr(), contrib.data_ptr(),
+        routing.pairs.data_ptr(), routing.tiles.data_ptr(), work.data_ptr(), nbytes, contrib.data_ptr(),
         nat.stream(),
     )
 

@@ -299,3 +299,19 @@ class Store:
         if self.fd_w is not None:
             offset = (layer * self.num_experts + expert) * self.record_bytes + self.offset[name]
             os.pwrite(self.fd_w, memoryview(words), offset)
+
+    def write_raw_rows(self, layer: int, name: str, rows: torch.Tensor) -> None:
+        """Put experts 0..n-1 of ``layer`` in one copy: an uncompressed tier without a paging file.
+
+        ``rows`` is ``(n, row_bytes)`` (any device, any 1-byte dtype) with
+        n <= R; RAM-tier slot e of the layer receives expert e, as ``write``
+        would place it. Used to load synthetic models quickly.
+        """
+        if self.compress or self.fd_w is not None:
+            raise ValueError("write_raw_rows needs an uncompressed tier without a paging file; use write")
+        rows = rows.contiguous().view(torch.uint8)
+        n = rows.shape[0]
+        if rows.dim() != 2 or rows.shape[1] != self.row_bytes[name] or n > self.ram_slots:
+            raise ValueError(f"{name}: rows must be (n <= {self.ram_slots}, {self.row_bytes[name]}) bytes")
+        base = layer * self.ram_slots
+        self.pinned[name][base : base + n].view(torch.uint8).copy_(rows)
