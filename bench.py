@@ -417,11 +417,13 @@ def quantised_experts(E: int, H: int, I: int, g, dev):
 class QwenMoeDecoder:
     """Random-init Qwen3-MoE-shaped decoder (bf16 non-expert weights) whose experts are paged.
 
-    Per layer: RMSNorm, fused QKV projection, per-head q/k RMSNorm, RoPE,
-    GQA attention over a static KV cache with a position mask, output
-    projection, RMSNorm, router (softmax over the logits of the traced
-    ids), the paged expert FFN, residuals. Final RMSNorm, LM head, greedy
-    next token. Shapes are static, so one step is captured in a hipGraph.
+    Per layer: RMSNorm, fused QKV projection, per-head q/k RMSNorm, rotary
+    embedding, GQA attention over a static KV cache with a position mask,
+    output projection added to the residual, RMSNorm, router (softmax over
+    the logits of the traced ids), the paged expert FFN, residual. Final
+    RMSNorm, LM head, greedy next token. Shapes are static, so one step is
+    captured in a hipGraph; the non-expert part is written with few, fused
+    torch launches (about 20 per layer).
     """
 
     def __init__(self, dev, pager, layers, trace, ctx: int):
@@ -434,12 +436,11 @@ class QwenMoeDecoder:
         rnd = lambda *shape: (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
         L = len(layers)
         self.w_qkv = [rnd((nh + 2 * kv) * hd, H) for _ in range(L)]
-        self.w_o = [rnd(H, nh * hd) for _ in range(L)]
+        self.w_o_t = [rnd(nh * hd, H) for _ in range(L)]        # output projection, stored (in, out)
         self.w_router = [rnd(c["experts"], H) for _ in range(L)]
         self.ln1 = [torch.ones(H, **bf) for _ in range(L)]
         self.ln2 = [torch.ones(H, **bf) for _ in range(L)]
-        self.qn = [torch.ones(hd, **bf) for _ in range(L)]
-        self.kn = [torch.ones(hd, **bf) for _ in range(L)]
+        self.qkn = [torch.ones((nh + kv, hd), **bf) for _ in range(L)]  # q-norm rows, then k-norm rows
         self.embed = rnd(c["vocab"], H)
         self.lm_head = rnd(c["vocab"], H)
         self.norm = torch.ones(H, **bf)
@@ -447,52 +448,41 @@ class QwenMoeDecoder:
         self.vcache = torch.zeros((L, kv, ctx, hd), **bf)
         inv = 1.0 / (c["rope_theta"] ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
         ang = torch.arange(ctx, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
-        self.cos, self.sin = ang.cos(), ang.sin()
+        self.freqs = torch.polar(torch.ones_like(ang), ang)   # (ctx, hd/2) complex64
         self.trace = trace                                   # (steps, L, k) int32 on the device
         self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
         self.pos = torch.zeros((1,), dtype=torch.int64, device=dev)
         self.token = torch.zeros((1,), dtype=torch.int64, device=dev)
         self.positions = torch.arange(ctx, device=dev)
-
-    def _rms(self, x, w):
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + QWEN["eps"])).to(torch.bfloat16) * w
-
-    def _rope(self, x):  # x (heads, hd) bf16
-        cos = self.cos.index_select(0, self.pos)  # (1, hd/2)
-        sin = self.sin.index_select(0, self.pos)
-        xf = x.float()
-        a, b = xf[:, 0::2], xf[:, 1::2]
-        out = torch.empty_like(xf)
-        out[:, 0::2] = a * cos - b * sin
-        out[:, 1::2] = a * sin + b * cos
-        return out.to(torch.bfloat16)
+        self.neg = torch.full((ctx,), float("-inf"), device=dev)
+        self.zero = torch.zeros((ctx,), device=dev)
 
     def forward_step(self):
-        nh, kv, hd, H = self.nh, self.kv, self.hd, self.H
-        ids_all = self.trace.index_select(0, self.step).squeeze(0)  # (L, k)
-        h = self.embed.index_select(0, self.token)                  # (1, H)
-        mask = self.positions <= self.pos
+        F = torch.nn.functional
+        nh, kv, hd, H, eps = self.nh, self.kv, self.hd, self.H, QWEN["eps"]
+        ids_all = self.trace.index_select(0, self.step).squeeze(0).long()  # (L, k)
+        h = self.embed.index_select(0, self.token)                         # (1, H)
+        freqs = self.freqs.index_select(0, self.pos)                        # (1, hd/2)
+        bias = torch.where(self.positions <= self.pos, self.zero, self.neg)  # attention mask for this step
+        scale = hd ** -0.5
         for l, layer in enumerate(self.layers):
-            x = self._rms(h, self.ln1[l])
-            qkv = torch.nn.functional.linear(x, self.w_qkv[l])[0]
-            q = self._rope(self._rms(qkv[: nh * hd].view(nh, hd), self.qn[l]))
-            k = self._rope(self._rms(qkv[nh * hd : (nh + kv) * hd].view(kv, hd), self.kn[l]))
+            x = F.rms_norm(h, (H,), self.ln1[l], eps)
+            qkv = F.linear(x, self.w_qkv[l])[0]
+            qk = F.rms_norm(qkv[: (nh + kv) * hd].view(nh + kv, hd), (hd,), None, eps) * self.qkn[l]
+            qk = torch.view_as_real(torch.view_as_complex(qk.float().view(nh + kv, hd // 2, 2)) * freqs)
+            qk = qk.reshape(nh + kv, hd).to(torch.bfloat16)
             v = qkv[(nh + kv) * hd :].view(kv, hd)
-            self.kcache[l].index_copy_(2, self.pos, k.unsqueeze(2))
+            self.kcache[l].index_copy_(2, self.pos, qk[nh:].unsqueeze(2))
             self.vcache[l].index_copy_(1, self.pos, v.unsqueeze(1))
-            qg = q.view(kv, nh // kv, hd)
-            scores = torch.matmul(qg, self.kcache[l]).float() * (hd ** -0.5)  # (kv, g, ctx)
-            scores = scores.masked_fill(~mask, float("-inf"))
-            probs = torch.softmax(scores, dim=-1).to(torch.bfloat16)
-            attn = torch.matmul(probs, self.vcache[l]).reshape(1, nh * hd)
-            h = h + torch.nn.functional.linear(attn, self.w_o[l])
-            x2 = self._rms(h, self.ln2[l])
-            logits = torch.nn.functional.linear(x2, self.w_router[l]).float()
-            ids = ids_all[l : l + 1]                                         # (1, k) traced routing
-            w = torch.softmax(logits.gather(1, ids.long()), dim=-1)          # renormalised over the top-k
+            scores = torch.matmul(qk[:nh].view(kv, nh // kv, hd), self.kcache[l])  # (kv, g, ctx)
+            probs = torch.softmax(torch.add(bias, scores, alpha=scale), dim=-1).to(torch.bfloat16)
+            attn = torch.matmul(probs, self.vcache[l]).view(1, nh * hd)
+            h = torch.addmm(h, attn, self.w_o_t[l])
+            x2 = F.rms_norm(h, (H,), self.ln2[l], eps)
+            ids = ids_all[l : l + 1]                                        # (1, k) traced routing
+            w = torch.softmax(F.linear(x2, self.w_router[l]).gather(1, ids).float(), dim=-1)
             h = h + layer.forward(x2, w, ids)
-        logits = torch.nn.functional.linear(self._rms(h, self.norm), self.lm_head)
+        logits = F.linear(F.rms_norm(h, (H,), self.norm, eps), self.lm_head)
         # Greedy token in two single-workgroup reductions (vocab = 1187 x 128).
         best, idx = logits.view(-1, 128).max(dim=1)
         row = best.argmax().view(1)
@@ -554,6 +544,34 @@ def bench_model_decode(args, dev):
     after = [lay.hit_rates() for lay in layers]
     vh = sum(a[0] - b[0] for a, b in zip(after, before))
     vm = sum(a[1] - b[1] for a, b in zip(after, before))
+    # The paging path alone on the continuing trace: acquire, gather, expert
+    # FFN and top-k sum of the 40 layers in one graph (fixed hidden states).
+    x = torch.randn((1, H), device=dev).to(torch.bfloat16)
+    wk = torch.full((1, k), 1.0 / k, device=dev)
+    pstep = torch.zeros((1,), dtype=torch.int64, device=dev)
+    ptrace = torch.from_numpy(zipf_trace(np.random.default_rng(7), warm + steps, L, E, k, 1.1, 0.7)).to(dev)
+
+    def pager_step():
+        ids_all = ptrace.index_select(0, pstep).squeeze(0).long()
+        for l, layer in enumerate(layers):
+            layer.forward(x, wk, ids_all[l : l + 1])
+        pstep.add_(1)
+
+    with torch.cuda.stream(s):
+        pager_step()
+        pgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(pgraph, stream=s):
+            pager_step()
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(max(0, warm - 1)):
+        pgraph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        pgraph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    pager_ms = e0.elapsed_time(e1) / steps
     out = {
         "workload": f"{L}-layer decode trace, {E} experts x 3 MiB, 32 cache slots, all experts in a raw "
                     f"pinned RAM tier, batch 1, top-{k}, Zipf(1.1) with 0.7 reuse, {steps} steps in one "
@@ -563,6 +581,7 @@ def bench_model_decode(args, dev):
         "us_per_layer": round(ms * 1e3 / L, 2),
         "vram_hit_rate": round(vh / max(1, vh + vm), 4),
         "misses_per_layer_step": round(vm / (L * steps), 3),
+        "paging_path_us_per_layer": round(pager_ms * 1e3 / L, 2),
         "steps": steps,
     }
     log(f"model decode: {out}")
