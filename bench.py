@@ -491,31 +491,43 @@ class QwenMoeDecoder:
         self.step.add_(1)
 
 
-def bench_model_decode(args, dev):
-    """Decode trace: 40 MoE layers x 256 experts x 3 MiB, 32 cache slots, every expert in a raw pinned
-    RAM tier, batch 1, top-8, Zipf(1.1) routing with 70% reuse of the previous step's set per layer.
-    One decode step of the whole model is one hipGraph replay."""
+def build_paged_model(dev, settings, keep_weights: bool = False):
+    """The 40 MoE layers of 256 synthetic block-fp8 experts behind one pager (per-layer seeds)."""
     from vllm_expert_pager import pager as pg
 
     c = QWEN
-    L, E, H, I, k = c["layers"], c["experts"], c["hidden"], c["intermediate"], c["topk"]
-    steps, warm = args.decode_steps, args.decode_warmup
+    L, E, H, I = c["layers"], c["experts"], c["hidden"], c["intermediate"]
     t0 = time.time()
-    settings = pg.Settings(cache_slots=32, ram_slots=None, compress="off", working_rows=64, log_interval=0)
     pager = pg.Pager(settings, L, E, H, I, dev)
-    layers = []
-    g = torch.Generator(device=dev).manual_seed(3)
+    layers, weights = [], []
     for l in range(L):
+        g = torch.Generator(device=dev).manual_seed(1000 + l)
         layer = pager.add_layer()
         w13, w13s, w2, w2s = quantised_experts(E, H, I, g, dev)
-        pager.store.write_raw_rows(layer.layer, "w13_weight", w13.view(E, -1))
-        pager.store.write_raw_rows(layer.layer, "w2_weight", w2.view(E, -1))
-        del w13, w2
+        pager.store.write_rows(layer.layer, "w13_weight", w13.view(E, -1))
+        pager.store.write_rows(layer.layer, "w2_weight", w2.view(E, -1))
         layer.setup({pg.SCALES[0]: w13s, pg.SCALES[1]: w2s})
         layers.append(layer)
+        if keep_weights:
+            weights.append((w13, w13s, w2, w2s))
+        del w13, w2
+        if (l + 1) % 10 == 0:
+            log(f"model: {l + 1}/{L} layers written ({time.time() - t0:.1f}s)")
     torch.cuda.synchronize()
-    log(f"model: {L} layers x {E} experts loaded in {time.time() - t0:.1f}s "
-        f"(RAM tier {pager.store.rows * pager.store.record_bytes / 2**30:.1f} GiB pinned)")
+    st = pager.store
+    log(f"model: {L} layers x {E} experts loaded in {time.time() - t0:.1f}s (RAM tier "
+        f"{st.rows * st.record_bytes / 2**30:.1f} GiB pinned, {'compressed' if st.compress else 'raw'}"
+        f"{', paging file ' + st.path if st.path else ''})")
+    return pager, layers, weights
+
+
+def decode_trace(args, dev, pager, layers, label: str) -> dict:
+    """Run the Zipf(1.1)/0.7-reuse decode trace through a captured 40-layer step; tok/s, hit rates,
+    and the paging path alone per layer."""
+    c = QWEN
+    L, E, H, k = c["layers"], c["experts"], c["hidden"], c["topk"]
+    steps, warm = args.decode_steps, args.decode_warmup
+    store = pager.store
     rng = np.random.default_rng(2025)
     trace = torch.from_numpy(zipf_trace(rng, warm + steps, L, E, k, 1.1, 0.7)).to(dev)
     model = QwenMoeDecoder(dev, pager, layers, trace, ctx=warm + steps + 1)
@@ -534,6 +546,7 @@ def bench_model_decode(args, dev):
         graph.replay()
     torch.cuda.synchronize()
     before = [lay.hit_rates() for lay in layers]
+    ssd0 = (store.fetches, store.reads, store.io_seconds) if store.path else None
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -542,10 +555,13 @@ def bench_model_decode(args, dev):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     after = [lay.hit_rates() for lay in layers]
-    vh = sum(a[0] - b[0] for a, b in zip(after, before))
-    vm = sum(a[1] - b[1] for a, b in zip(after, before))
-    # The paging path alone on the continuing trace: acquire, gather, expert
-    # FFN and top-k sum of the 40 layers in one graph (fixed hidden states).
+    d = [sum(a[i] - b[i] for a, b in zip(after, before)) for i in range(4)]
+    ssd = None
+    if ssd0 is not None:
+        ssd = {"fetches": store.fetches - ssd0[0], "reads": store.reads - ssd0[1],
+               "io_seconds": round(store.io_seconds - ssd0[2], 4), "failed": store.failed}
+    # The paging path alone on a continuing trace: acquire, gather (+ SSD
+    # fetch, expansion), expert FFN and top-k sum of the 40 layers in one graph.
     x = torch.randn((1, H), device=dev).to(torch.bfloat16)
     wk = torch.full((1, k), 1.0 / k, device=dev)
     pstep = torch.zeros((1,), dtype=torch.int64, device=dev)
@@ -573,20 +589,106 @@ def bench_model_decode(args, dev):
     torch.cuda.synchronize()
     pager_ms = e0.elapsed_time(e1) / steps
     out = {
-        "workload": f"{L}-layer decode trace, {E} experts x 3 MiB, 32 cache slots, all experts in a raw "
-                    f"pinned RAM tier, batch 1, top-{k}, Zipf(1.1) with 0.7 reuse, {steps} steps in one "
-                    "captured hipGraph per step",
+        "workload": label,
         "tok_s": round(1e3 / ms, 2),
         "ms_per_token": round(ms, 4),
         "us_per_layer": round(ms * 1e3 / L, 2),
-        "vram_hit_rate": round(vh / max(1, vh + vm), 4),
-        "misses_per_layer_step": round(vm / (L * steps), 3),
+        "vram_hit_rate": round(d[0] / max(1, d[0] + d[1]), 4),
+        "ram_hit_rate": round(d[2] / max(1, d[2] + d[3]), 4),
+        "misses_per_layer_step": round(d[1] / (L * steps), 3),
         "paging_path_us_per_layer": round(pager_ms * 1e3 / L, 2),
         "steps": steps,
     }
-    log(f"model decode: {out}")
-    pager.close()
+    if ssd is not None:
+        out["ssd"] = ssd
+    log(f"decode trace: {out}")
     return out
+
+
+def bench_model_decode(args, dev):
+    """Decode trace: 40 MoE layers x 256 experts x 3 MiB, 32 cache slots, every expert in a raw pinned
+    RAM tier, batch 1, top-8, Zipf(1.1) routing with 70% reuse of the previous step's set per layer.
+    One decode step of the whole model is one hipGraph replay."""
+    from vllm_expert_pager import pager as pg
+
+    settings = pg.Settings(cache_slots=32, ram_slots=None, compress="off", working_rows=64, log_interval=0)
+    pager, layers, _ = build_paged_model(dev, settings)
+    try:
+        return decode_trace(args, dev, pager, layers,
+                            "40-layer decode trace, 256 experts x 3 MiB, 32 cache slots, all experts in a raw "
+                            f"pinned RAM tier, batch 1, top-8, Zipf(1.1) with 0.7 reuse, {args.decode_steps} "
+                            "steps in one captured hipGraph per step")
+    finally:
+        pager.close()
+
+
+def bench_tiered(args, dev):
+    """The compressed tier: 40 layers x 256 experts, 32 cache slots, 128 RAM slots holding rows
+    compressed at pitch 0.89, the rest in a paging file read with O_DIRECT by the host server.
+
+    Prefill: one 2048-token prompt (hidden states bf16 N(0,1), top-8 of random logits, softmax
+    weights), every layer through the 64-row working slab in chunks; each layer's output is
+    checked bit for bit against a one-shot run over all its experts. Then the decode trace."""
+    from vllm_expert_pager import moe
+    from vllm_expert_pager import pager as pg
+
+    c = QWEN
+    L, E, H, k = c["layers"], c["experts"], c["hidden"], c["topk"]
+    T = args.prefill_tokens
+    path = os.path.join(args.paging_dir, f"xp_paging_{os.getpid()}.bin")
+    settings = pg.Settings(cache_slots=32, ram_slots=128, ssd_path=path, compress="on", pitch_ratio=0.89,
+                           working_rows=64, log_interval=0)
+    pager, layers, weights = build_paged_model(dev, settings, keep_weights=True)
+    store = pager.store
+    try:
+        g = torch.Generator(device=dev).manual_seed(77)
+        xs, ws, ids = [], [], []
+        for l in range(L):
+            xs.append(torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16))
+            top, i = torch.randn((T, E), generator=g, device=dev).topk(k, dim=1)
+            ws.append(torch.softmax(top, dim=1).float().contiguous())
+            ids.append(i)
+        torch.cuda.synchronize()
+        f0, r0, io0 = store.fetches, store.reads, store.io_seconds
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        outs = [layers[l].forward(xs[l], ws[l], ids[l]) for l in range(L)]
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = e0.elapsed_time(e1)
+        exact = sum(
+            bool(torch.equal(outs[l].view(torch.int16), moe.fused_moe(xs[l], ws[l], ids[l], *weights[l]).view(torch.int16)))
+            for l in range(L)
+        )
+        prefill = {
+            "workload": f"40-layer prefill of one {T}-token prompt (bf16 N(0,1) hidden states, top-8 of 256 "
+                        "experts, softmax weights), 32 cache slots, 64 working rows, 128 compressed RAM slots, "
+                        "the other experts read from the paging file",
+            "ms": round(ms, 2),
+            "wall_s": round(wall, 3),
+            "ms_per_layer": round(ms / L, 3),
+            "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "ssd_fetches": store.fetches - f0,
+            "ssd_reads": store.reads - r0,
+            "ssd_io_seconds": round(store.io_seconds - io0, 3),
+            "layers_bit_exact_vs_one_shot": f"{exact}/{L}",
+        }
+        log(f"prefill: {prefill}")
+        if exact != L:
+            raise SystemExit("chunked prefill differs from the one-shot run")
+        del xs, ws, ids, outs, weights
+        decode = decode_trace(args, dev, pager, layers,
+                              "40-layer decode trace, 256 experts x 3 MiB, 32 cache slots, 128 RAM slots of "
+                              "rows compressed at pitch 0.89, the rest read from the paging file (O_DIRECT), "
+                              f"batch 1, top-8, Zipf(1.1) with 0.7 reuse, {args.decode_steps} steps in one "
+                              "captured hipGraph per step")
+        return {"prefill": prefill, "decode": decode}
+    finally:
+        pager.close()
+        if os.path.exists(path):
+            os.unlink(path)
 
 
 def main() -> None:
@@ -602,6 +704,11 @@ def main() -> None:
     ap.add_argument("--only-decode", action="store_true")
     ap.add_argument("--only-moe", action="store_true")
     ap.add_argument("--only-model", action="store_true")
+    ap.add_argument("--tiered", action="store_true",
+                    help="run only the compressed-tier legs (2048-token prefill, decode trace; needs ~30 GB "
+                         "of disk for the paging file)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--paging-dir", default=os.environ.get("TMPDIR", "/tmp"))
     ap.add_argument("--decode-steps", type=int, default=2000)
     ap.add_argument("--decode-warmup", type=int, default=20)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -626,6 +733,9 @@ def main() -> None:
         return
     if args.only_model:
         print(json.dumps({"model_decode": bench_model_decode(args, dev)}), flush=True)
+        return
+    if args.tiered:
+        print(json.dumps({"tiered": bench_tiered(args, dev)}), flush=True)
         return
     dec = bench_decode(args, dev, cores)
     if args.copy_probe_mib:

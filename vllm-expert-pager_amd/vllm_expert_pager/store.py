@@ -14,6 +14,7 @@ Layout, validation and messages follow the reference (store.py:351-599).
 
 from __future__ import annotations
 
+import concurrent.futures
 import ctypes
 import faulthandler
 import logging
@@ -300,18 +301,39 @@ class Store:
             offset = (layer * self.num_experts + expert) * self.record_bytes + self.offset[name]
             os.pwrite(self.fd_w, memoryview(words), offset)
 
-    def write_raw_rows(self, layer: int, name: str, rows: torch.Tensor) -> None:
-        """Put experts 0..n-1 of ``layer`` in one copy: an uncompressed tier without a paging file.
+    def write_rows(self, layer: int, name: str, rows: torch.Tensor, threads: int = 16) -> None:
+        """Put experts 0..n-1 of ``layer`` at once, as ``write`` would place each of them.
 
-        ``rows`` is ``(n, row_bytes)`` (any device, any 1-byte dtype) with
-        n <= R; RAM-tier slot e of the layer receives expert e, as ``write``
-        would place it. Used to load synthetic models quickly.
+        ``rows`` is ``(n, row_bytes)`` of any 1-byte dtype on any device.
+        Compressed tiers encode the rows in a thread pool (the encoder
+        releases the GIL); RAM-tier slots 0..min(n, R)-1 of the layer are
+        filled with one copy and each expert's record goes to the paging
+        file.
         """
-        if self.compress or self.fd_w is not None:
-            raise ValueError("write_raw_rows needs an uncompressed tier without a paging file; use write")
-        rows = rows.contiguous().view(torch.uint8)
-        n = rows.shape[0]
-        if rows.dim() != 2 or rows.shape[1] != self.row_bytes[name] or n > self.ram_slots:
-            raise ValueError(f"{name}: rows must be (n <= {self.ram_slots}, {self.row_bytes[name]}) bytes")
+        raw = rows.contiguous().view(torch.uint8)
+        if raw.dim() != 2 or raw.shape[1] != self.row_bytes[name] or raw.shape[0] > self.num_experts:
+            raise ValueError(f"{name}: rows must be (n <= {self.num_experts}, {self.row_bytes[name]}) bytes")
+        n = raw.shape[0]
+        r = min(n, self.ram_slots)
         base = layer * self.ram_slots
-        self.pinned[name][base : base + n].view(torch.uint8).copy_(rows)
+        if not self.compress and self.fd_w is None:
+            self.pinned[name][base : base + r].view(torch.uint8).copy_(raw[:r])
+            return
+        host = raw.cpu().numpy()
+        if self.compress:
+            words = np.zeros((n, self.pitch[name]), np.uint8)
+            luts = np.empty((n, codec.LUT_BYTES), np.uint8)
+
+            def encode(e: int) -> None:
+                codec.encode_into(host[e], words[e], luts[e])
+
+            with concurrent.futures.ThreadPoolExecutor(max(1, threads)) as pool:
+                list(pool.map(encode, range(n)))
+            self.lut[layer, :n, self.names.index(name)] = torch.from_numpy(luts).to(self.device)
+        else:
+            words = host
+        self.pinned[name][base : base + r].view(torch.uint8).copy_(torch.from_numpy(words[:r]))
+        if self.fd_w is not None:
+            for e in range(n):
+                offset = (layer * self.num_experts + e) * self.record_bytes + self.offset[name]
+                os.pwrite(self.fd_w, memoryview(words[e]), offset)
