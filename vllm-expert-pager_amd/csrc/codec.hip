@@ -11,11 +11,11 @@
 // (symbol index, lane) word order.
 //
 // Memory: the group's Huffman words stream through a 256-word ring in LDS
-// (plus a 160-word mirror of its head, so a half-iteration's reads never
-// wrap), filled with coalesced 32-word loads issued one half-iteration (4
-// symbols) ahead of use; the
-// 512-entry LUT is split into a length table and a pre-shifted exponent
-// table in LDS; the sign/mantissa nibbles arrive as coalesced 32-bit words
+// (plus a 128-word mirror of its head, so an iteration's reads never wrap),
+// filled with coalesced 32-word loads issued one 8-symbol iteration ahead
+// of use; the
+// 512-entry LUT is a 16-bit table in LDS (length, pre-shifted exponent); the
+// sign/mantissa nibbles arrive as coalesced 32-bit words
 // (8 values each), prefetched an iteration ahead.
 #include "common.h"
 
@@ -27,8 +27,12 @@ constexpr int kChains = 2;                     // independent chunk streams per 
 constexpr int kGroupsPerWave = 2 * kChains;    // lanes 0-31 and 32-63 of each chain
 constexpr int kGroupsPerBlock = kGroupsPerWave * kThreads / 64;  // 16
 constexpr uint32_t kRing = 256;                // ring words per group
-constexpr uint32_t kHalf = 4;                  // symbols between ring maintenance
-constexpr uint32_t kAhead = kHalf * 32;        // words a half-iteration may consume
+constexpr uint32_t kHalf = 8;                  // symbols between ring maintenance (one nibble word)
+// Words a group may consume in kHalf symbols. A lane refills only when fewer
+// than LIMIT bits are left and then holds at least 32; a symbol takes at most
+// LIMIT bits, so its next refill is at least ceil((32 - LIMIT + 1) / LIMIT) = 3
+// symbols later: at most ceil(kHalf / 3) refills per lane in a half.
+constexpr uint32_t kAhead = 32 * ((kHalf + 2) / 3);
 constexpr uint32_t kMirror = kAhead + 32;      // reads of a half never wrap
 constexpr uint32_t kRingPad = kRing + kMirror;
 constexpr uint32_t kFetch = 32;                // words requested per half-iteration
@@ -138,32 +142,51 @@ __device__ __forceinline__ uint32_t lane_select(unsigned long long mask, uint32_
   return r;
 }
 
+// out |= (byte 1 of e) << 8k as one byte-select OR (byte k of out is zero).
+template <int K>
+__device__ __forceinline__ void or_byte(uint32_t& out, uint32_t e) {
+  if constexpr (K == 0)
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_0"
+        : "+v"(out) : "v"(e));
+  else if constexpr (K == 1)
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_1"
+        : "+v"(out) : "v"(e));
+  else if constexpr (K == 2)
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_2"
+        : "+v"(out) : "v"(e));
+  else
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_3"
+        : "+v"(out) : "v"(e));
+}
+
 // One symbol of one stream, without branches: every lane reads a ring word
-// at its refill address and keeps it only if it refills.
-__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& ab, uint32_t& out, int k,
-                                              uint32_t half_shift, const uint8_t* s_len, const uint8_t* s_sym) {
+// at its refill address and keeps it only if it refills. `low` is all ones
+// in the lower half-wave and zero in the upper one; s_lut holds
+// len | (symbol << 3) << 8 per 9-bit code.
+template <int K>
+__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& ab, uint32_t& out,
+                                              uint32_t low, uint32_t half_shift, const uint16_t* s_lut) {
   const bool refill = pos > 64u - kLimit;
   const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
-  const uint32_t c_lo = static_cast<uint32_t>(__popc(m_lo)), c_hi = static_cast<uint32_t>(__popc(m_hi));
-  // Refilling lanes below this one in its half: the wave-wide count, minus
-  // the lower half's refills for lanes of the upper half.
-  const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u)) -
-                         __builtin_amdgcn_ubfe(c_lo << 16, half_shift, 16u);
+  // Refilling lanes below this one in its half: for the upper half the
+  // lower half's count (all of m_lo) is masked off before counting m_hi.
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u) & low);
   const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(ab + 4u * below);
   const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
   const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
   pos = lane_select(mask, pos, pos - 32u);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
-  ab += __builtin_amdgcn_ubfe((c_lo << 2) | (c_hi << 18), half_shift, 16u);
+  const uint32_t counts = static_cast<uint32_t>(__popc(m_lo)) | (static_cast<uint32_t>(__popc(m_hi)) << 16);
+  ab += 4u * __builtin_amdgcn_ubfe(counts, half_shift, 16u);
   const uint32_t idx = static_cast<uint32_t>(buf >> (pos & 63u)) & (XP_LUT_BYTES - 1);
-  pos += s_len[idx];
-  out |= static_cast<uint32_t>(s_sym[idx]) << (8 * (k & 3));
+  const uint32_t e = s_lut[idx];
+  pos += e & 0xffu;
+  or_byte<K & 3>(out, e);
 }
 
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
-  __shared__ uint8_t s_len[XP_LUT_BYTES];
-  __shared__ uint8_t s_sym[XP_LUT_BYTES];
+  __shared__ uint16_t s_lut[XP_LUT_BYTES];
   __shared__ uint32_t s_ring[kGroupsPerBlock][kRingPad];
 
   const int j = blockIdx.x / a.blocks_per_row;
@@ -185,14 +208,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   const uint8_t* lut = a.lut + (e * a.num_names + name) * XP_LUT_BYTES;
   for (int i = tid; i < XP_LUT_BYTES; i += kThreads) {
     const uint32_t ent = lut[i];
-    s_len[i] = static_cast<uint8_t>(ent & 15u);
-    s_sym[i] = static_cast<uint8_t>((ent >> 4) << 3);
+    s_lut[i] = static_cast<uint16_t>((ent & 15u) | (((ent >> 4) << 3) << 8));
   }
 
   const int wave = tid >> 6, lane = tid & 63;
   const bool upper = lane >= 32;
   const uint32_t li = lane & 31;
   const uint32_t half_shift = upper ? 16u : 0u;
+  const uint32_t low = upper ? 0u : ~0u;
   const int G = nm.G;
   const int msteps = a.chunk / 8;
   const uint32_t* rec = reinterpret_cast<const uint32_t*>(nm.stg + int64_t(j) * nm.pitch);
@@ -271,15 +294,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
         ch[c].x_next = ch[c].nib[(m + 1 < msteps ? m + 1 : m) * 32];
         o[c] = nibble_template(x);
       }
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      {
         uint32_t ab[kChains];
 #pragma unroll
         for (int c = 0; c < kChains; ++c) {
           half_begin(ch[c], li);
           ab[c] = ch[c].ab0;
         }
-        if (u == 0 && half == 0 && m0 > 0) {
+        if (u == 0 && m0 > 0) {
 #pragma unroll
           for (int c = 0; c < kChains; ++c)
             if (valid[c]) {
@@ -290,15 +312,23 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int k = 0; k < static_cast<int>(kHalf); ++k) {
-#pragma unroll
-          for (int c = 0; c < kChains; ++c) {
-            if (half == 0)
-              decode_symbol(ch[c].buf, ch[c].pos, ab[c], o[c].x, k, half_shift, s_len, s_sym);
-            else
-              decode_symbol(ch[c].buf, ch[c].pos, ab[c], o[c].y, k, half_shift, s_len, s_sym);
-          }
+        for (int c = 0; c < kChains; ++c) {
+          decode_symbol<0>(ch[c].buf, ch[c].pos, ab[c], o[c].x, low, half_shift, s_lut);
         }
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<1>(ch[c].buf, ch[c].pos, ab[c], o[c].x, low, half_shift, s_lut);
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<2>(ch[c].buf, ch[c].pos, ab[c], o[c].x, low, half_shift, s_lut);
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<3>(ch[c].buf, ch[c].pos, ab[c], o[c].x, low, half_shift, s_lut);
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<0>(ch[c].buf, ch[c].pos, ab[c], o[c].y, low, half_shift, s_lut);
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<1>(ch[c].buf, ch[c].pos, ab[c], o[c].y, low, half_shift, s_lut);
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<2>(ch[c].buf, ch[c].pos, ab[c], o[c].y, low, half_shift, s_lut);
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) decode_symbol<3>(ch[c].buf, ch[c].pos, ab[c], o[c].y, low, half_shift, s_lut);
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int c = 0; c < kChains; ++c) half_end(ch[c], li, ab[c]);
