@@ -84,12 +84,65 @@ __device__ __forceinline__ void block_scan2(bool fa, bool fb, int* pa, int* pb, 
 // torch version reads `current` through a view of slot_of, table.py:95-118);
 // otherwise the fused kernel's value, the slot loaded before the update for
 // experts that did not miss (acquire.py:309-341). Both agree on needed experts.
+// The M smallest keys of key[0..S) in ascending order into order[], by one
+// wave: M rounds of a wave-wide minimum (keys are distinct: the slot is in
+// the low bits). Used when the misses are few.
+__device__ __forceinline__ void smallest_keys_wave(const uint64_t* key, int S, int M, int16_t* order) {
+  const int lane = threadIdx.x & 63;
+  constexpr int kPer = XP_MAX_SLOTS / 64;
+  uint64_t k[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int s = lane + 64 * i;
+    k[i] = s < S ? key[s] : ~0ull;
+  }
+  for (int r = 0; r < M; ++r) {
+    uint64_t m = k[0];
+#pragma unroll
+    for (int i = 1; i < kPer; ++i) m = k[i] < m ? k[i] : m;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint64_t o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(m), off, 64));
+      m = o < m ? o : m;
+    }
+    if (lane == 0) order[r] = static_cast<int16_t>(m & ((1u << kSlotBits) - 1));
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (k[i] == m) k[i] = ~0ull;
+  }
+}
+
+// One acquire on table `t` (table.py:75-128). `ids(k)` yields the k-th id of
+// the step. Writes the outputs that are non-null. The table arrays may be in
+// global memory or LDS (generic pointers). On return lds.fin holds slot_of
+// after the update for every expert.
+// slot_out: with slot_final, slot_of after the update for every expert (the
+// torch version reads `current` through a view of slot_of, table.py:95-118);
+// otherwise the fused kernel's value, the slot loaded before the update for
+// experts that did not miss (acquire.py:309-341). Both agree on needed experts.
 template <typename Ids>
 __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_t* map32,
                               int64_t* slot_out, int64_t* todo, bool count_refs, bool slot_final,
                               AcquireLds& lds) {
   const int tid = threadIdx.x;
   const int E = t.E, S = t.S;
+  constexpr int kPerE = XP_MAX_EXPERTS / kThreads;
+  constexpr int kPerS = XP_MAX_SLOTS / kThreads;
+
+  // Every read of the table is issued first, so the latencies overlap.
+  int64_t cur_r[kPerE], occ_r[kPerS], lu_r[kPerS];
+#pragma unroll
+  for (int i = 0; i < kPerE; ++i) {
+    const int e = tid + kThreads * i;
+    cur_r[i] = e < E ? t.slot_of[e] : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kPerS; ++i) {
+    const int s = tid + kThreads * i;
+    occ_r[i] = s < S ? t.expert_in[s] : -1;
+    lu_r[i] = s < S ? t.last_used[s] : 0;
+  }
+  const int64_t step = *t.step;
 
   for (int e = tid; e < E; e += kThreads) lds.need[e] = 0;
   __syncthreads();
@@ -98,29 +151,31 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
     if (id >= 0 && id < E) lds.need[id] = 1;  // same value for duplicates
   }
   __syncthreads();
-  const int64_t step = *t.step;
 
   // Victim keys: slots holding an expert needed this step are pushed to the
   // end (acquire.py:52-58, table.py:99-107). The slot number in the low bits
   // makes equal stamps order by slot, as the stable argsort does.
-  for (int s = tid; s < S; s += kThreads) {
-    int64_t occ = t.expert_in[s];
-    bool used = occ >= 0 && occ < E && lds.need[occ];
-    int64_t key = t.last_used[s] + (used ? kProtect : 0);
-    lds.key[s] = (static_cast<uint64_t>(key) << kSlotBits) | static_cast<uint64_t>(s);
-    lds.occ[s] = static_cast<int16_t>(occ < 0 ? -1 : occ);
+#pragma unroll
+  for (int i = 0; i < kPerS; ++i) {
+    const int s = tid + kThreads * i;
+    if (s < S) {
+      const int64_t occ = occ_r[i];
+      const bool used = occ >= 0 && occ < E && lds.need[occ];
+      const int64_t key = lu_r[i] + (used ? kProtect : 0);
+      lds.key[s] = (static_cast<uint64_t>(key) << kSlotBits) | static_cast<uint64_t>(s);
+      lds.occ[s] = static_cast<int16_t>(occ < 0 ? -1 : occ);
+    }
   }
 
   // Hits and misses; the rank of a miss is its ordinal in ascending expert id.
   int miss_base = 0, hit_total = 0;
-  for (int e0 = 0; e0 < E; e0 += kThreads) {
+#pragma unroll
+  for (int i = 0; i < kPerE; ++i) {
+    const int e0 = kThreads * i;
+    if (e0 >= E) break;  // uniform
     const int e = e0 + tid;
-    int64_t cur = -1;
-    bool n = false;
-    if (e < E) {
-      n = lds.need[e];
-      cur = t.slot_of[e];
-    }
+    const int64_t cur = cur_r[i];
+    const bool n = e < E && lds.need[e];
     const bool miss = n && cur < 0, hit = n && cur >= 0;
     int pm, ph, tm, th;
     block_scan2(miss, hit, &pm, &ph, &tm, &th, lds.wave_a, lds.wave_b);
@@ -135,12 +190,16 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
   const int M = miss_base;  // <= K <= S (checked on the host)
   __syncthreads();
 
-  // order[r] for r < M: the slot whose key has exactly r smaller keys.
-  for (int s = tid; s < S; s += kThreads) {
-    const uint64_t mine = lds.key[s];
-    int c = 0;
-    for (int s2 = 0; s2 < S; ++s2) c += lds.key[s2] < mine ? 1 : 0;
-    if (c < M) lds.order[c] = static_cast<int16_t>(s);
+  // order[r] for r < M: the slot with the r-th smallest key.
+  if (M <= 32) {
+    if (tid < 64) smallest_keys_wave(lds.key, S, M, lds.order);
+  } else {
+    for (int s = tid; s < S; s += kThreads) {
+      const uint64_t mine = lds.key[s];
+      int c = 0;
+      for (int s2 = 0; s2 < S; ++s2) c += lds.key[s2] < mine ? 1 : 0;
+      if (c < M) lds.order[c] = static_cast<int16_t>(s);
+    }
   }
   __syncthreads();
 

@@ -225,14 +225,21 @@ class PagedExperts:
             self.scale_rows,
             self.cache_rows[2:],
         )
-        # One launch publishes the SSD request and copies the experts that
-        # are in RAM while the host reads; then the ones read from SSD.
-        gather_rows(todo, dst_row, cached_row, src_row, base, *rows, fetch=(ssd_todo, layer, store))
-        if store.compress:
-            decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut, skip=ssd_todo)
-        gather_rows(ssd_todo, dst_row, cached_row, src_row, base, *rows)
-        if store.compress:
-            decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
+        if store.path is None:
+            # Every expert is in RAM (R = E): the RAM table always hits, so
+            # there is never an SSD read and one copy does it all.
+            gather_rows(todo, dst_row, cached_row, src_row, base, *rows)
+            if store.compress:
+                decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut)
+        else:
+            # One launch publishes the SSD request and copies the experts
+            # that are in RAM while the host reads; then the ones read from SSD.
+            gather_rows(todo, dst_row, cached_row, src_row, base, *rows, fetch=(ssd_todo, layer, store))
+            if store.compress:
+                decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut, skip=ssd_todo)
+            gather_rows(ssd_todo, dst_row, cached_row, src_row, base, *rows)
+            if store.compress:
+                decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
 
         xq, xs = moe.quant_tokens(x)
         contrib = self._contrib(topk_weights, x)

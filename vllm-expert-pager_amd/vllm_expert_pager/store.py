@@ -33,8 +33,20 @@ logger = logging.getLogger(f"vllm.{__name__}")
 
 # O_DIRECT alignment of rows, records and the pinned base (store.py:51-53).
 _ALIGN = 4096
-# Concurrent reads per request: the server thread and 7 workers (store.py:59-64).
+# Concurrent reads per request: the server thread and 7 workers
+# (store.py:59-64). VLLM_EXPERT_PAGER_READ_WORKERS overrides it (1..64) for
+# disks that want a deeper queue; it is not a reference setting.
 _READ_WORKERS = 8
+
+
+def _read_workers() -> int:
+    v = os.environ.get("VLLM_EXPERT_PAGER_READ_WORKERS")
+    if not v:
+        return _READ_WORKERS
+    n = int(v)
+    if not 1 <= n <= 64:
+        raise ValueError(f"VLLM_EXPERT_PAGER_READ_WORKERS must be in [1, 64], got {n}")
+    return n
 # Request ring slots (store.py:65-67).
 RING = 4
 
@@ -202,7 +214,7 @@ class Store:
         self._handle = self._so.ssd_start(
             self.fd_r, ctypes.c_void_p(self.req.data_ptr()), ctypes.c_void_p(self.done.data_ptr()), self.ring,
             self.block, self.num_layers, self.num_experts, self.rows, self.record_bytes, n, pinned, pitch,
-            _READ_WORKERS - 1,
+            _read_workers() - 1,
         )
         if not self._handle:
             raise RuntimeError("vllm-expert-pager: cannot start the SSD server")
