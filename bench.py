@@ -227,6 +227,30 @@ def bench_gather(args, dev):
         key = "fine" if coherent else "coarse"
         out[key] = {"gbps": round(total / (ms * 1e-3) / 1e9, 2), "ceiling_gbps": round(best, 2), "ok": ok}
         log(f"gather ({key}-grained pinned): {out[key]}")
+        if coherent:
+            # CPU baseline: the same K rows memcpy'd from the pinned tier into
+            # a host buffer by the host's cores (threads over 1 MiB pieces).
+            cores = len(os.sched_getaffinity(0))
+            src_np = [h[:K].numpy().reshape(-1) for h in host]
+            dst_np = [np.empty_like(a) for a in src_np]
+            piece = 1 << 20
+            jobs = [(k, o) for k in range(2) for o in range(0, src_np[k].size, piece)]
+
+            def cp(job):
+                k, o = job
+                np.copyto(dst_np[k][o : o + piece], src_np[k][o : o + piece])
+
+            with cf.ThreadPoolExecutor(cores) as pool:
+                list(pool.map(cp, jobs))
+                reps, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < args.cpu_seconds / 4:
+                    list(pool.map(cp, jobs))
+                    reps += 1
+            cpu = total * reps / (time.perf_counter() - t0) / 1e9
+            out["cpu_baseline"] = {"value": round(cpu, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+                                   "sample": f"memcpy of the same {K} rows from pinned RAM to a host buffer, "
+                                             f"{reps} repetitions"}
+            log(f"cpu gather: {cpu:.1f} GB/s on {cores} threads")
         for b in bufs:
             b.free()
     return out
@@ -276,7 +300,28 @@ def bench_acquire(args, dev):
         total += e0.elapsed_time(e1)
     us_layer = total / steps / L * 1e3
     log(f"acquire: {us_layer:.2f} us/layer (graph of {L} layers, both tables)")
-    return {"us_per_layer": round(us_layer, 3)}
+    # CPU baseline: the oracle's numpy restatement of ExpertTable.acquire
+    # (table.py:75-128) on the same routing, both tables per layer, one thread.
+    from oracle.table_ref import TableRef
+
+    refs = []
+    for _ in range(L):
+        v, r = TableRef(E, S), TableRef(E, R)
+        r.warm(R)
+        refs.append((v, r))
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < args.cpu_seconds / 4:
+        for layer in range(L):
+            ids_l = host_ids[n % steps, layer]
+            refs[layer][0].acquire(ids_l, pair_slots=True)
+            refs[layer][1].acquire(ids_l, pair_slots=True)
+        n += 1
+    cpu_us = (time.perf_counter() - t0) / (n * L) * 1e6
+    log(f"cpu acquire: {cpu_us:.1f} us/layer ({n} steps x {L} layers)")
+    return {"us_per_layer": round(us_layer, 3),
+            "cpu_baseline": {"value": round(cpu_us, 2), "unit": "us/layer", "cores": 1, "kind": "port",
+                             "sample": f"oracle numpy acquire of both tables, {n} steps x {L} layers of the "
+                                       "same Zipf routing"}}
 
 
 def bench_moe(args, dev):

@@ -33,6 +33,9 @@ GPU_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs, so the block-scale FMAs read them directly
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 ]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 

@@ -13,7 +13,7 @@
 //
 // Numerics of one pair follow the rounding sequence of a w8a8 block-fp8 MoE:
 // x -> fp8 per 128-group (scale = max(amax, 1e-10) / 448, q = clamp(x / s));
-// h = sum over K blocks of (xq . wq) * sx * sw in fp32; gate, up -> bf16;
+// h = sum over K blocks of (xq . wq) * (sx * sw) in fp32; gate, up -> bf16;
 // a = bf16(silu(gate) * up); a -> fp8 per 128-group; y likewise with w2;
 // contribution = bf16(y * routed weight).
 //
@@ -202,14 +202,27 @@ struct Tile {
   int slot, first, count;
 };
 
-__device__ __forceinline__ bool load_tile(const int32_t* tiles, const int32_t* offsets, Tile& t) {
-  const int i = blockIdx.y;
+// Work item of a 1-D GEMM grid of ncols column blocks per tile, laid out so
+// that every column block of a tile runs on the same XCD (workgroup L is
+// dispatched to XCD L % 8): the tile's token rows and its expert's weight
+// rows are then read into one L2. Tiles t, t + 8, ... belong to XCD t % 8.
+__device__ __forceinline__ void xcd_item(int ncols, int& tile, int& col) {
+  const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
+  tile = (j / ncols) * 8 + xcd;
+  col = j - (j / ncols) * ncols;
+}
+
+__device__ __forceinline__ bool load_tile_at(int i, const int32_t* tiles, const int32_t* offsets, Tile& t) {
   if (i >= tiles[0]) return false;
   t.slot = tiles[1 + 2 * i];
   t.first = tiles[2 + 2 * i];
   const int end = offsets[t.slot + 1];
   t.count = end - t.first < kBM ? end - t.first : kBM;
   return true;
+}
+
+__device__ __forceinline__ bool load_tile(const int32_t* tiles, const int32_t* offsets, Tile& t) {
+  return load_tile_at(blockIdx.y, tiles, offsets, t);
 }
 
 // Tile rows: the pair of each row (-1 for padding) and the A row it reads
@@ -250,13 +263,13 @@ inline int64_t work_layout(int64_t npairs, int64_t I, Work* w, uint8_t* base) {
 constexpr int kC1 = 32;       // activation columns per gemm1 workgroup
 constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I <= 8192)
 
-// GEMM1: gate and up for 32 activation columns of one tile. The 4 waves
+// GEMM1: gate and up for 32 activation columns of one tile (1-D grid in
+// XCD order, see xcd_item). The 4 waves
 // are 2 K halves x 2 column halves: wave w takes the K blocks kh, kh+2, ...
 // (kh = w / 2) of the gate and up rows of column half ch = w % 2; the second
 // K half's partial sums are added in LDS. Then a = bf16(silu(bf16 gate) *
 // bf16 up) is written as bf16 together with the maximum |a| of each row's
 // 32 columns. Only the 16-row subtiles that hold pairs are computed.
-// grid = (I / 32, tile bound).
 __global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
                                                          int64_t H, int64_t I, int topk,
                                                          const uint8_t* __restrict__ w13,
@@ -272,8 +285,10 @@ __global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restri
   __shared__ float s_sw[2][kMaxKB];     // gate and up weight scales per K block
 
   Tile tile;
-  if (!load_tile(tiles, offsets, tile)) return;
-  const int c0 = blockIdx.x * kC1;
+  int ti, cb;
+  xcd_item(static_cast<int>(I / kC1), ti, cb);
+  if (!load_tile_at(ti, tiles, offsets, tile)) return;
+  const int c0 = cb * kC1;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int kh = wave >> 1, ch = wave & 1;
@@ -320,15 +335,20 @@ __global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restri
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       if (mi >= nmi) continue;
-      float sa[4];
+      // One combined scale per output row and K block (token scale x weight
+      // scale), so each MFMA output needs a single FMA.
+      float sc[2][4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sa[r] = s_xs[(16 * mi + 4 * q + r) * KB + kb];
+      for (int r = 0; r < 4; ++r) {
+        const float sa = s_xs[(16 * mi + 4 * q + r) * KB + kb];
+        sc[0][r] = sa * g;
+        sc[1][r] = sa * u;
+      }
 #pragma unroll
       for (int si = 0; si < 2; ++si) {
         const f32x4 part = mfma_k128(a[buf][mi], b[buf][si]);
-        const float sw = si == 0 ? g : u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][si][r] += part[r] * sa[r] * sw;
+        for (int r = 0; r < 4; ++r) acc[mi][si][r] = fmaf(part[r], sc[si][r], acc[mi][si][r]);
       }
     }
   };
@@ -430,7 +450,7 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(int64_t I, const in
 // GEMM2: down projection of 128 output columns times the routed weight,
 // bf16 rows per pair; each wave owns 32 columns and reads the tile's fp8
 // activations straight from memory (shared through the cache), one K block
-// ahead. grid = (H / 128, tile bound).
+// ahead. 1-D grid in XCD order (see xcd_item).
 __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, const float* __restrict__ topk_weight,
                                                          const uint8_t* __restrict__ w2,
                                                          const float* __restrict__ w2_scale,
@@ -446,8 +466,10 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
   __shared__ __attribute__((aligned(16))) uint16_t s_o[kBM * kBN];
 
   Tile tile;
-  if (!load_tile(tiles, offsets, tile)) return;
-  const int n0 = blockIdx.x * kBN;
+  int ti, cb;
+  xcd_item(static_cast<int>(H / kBN), ti, cb);
+  if (!load_tile_at(ti, tiles, offsets, tile)) return;
+  const int n0 = cb * kBN;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(I / kKB);
@@ -489,14 +511,14 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       if (mi >= nmi) continue;
-      float sa[4];
+      float sc[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sa[r] = s_as[(16 * mi + 4 * q + r) * KB + kb];
+      for (int r = 0; r < 4; ++r) sc[r] = s_as[(16 * mi + 4 * q + r) * KB + kb] * w;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const f32x4 part = mfma_k128(a[buf][mi], b[buf][t]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][t][r] += part[r] * sa[r] * w;
+        for (int r = 0; r < 4; ++r) acc[mi][t][r] = fmaf(part[r], sc[r], acc[mi][t][r]);
       }
     }
   };
@@ -624,15 +646,18 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   Work w;
   work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
   const unsigned ty = static_cast<unsigned>(bound);
-  hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(I / kC1), ty), dim3(kThreads), 0, as_stream(stream), xq,
-                     xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
+  const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
+  const int64_t g1 = tiles8 * (I / kC1), g2 = tiles8 * (H / kBN);
+  XP_REQUIRE(g1 <= INT32_MAX && g2 <= INT32_MAX, "xp_moe_experts: grid too large");
+  hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, as_stream(stream), xq, xs, H,
+                     I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
   int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles, w);
   rc = check_launch("act_quant_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(H / kBN), ty), dim3(kThreads), 0, as_stream(stream), H,
-                     I, topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
+  hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, as_stream(stream), H, I,
+                     topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
   return check_launch("gemm2_kernel");
 }
 
