@@ -295,6 +295,14 @@ int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T,
                  int64_t slots, int32_t* offsets, int32_t* pairs,
                  int32_t* tiles, void* stream);
 
+/* xp_quant_tokens and xp_moe_route in one launch (the decode step's
+ * quantisation and routing). Same arguments and results as the two calls. */
+int xp_moe_quant_route(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq,
+                       float* xs, const void* topk_ids, int topk_elem_bytes,
+                       int64_t topk, const int32_t* expert_map,
+                       int64_t num_experts, int64_t slots, int32_t* offsets,
+                       int32_t* pairs, int32_t* tiles, void* stream);
+
 /* Bytes of the workspace xp_moe_experts needs for npairs = T*topk pairs
  * (bf16 and fp8 activations with their scales). */
 int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I);

@@ -199,3 +199,26 @@ def test_chunked_equals_one_shot_prefill_2048x8():
         w13.cpu().numpy(), w13s.cpu().numpy(), w2.cpu().numpy(), w2s.cpu().numpy(),
     )
     _check_close(one[sample].float().cpu().numpy(), ref, "prefill sample")
+
+
+@pytest.mark.parametrize("T, topk, E, slots", [(1, 8, 256, 32), (37, 4, 20, 12), (513, 8, 64, 64)])
+def test_quant_route_matches_separate_calls(T, topk, E, slots):
+    moe = _moe()
+    rng = np.random.default_rng(T + 3)
+    x = _bf16(rng.standard_normal((T, 256)).astype(np.float32))
+    ids = np.stack([rng.permutation(E)[:topk] for _ in range(T)]).astype(np.int64)
+    emap = np.full(E, -1, np.int32)
+    emap[rng.permutation(E)[:slots]] = rng.permutation(slots)
+    ids_t, emap_t = _dev(ids, emap)
+    xq, xs, r = moe.quant_route(x, ids_t, emap_t, slots)
+    xq2, xs2 = moe.quant_tokens(x)
+    r2 = moe.route(ids_t, emap_t, slots)
+    assert torch.equal(xq, xq2) and torch.equal(xs, xs2)
+    assert torch.equal(r.offsets, r2.offsets)
+    n = int(r.tiles[0])
+    assert n == int(r2.tiles[0]) and torch.equal(r.tiles[: 1 + 2 * n], r2.tiles[: 1 + 2 * n])
+    o = r.offsets.cpu().numpy()
+    for s in range(slots):
+        a = np.sort(r.pairs[o[s] : o[s + 1]].cpu().numpy())
+        b = np.sort(r2.pairs[o[s] : o[s + 1]].cpu().numpy())
+        assert np.array_equal(a, b)

@@ -83,12 +83,11 @@ __device__ __forceinline__ void load32(const uint8_t* p, u32x4 (&v)[2]) {
   v[1] = *reinterpret_cast<const u32x4*>(p + 16);
 }
 
-// ---- token quantisation: one workgroup per token, 16 lanes per group ----
-__global__ void __launch_bounds__(256) quant_tokens_kernel(const uint16_t* __restrict__ x, int64_t H,
-                                                           uint8_t* __restrict__ xq, float* __restrict__ xs) {
-  const int64_t t = blockIdx.x;
+// ---- token quantisation: 256 threads per token, 16 lanes per group ----
+__device__ __forceinline__ void quant_token(const uint16_t* __restrict__ x, int64_t H, uint8_t* __restrict__ xq,
+                                            float* __restrict__ xs, int64_t t, int tid) {
   const uint16_t* row = x + t * H;
-  for (int64_t c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+  for (int64_t c0 = tid * 8; c0 < H; c0 += 256 * 8) {
     const u32x4 raw = *reinterpret_cast<const u32x4*>(row + c0);
     float v[8];
     float amax = 0.f;
@@ -109,8 +108,13 @@ __global__ void __launch_bounds__(256) quant_tokens_kernel(const uint16_t* __res
       q1 |= to_fp8(clamp_fp8(v[4 + i] / s)) << (8 * i);
     }
     *reinterpret_cast<uint2*>(xq + t * H + c0) = make_uint2(q0, q1);
-    if ((threadIdx.x & 15) == 0) xs[t * (H / kKB) + c0 / kKB] = s;
+    if ((tid & 15) == 0) xs[t * (H / kKB) + c0 / kKB] = s;
   }
+}
+
+__global__ void __launch_bounds__(256) quant_tokens_kernel(const uint16_t* __restrict__ x, int64_t H,
+                                                           uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  quant_token(x, H, xq, xs, blockIdx.x, threadIdx.x);
 }
 
 // Exclusive scan of two counters over a 1024-thread workgroup.
@@ -147,13 +151,10 @@ __device__ __forceinline__ int2 block_scan2(int a, int b, int2* s_tot, int2* tot
 // per tile. Each wave counts a contiguous range of pairs into its own LDS
 // histogram (no contention between waves), so a slot's list is ordered by
 // wave range; dynamic LDS = 16 * slots ints.
-__global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, int eb, int64_t npairs,
-                                                              const int32_t* __restrict__ expert_map, int E,
-                                                              int slots, int32_t* __restrict__ offsets,
-                                                              int32_t* __restrict__ pairs,
-                                                              int32_t* __restrict__ tiles) {
-  extern __shared__ int s_hist[];  // [16 waves][slots]
-  __shared__ int2 s_tot[kRouteThreads / 64];
+__device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npairs,
+                                            const int32_t* __restrict__ expert_map, int E, int slots,
+                                            int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
+                                            int32_t* __restrict__ tiles, int* s_hist, int2* s_tot) {
   constexpr int kW = kRouteThreads / 64;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < kW * slots; i += kRouteThreads) s_hist[i] = 0;
@@ -196,6 +197,36 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, i
     const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
     if (s >= 0 && s < slots) pairs[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(p);
   }
+}
+
+__global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, int eb, int64_t npairs,
+                                                              const int32_t* __restrict__ expert_map, int E,
+                                                              int slots, int32_t* __restrict__ offsets,
+                                                              int32_t* __restrict__ pairs,
+                                                              int32_t* __restrict__ tiles) {
+  extern __shared__ int s_hist[];  // [16 waves][slots]
+  __shared__ int2 s_tot[kRouteThreads / 64];
+  route_block(ids, eb, npairs, expert_map, E, slots, offsets, pairs, tiles, s_hist, s_tot);
+}
+
+// Quantisation and routing of one MoE call in one launch: workgroup 0
+// routes, workgroup b >= 1 quantises tokens 4(b-1) .. 4(b-1)+3.
+__global__ void __launch_bounds__(kRouteThreads) quant_route_kernel(const uint16_t* __restrict__ x, int64_t T,
+                                                                    int64_t H, uint8_t* __restrict__ xq,
+                                                                    float* __restrict__ xs, const void* ids, int eb,
+                                                                    int64_t npairs,
+                                                                    const int32_t* __restrict__ expert_map, int E,
+                                                                    int slots, int32_t* __restrict__ offsets,
+                                                                    int32_t* __restrict__ pairs,
+                                                                    int32_t* __restrict__ tiles) {
+  extern __shared__ int s_hist[];
+  __shared__ int2 s_tot[kRouteThreads / 64];
+  if (blockIdx.x == 0) {
+    route_block(ids, eb, npairs, expert_map, E, slots, offsets, pairs, tiles, s_hist, s_tot);
+    return;
+  }
+  const int64_t t = (static_cast<int64_t>(blockIdx.x) - 1) * 4 + (threadIdx.x >> 8);
+  if (t < T) quant_token(x, H, xq, xs, t, threadIdx.x & 255);
 }
 
 struct Tile {
@@ -615,6 +646,29 @@ int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T, int64_t t
                      T * topk, expert_map, static_cast<int>(num_experts), static_cast<int>(slots), offsets, pairs,
                      tiles);
   return check_launch("route_kernel");
+}
+
+int xp_moe_quant_route(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq, float* xs, const void* topk_ids,
+                       int topk_elem_bytes, int64_t topk, const int32_t* expert_map, int64_t num_experts,
+                       int64_t slots, int32_t* offsets, int32_t* pairs, int32_t* tiles, void* stream) {
+  XP_REQUIRE(T >= 0 && T <= INT32_MAX && H > 0 && H % kKB == 0,
+             "xp_moe_quant_route: T=%lld, H=%lld (H must be a positive multiple of %d)", (long long)T,
+             (long long)H, kKB);
+  XP_REQUIRE(topk_elem_bytes == 4 || topk_elem_bytes == 8, "xp_moe_quant_route: id size %d", topk_elem_bytes);
+  XP_REQUIRE(topk >= 1 && T * topk <= INT32_MAX, "xp_moe_quant_route: topk=%lld", (long long)topk);
+  XP_REQUIRE(slots >= 1 && slots <= kMaxRouteSlots, "xp_moe_quant_route: %lld slots (at most %d)",
+             (long long)slots, kMaxRouteSlots);
+  XP_REQUIRE(num_experts >= 1 && num_experts <= INT32_MAX, "xp_moe_quant_route: %lld experts",
+             (long long)num_experts);
+  XP_REQUIRE(expert_map && offsets && pairs && tiles, "xp_moe_quant_route: null argument");
+  XP_REQUIRE(T == 0 || (x && xq && xs && topk_ids && aligned16(x) && aligned16(xq)),
+             "xp_moe_quant_route: null or misaligned buffer");
+  const size_t lds = static_cast<size_t>(kRouteThreads / 64) * static_cast<size_t>(slots) * sizeof(int);
+  const unsigned grid = static_cast<unsigned>(1 + (T + 3) / 4);
+  hipLaunchKernelGGL(quant_route_kernel, dim3(grid), dim3(kRouteThreads), lds, as_stream(stream), x, T, H, xq, xs,
+                     topk_ids, topk_elem_bytes, T * topk, expert_map, static_cast<int>(num_experts),
+                     static_cast<int>(slots), offsets, pairs, tiles);
+  return check_launch("quant_route_kernel");
 }
 
 int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I) {

@@ -84,9 +84,7 @@ def _shape(topk_ids: torch.Tensor) -> tuple[int, int]:
     return topk_ids.numel(), 1
 
 
-def route(topk_ids: torch.Tensor, expert_map: torch.Tensor, slots: int, out: Routing | None = None) -> Routing:
-    """List the pairs whose expert ``expert_map`` places in a slot ``< slots``."""
-    ids, eb = nat.ids_arg(topk_ids)
+def _routing(topk_ids: torch.Tensor, expert_map: torch.Tensor, slots: int, out: Routing | None) -> Routing:
     nat.require_device(expert_map, "expert_map")
     if expert_map.dtype != torch.int32 or not expert_map.is_contiguous():
         raise ValueError("expert_map must be a contiguous int32 tensor")
@@ -103,11 +101,42 @@ def route(topk_ids: torch.Tensor, expert_map: torch.Tensor, slots: int, out: Rou
             torch.empty((max(n, 1),), dtype=torch.int32, device=dev),
             torch.empty((1 + 2 * max(bound, 1),), dtype=torch.int32, device=dev),
         )
+    return out
+
+
+def route(topk_ids: torch.Tensor, expert_map: torch.Tensor, slots: int, out: Routing | None = None) -> Routing:
+    """List the pairs whose expert ``expert_map`` places in a slot ``< slots``."""
+    ids, eb = nat.ids_arg(topk_ids)
+    out = _routing(topk_ids, expert_map, slots, out)
+    T, topk = _shape(topk_ids)
     nat.call(
         "xp_moe_route", nat.ptr(ids), eb, T, topk, expert_map.data_ptr(), expert_map.numel(), slots,
         out.offsets.data_ptr(), out.pairs.data_ptr(), out.tiles.data_ptr(), nat.stream(),
     )
     return out
+
+
+def quant_route(x: torch.Tensor, topk_ids: torch.Tensor, expert_map: torch.Tensor,
+                slots: int) -> tuple[torch.Tensor, torch.Tensor, Routing]:
+    """``quant_tokens(x)`` and ``route(topk_ids, expert_map, slots)`` in one launch."""
+    nat.require_device(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError(f"x must be a 2-D bfloat16 tensor, got {x.dtype} {tuple(x.shape)}")
+    x = x.contiguous()
+    T, H = x.shape
+    if _shape(topk_ids)[0] != T:
+        raise ValueError(f"topk_ids has {_shape(topk_ids)[0]} tokens, x has {T}")
+    ids, eb = nat.ids_arg(topk_ids)
+    topk = _shape(topk_ids)[1]
+    r = _routing(topk_ids, expert_map, slots, None)
+    xq = torch.empty((T, H), dtype=torch.uint8, device=x.device)
+    xs = torch.empty((T, H // BLOCK if H % BLOCK == 0 else 0), dtype=torch.float32, device=x.device)
+    nat.call(
+        "xp_moe_quant_route", x.data_ptr(), T, H, xq.data_ptr(), xs.data_ptr(), nat.ptr(ids), eb, topk,
+        expert_map.data_ptr(), expert_map.numel(), slots, r.offsets.data_ptr(), r.pairs.data_ptr(),
+        r.tiles.data_ptr(), nat.stream(),
+    )
+    return xq, xs, r
 
 
 def run_experts(

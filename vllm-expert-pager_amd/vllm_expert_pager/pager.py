@@ -241,9 +241,9 @@ class PagedExperts:
             if store.compress:
                 decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
 
-        xq, xs = moe.quant_tokens(x)
+        xq, xs, routing = moe.quant_route(x, topk_ids, self.expert_map, self.table.num_slots)
         contrib = self._contrib(topk_weights, x)
-        self._run(self.cache_slab, xq, xs, topk_weights, topk_ids, contrib)
+        self._run(self.cache_slab, xq, xs, topk_weights, topk_ids, contrib, routing)
         self._log()
         return moe.topk_sum(contrib, topk_ids, E)
 
@@ -312,16 +312,19 @@ class PagedExperts:
         return moe.topk_sum(contrib, topk_ids, E)
 
     def _contrib(self, topk_weights: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        # Pairs outside every map contribute zero, as the reference's kernel
-        # writes zeros for experts outside expert_map.
+        # Every pair with a valid expert id is written: acquire maps every
+        # needed expert, and plan_chunks maps each needed expert in exactly
+        # one chunk. Pairs with an id outside [0, E) are skipped by the top-k
+        # sum. So no zero fill is needed (the reference's kernel writes zeros
+        # for experts outside a chunk's map, which the sum adds exactly).
         T, topk = topk_weights.shape
-        return torch.zeros((T * topk, x.shape[1]), dtype=torch.bfloat16, device=x.device)
+        return torch.empty((T * topk, x.shape[1]), dtype=torch.bfloat16, device=x.device)
 
     def _run(self, slab: dict[str, torch.Tensor], xq: torch.Tensor, xs: torch.Tensor, topk_weights: torch.Tensor,
-             topk_ids: torch.Tensor, contrib: torch.Tensor) -> None:
+             topk_ids: torch.Tensor, contrib: torch.Tensor, routing: moe.Routing | None = None) -> None:
         """Run the experts that ``expert_map`` places in ``slab`` (experts.py:579-604)."""
         S = slab[PARAMS[0]].shape[0]
-        r = moe.route(topk_ids, self.expert_map, S)
+        r = routing if routing is not None else moe.route(topk_ids, self.expert_map, S)
         moe.run_experts(xq, xs, topk_weights, slab[PARAMS[0]], slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]],
                         r, contrib)
 
