@@ -291,81 +291,113 @@ inline int64_t work_layout(int64_t npairs, int64_t I, Work* w, uint8_t* base) {
   return sz[0] + sz[1] + sz[2] + sz[3];
 }
 
-constexpr int kC1 = 32;       // activation columns per gemm1 workgroup
+constexpr int kC1 = 32;       // activation columns per narrow gemm1 workgroup
+constexpr int kWideTiles = 64;  // tile bound from which gemm1 uses the wide workgroups
+constexpr int kWideNW = 8;      // waves (16 activation columns each) of a wide gemm1 workgroup
 constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I <= 8192)
 
-// GEMM1: gate and up for 32 activation columns of one tile (1-D grid in
-// XCD order, see xcd_item). The 4 waves
-// are 2 K halves x 2 column halves: wave w takes the K blocks kh, kh+2, ...
-// (kh = w / 2) of the gate and up rows of column half ch = w % 2; the second
-// K half's partial sums are added in LDS. Then a = bf16(silu(bf16 gate) *
-// bf16 up) is written as bf16 together with the maximum |a| of each row's
-// 32 columns. Only the 16-row subtiles that hold pairs are computed.
-__global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                         int64_t H, int64_t I, int topk,
-                                                         const uint8_t* __restrict__ w13,
-                                                         const float* __restrict__ w13_scale,
-                                                         const int32_t* __restrict__ offsets,
-                                                         const int32_t* __restrict__ pairs,
-                                                         const int32_t* __restrict__ tiles, Work work) {
+constexpr int kAPitch = 144;  // LDS bytes per staged A row (128 + 16 against bank conflicts)
+
+// The A rows of a tile for one K block, staged through registers into LDS
+// by all NT threads of the workgroup (16 bytes per thread per piece), so
+// the global loads of the next block are in flight while this one is used.
+template <int NT>
+struct AStage {
+  static constexpr int kPer = kBM * 8 / NT;  // 16-byte pieces per thread
+  const uint8_t* src[kPer];
+  int dst[kPer];
+  u32x4 v[kPer];
+  __device__ __forceinline__ void init(const uint8_t* A, int64_t lda, const int* s_row) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = static_cast<int>(threadIdx.x) + NT * i, row = c >> 3, off = (c & 7) * 16;
+      src[i] = A + static_cast<int64_t>(s_row[row]) * lda + off;
+      dst[i] = row * kAPitch + off;
+    }
+  }
+  __device__ __forceinline__ void load(int kb) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) v[i] = *reinterpret_cast<const u32x4*>(src[i] + kb * kKB);
+  }
+  __device__ __forceinline__ void store(uint8_t* s_a) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) *reinterpret_cast<u32x4*>(s_a + dst[i]) = v[i];
+  }
+};
+
+__device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4 (&a)[2]) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(s_a + row * kAPitch + 32 * q);
+  a[0] = p[0];
+  a[1] = p[1];
+}
+
+// GEMM1: gate and up for NW*16 activation columns of one tile (1-D grid in
+// XCD order, see xcd_item); each wave owns 16 columns and runs the K blocks
+// in order, so a column's value does not depend on the workgroup width.
+// The tile's A rows are staged in LDS, double-buffered, one block ahead.
+// Then a = bf16(silu(bf16 gate) * bf16 up) is written as bf16 with the
+// maximum |a| of each row's 32-column blocks. Only the 16-row subtiles that
+// hold pairs are multiplied.
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                        int64_t H, int64_t I, int topk,
+                                                        const uint8_t* __restrict__ w13,
+                                                        const float* __restrict__ w13_scale,
+                                                        const int32_t* __restrict__ offsets,
+                                                        const int32_t* __restrict__ pairs,
+                                                        const int32_t* __restrict__ tiles, Work work) {
+  constexpr int NT = NW * 64, NC = NW * 16;
   __shared__ int s_row[kBM];
   __shared__ int s_pair[kBM];
-  __shared__ float s_xs[kBM * kMaxKB];  // token scales per row and K block; then the bf16 staging
-  __shared__ f32x4 s_red[2][4][2][64];  // [column half][row subtile][gate, up][lane]
-  __shared__ float s_m[2][kBM];         // row maxima per column half
+  __shared__ float s_xs[kBM * kMaxKB];  // token scales per row and K block
   __shared__ float s_sw[2][kMaxKB];     // gate and up weight scales per K block
+  __shared__ float s_m[NW][kBM];        // row maxima per wave (16 columns)
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kBM * kAPitch];  // A stages; then the bf16 staging
 
   Tile tile;
   int ti, cb;
-  xcd_item(static_cast<int>(I / kC1), ti, cb);
+  xcd_item(static_cast<int>(I / NC), ti, cb);
   if (!load_tile_at(ti, tiles, offsets, tile)) return;
-  const int c0 = cb * kC1;
+  const int c0 = cb * NC;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
-  const int kh = wave >> 1, ch = wave & 1;
   const int KB = static_cast<int>(H / kKB);
   const int nmi = (tile.count + 15) >> 4;
 
   tile_rows(tile, pairs, topk, s_pair, s_row);
   __syncthreads();
-  for (int i = tid; i < 16 * nmi * KB; i += kThreads) {
+  for (int i = tid; i < 16 * nmi * KB; i += NT) {
     const int r = i / KB, kb = i - r * KB;
     s_xs[i] = xs[static_cast<int64_t>(s_row[r]) * KB + kb];
   }
   {
-    // Weight scales of the gate and up rows: one 128-row block each.
+    // The workgroup's gate and up rows each lie in one 128-row scale block.
     const float* sg = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + c0 / kKB) * KB;
     const float* su = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
-    for (int i = tid; i < 2 * KB; i += kThreads) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
+    for (int i = tid; i < 2 * KB; i += NT) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
   }
-  __syncthreads();
+  AStage<NT> st;
+  st.init(xq, H, s_row);
 
   const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
-  const int64_t n = c0 + 16 * ch + j;
+  const int64_t n = c0 + 16 * wave + j;
   const uint8_t* brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
-  const uint8_t* arow[4];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) arow[mi] = xq + static_cast<int64_t>(s_row[16 * mi + j]) * H + 32 * q;
 
   f32x4 acc[4][2];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // A and B of the next K block are requested before the current one is
-  // multiplied (all A rows unconditionally: padding rows point at a live
-  // row), so the in-order load counter never makes the MFMAs wait for them.
-  u32x4 a[2][4][2], b[2][2][2];
-  auto load = [&](int buf, int kb) {
+  u32x4 b0[2][2], b1[2][2];
+  auto load_b = [&](u32x4 (&b)[2][2], int kb) {
 #pragma unroll
-    for (int si = 0; si < 2; ++si) load32(brow[si] + kb * kKB, b[buf][si]);
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) load32(arow[mi] + kb * kKB, a[buf][mi]);
+    for (int si = 0; si < 2; ++si) load32(brow[si] + kb * kKB, b[si]);
   };
-  auto compute = [&](int buf, int kb) {
+  auto compute = [&](const uint8_t* sa_buf, const u32x4 (&b)[2][2], int kb) {
     const float g = s_sw[0][kb], u = s_sw[1][kb];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       if (mi >= nmi) continue;
+      u32x4 a[2];
+      read_a(sa_buf, 16 * mi + j, q, a);
       // One combined scale per output row and K block (token scale x weight
       // scale), so each MFMA output needs a single FMA.
       float sc[2][4];
@@ -377,64 +409,64 @@ __global__ void __launch_bounds__(kThreads) gemm1_kernel(const uint8_t* __restri
       }
 #pragma unroll
       for (int si = 0; si < 2; ++si) {
-        const f32x4 part = mfma_k128(a[buf][mi], b[buf][si]);
+        const f32x4 part = mfma_k128(a, b[si]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[mi][si][r] = fmaf(part[r], sc[si][r], acc[mi][si][r]);
       }
     }
   };
-  // Branch-free prefetch: the block index is clamped at the wave's last
-  // block, so every iteration issues the same loads.
-  const int nk = (KB - kh + 1) / 2;  // K blocks kh, kh + 2, ... below KB
-  if (nk > 0) {
-    auto kidx = [&](int i) { return kh + 2 * (i < nk ? i : nk - 1); };
-    load(0, kidx(0));
-    for (int i = 0; i < nk; i += 2) {
-      load(1, kidx(i + 1));
-      compute(0, kidx(i));
-      load(0, kidx(i + 2));
-      if (i + 1 < nk) compute(1, kidx(i + 1));
-    }
+
+  // Every step issues the next block's loads (the index clamped at the last
+  // block, so the loads are unconditional) before multiplying the current.
+  __syncthreads();  // s_row, s_xs, s_sw
+  st.load(0);
+  load_b(b0, 0);
+  st.store(s_a[0]);
+  __syncthreads();
+  for (int kb = 0; kb < KB; kb += 2) {
+    const int k1 = kb + 1 < KB ? kb + 1 : KB - 1, k2 = kb + 2 < KB ? kb + 2 : KB - 1;
+    st.load(k1);
+    load_b(b1, k1);
+    compute(s_a[0], b0, kb);
+    st.store(s_a[1]);
+    __syncthreads();
+    st.load(k2);
+    load_b(b0, k2);
+    if (kb + 1 < KB) compute(s_a[1], b1, kb + 1);
+    st.store(s_a[0]);
+    __syncthreads();
   }
 
-  if (kh == 1) {
+  uint16_t* s_o = reinterpret_cast<uint16_t*>(s_a);  // [kBM][NC] bf16
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-      if (mi < nmi) {
-        s_red[ch][mi][0][lane] = acc[mi][0];
-        s_red[ch][mi][1][lane] = acc[mi][1];
-      }
-  }
-  __syncthreads();
-  uint16_t* s_o = reinterpret_cast<uint16_t*>(s_xs);  // [kBM][kC1] bf16
-  if (kh == 0) {
+  for (int mi = 0; mi < 4; ++mi) {
+    if (mi >= nmi) continue;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      if (mi >= nmi) continue;
-      const f32x4 gs = acc[mi][0] + s_red[ch][mi][0][lane];
-      const f32x4 us = acc[mi][1] + s_red[ch][mi][1][lane];
+    for (int r = 0; r < 4; ++r) {
+      const float g = bf16_round(acc[mi][0][r]), u = bf16_round(acc[mi][1][r]);
+      const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+      float m = fabsf(a);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float g = bf16_round(gs[r]), u = bf16_round(us[r]);
-        const float a = bf16_round(g / (1.0f + expf(-g)) * u);
-        float m = fabsf(a);
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
-        const int row = 16 * mi + 4 * q + r;
-        if (j == 0) s_m[ch][row] = m;
-        s_o[row * kC1 + 16 * ch + j] = static_cast<uint16_t>(bf16_bits(a));
-      }
+      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      const int row = 16 * mi + 4 * q + r;
+      if (j == 0) s_m[wave][row] = m;
+      s_o[row * NC + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(a));
     }
   }
   __syncthreads();
-  {
-    const int row = tid >> 2, part = tid & 3;  // 64 bytes per row: 4 threads x 16 bytes
+  for (int i = tid; i < kBM * (NW / 2); i += NT) {  // maxima of the 32-column blocks
+    const int row = i % kBM, k = i / kBM;
     const int p = s_pair[row];
-    if (p >= 0) {
-      *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + part * 8) =
-          *reinterpret_cast<const u32x4*>(s_o + row * kC1 + part * 8);
-      if (part == 0) work.amax32[static_cast<int64_t>(p) * (I / 32) + c0 / 32] = fmaxf(s_m[0][row], s_m[1][row]);
-    }
+    if (p >= 0)
+      work.amax32[static_cast<int64_t>(p) * (I / 32) + c0 / 32 + k] = fmaxf(s_m[2 * k][row], s_m[2 * k + 1][row]);
+  }
+  constexpr int kPieces = NC / 8;  // 16-byte pieces per row
+  for (int i = tid; i < kBM * kPieces; i += NT) {
+    const int row = i / kPieces, piece = i - row * kPieces;
+    const int p = s_pair[row];
+    if (p >= 0)
+      *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
+          *reinterpret_cast<const u32x4*>(s_o + row * NC + piece * 8);
   }
 }
 
@@ -479,9 +511,9 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(int64_t I, const in
 }
 
 // GEMM2: down projection of 128 output columns times the routed weight,
-// bf16 rows per pair; each wave owns 32 columns and reads the tile's fp8
-// activations straight from memory (shared through the cache), one K block
-// ahead. 1-D grid in XCD order (see xcd_item).
+// bf16 rows per pair; each wave owns 32 columns and runs the K blocks in
+// order over the tile's fp8 activations, staged in LDS one block ahead.
+// 1-D grid in XCD order (see xcd_item).
 __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, const float* __restrict__ topk_weight,
                                                          const uint8_t* __restrict__ w2,
                                                          const float* __restrict__ w2_scale,
@@ -493,7 +525,8 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
   __shared__ int s_pair[kBM];
   __shared__ float s_as[kBM * kMaxKB];
   __shared__ float s_w[kBM];
-  __shared__ float s_sw[kMaxKB];        // weight scales per K block of this 128-column block
+  __shared__ float s_sw[kMaxKB];  // weight scales per K block of this 128-column block
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kBM * kAPitch];
   __shared__ __attribute__((aligned(16))) uint16_t s_o[kBM * kBN];
 
   Tile tile;
@@ -514,52 +547,58 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
   }
   if (tid < kBM) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
   if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
-  __syncthreads();
+  AStage<kThreads> st;
+  st.init(work.act, I, s_row);
 
   const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
   const uint8_t* brow[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) brow[t] = wslot + static_cast<int64_t>(n0 + 32 * wave + 16 * t + j) * I + 32 * q;
-  const uint8_t* arow[4];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) arow[mi] = work.act + static_cast<int64_t>(s_row[16 * mi + j]) * I + 32 * q;
 
   f32x4 acc[4][2];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 b0[2][2], b1[2][2];
+  auto load_b = [&](u32x4 (&b)[2][2], int kb) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  u32x4 a[2][4][2], b[2][2][2];
-  auto load = [&](int buf, int kb) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) load32(brow[t] + kb * kKB, b[buf][t]);
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) load32(arow[mi] + kb * kKB, a[buf][mi]);
+    for (int t = 0; t < 2; ++t) load32(brow[t] + kb * kKB, b[t]);
   };
-  auto compute = [&](int buf, int kb) {
+  auto compute = [&](const uint8_t* sa_buf, const u32x4 (&b)[2][2], int kb) {
     const float w = s_sw[kb];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       if (mi >= nmi) continue;
+      u32x4 a[2];
+      read_a(sa_buf, 16 * mi + j, q, a);
       float sc[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) sc[r] = s_as[(16 * mi + 4 * q + r) * KB + kb] * w;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const f32x4 part = mfma_k128(a[buf][mi], b[buf][t]);
+        const f32x4 part = mfma_k128(a, b[t]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[mi][t][r] = fmaf(part[r], sc[r], acc[mi][t][r]);
       }
     }
   };
-  auto kidx = [&](int i) { return i < KB ? i : KB - 1; };
-  load(0, 0);
-  for (int i = 0; i < KB; i += 2) {
-    load(1, kidx(i + 1));
-    compute(0, i);
-    load(0, kidx(i + 2));
-    if (i + 1 < KB) compute(1, i + 1);
+
+  __syncthreads();  // s_row, s_as, s_w, s_sw
+  st.load(0);
+  load_b(b0, 0);
+  st.store(s_a[0]);
+  __syncthreads();
+  for (int kb = 0; kb < KB; kb += 2) {
+    const int k1 = kb + 1 < KB ? kb + 1 : KB - 1, k2 = kb + 2 < KB ? kb + 2 : KB - 1;
+    st.load(k1);
+    load_b(b1, k1);
+    compute(s_a[0], b0, kb);
+    st.store(s_a[1]);
+    __syncthreads();
+    st.load(k2);
+    load_b(b0, k2);
+    if (kb + 1 < KB) compute(s_a[1], b1, kb + 1);
+    st.store(s_a[0]);
+    __syncthreads();
   }
 
 #pragma unroll
@@ -703,8 +742,18 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
   const int64_t g1 = tiles8 * (I / kC1), g2 = tiles8 * (H / kBN);
   XP_REQUIRE(g1 <= INT32_MAX && g2 <= INT32_MAX, "xp_moe_experts: grid too large");
-  hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(g1)), dim3(kThreads), 0, as_stream(stream), xq, xs, H,
-                     I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
+  // Prefill-sized calls take 16*kWideNW activation columns per workgroup
+  // (token rows shared by more waves), small calls 32 (more workgroups for
+  // few pairs). Every column is computed the same way in both.
+  if (bound >= kWideTiles && I % (16 * kWideNW) == 0) {
+    const int64_t g1w = tiles8 * (I / (16 * kWideNW));
+    hipLaunchKernelGGL(gemm1_kernel<kWideNW>, dim3(static_cast<unsigned>(g1w)), dim3(64 * kWideNW), 0,
+                       as_stream(stream), xq, xs,
+                       H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
+  } else {
+    hipLaunchKernelGGL(gemm1_kernel<2>, dim3(static_cast<unsigned>(g1)), dim3(128), 0, as_stream(stream), xq, xs, H,
+                       I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
+  }
   int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles, w);
