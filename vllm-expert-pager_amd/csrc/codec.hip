@@ -142,84 +142,47 @@ __device__ __forceinline__ uint32_t lane_select(unsigned long long mask, uint32_
   return r;
 }
 
-// out |= (word 1 of e) << 16k as one word-select OR (word k of out is zero).
+// out |= (byte 1 of e) << 8k as one byte-select OR (byte k of out is zero).
 template <int K>
-__device__ __forceinline__ void or_word(uint32_t& out, uint32_t e) {
+__device__ __forceinline__ void or_byte(uint32_t& out, uint32_t e) {
   if constexpr (K == 0)
-    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:WORD_0 dst_unused:UNUSED_PRESERVE src0_sel:WORD_1 src1_sel:WORD_0"
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_0"
+        : "+v"(out) : "v"(e));
+  else if constexpr (K == 1)
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_1"
+        : "+v"(out) : "v"(e));
+  else if constexpr (K == 2)
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_2"
         : "+v"(out) : "v"(e));
   else
-    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_1 src1_sel:WORD_1"
+    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_3"
         : "+v"(out) : "v"(e));
 }
 
-// Lanes of `mask` below this one in its half-wave. `low` is all ones in
-// the lower half and zero in the upper one: for the upper half the lower
-// half's count (all of the low word) is masked off before counting.
-__device__ __forceinline__ uint32_t below_in_half(unsigned long long mask, uint32_t low) {
-  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u) & low);
-}
-
-// popc of each half of a mask, packed as lo | hi << 16.
-__device__ __forceinline__ uint32_t half_counts(unsigned long long mask) {
-  return static_cast<uint32_t>(__popc(static_cast<uint32_t>(mask))) |
-         (static_cast<uint32_t>(__popc(static_cast<uint32_t>(mask >> 32))) << 16);
-}
-
-__device__ __forceinline__ uint32_t ring_word(uint32_t addr) {
-  return *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(addr);
-}
-
-// Symbols s and s+1 of one stream with one table read, and the refills the
-// format makes before s+1 and before s+2. On entry the refill before s is
-// done, so at least LIMIT bits are buffered, and s_pair[window] holds
-//   bits 0-3   c1 = length of s,
-//   bits 4-7   c2 = c1 + length of s+1 when s+1 also lies in the window, else 0,
-//   bits 16-31 (exponent of s) << 3 | (exponent of s+1) << 11 (zero if c2 is 0).
-// A lane refills at most once in three symbols (it then holds at least
-// 32 bits and a symbol takes at most LIMIT), so at most once per pair: its
-// ring word is the (refills before s+1 below it) for a refill before s+1,
-// and (all refills before s+1) + (refills before s+2 below it) for one
-// before s+2 -- the (symbol, lane) word order. The rare pair that does not
-// fit the window takes a second read, after its refill when one is due.
+// One symbol of one stream, without branches: every lane reads a ring word
+// at its refill address and keeps it only if it refills. `low` is all ones
+// in the lower half-wave and zero in the upper one; s_lut holds
+// len | (symbol << 3) << 8 per 9-bit code.
 template <int K>
-__device__ __forceinline__ void decode_pair(uint64_t& buf, uint32_t& pos, uint32_t& ab, uint32_t& out, uint32_t low,
-                                            uint32_t half_shift, const uint32_t* s_pair) {
-  uint32_t e = s_pair[static_cast<uint32_t>(buf >> pos) & (XP_LUT_BYTES - 1)];
-  const uint32_t c1 = e & 15u;
-  uint32_t c2 = (e >> 4) & 15u;
-  const uint32_t t = (64u - kLimit) - pos;  // a refill is due once more than t bits are used
-  const unsigned long long b1 = __builtin_amdgcn_ballot_w64(c1 > t);
-  const uint32_t mb1 = below_in_half(b1, low);
-  unsigned long long done = 0;  // lanes that took their ring word in the second read
-  const unsigned long long slow = __builtin_amdgcn_ballot_w64(c2 == 0u);
-  if (slow) {
-    if (c2 == 0u) {
-      uint32_t p1 = pos + c1;
-      if (c1 > t) {
-        const uint32_t w = ring_word(ab + 4u * mb1);
-        buf = (static_cast<uint64_t>(w) << 32) | (buf >> 32);
-        p1 -= 32u;
-      }
-      const uint32_t e2 = s_pair[static_cast<uint32_t>(buf >> p1) & (XP_LUT_BYTES - 1)];
-      c2 = c1 + (e2 & 15u);
-      e |= (e2 << 8) & 0xff000000u;  // exponent of s+1 into byte 3
-    }
-    done = slow & b1;
-  }
-  const unsigned long long b2 = __builtin_amdgcn_ballot_w64(c2 > t);
-  const uint32_t mb2 = below_in_half(b2, low);
-  const uint32_t n1 = __builtin_amdgcn_ubfe(half_counts(b1), half_shift, 16u);
-  const uint32_t below = lane_select(b1, n1 + mb2 - mb1, mb1);
-  const uint32_t w = ring_word(ab + 4u * below);
-  const unsigned long long take = b2 & ~done;
+__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& ab, uint32_t& out,
+                                              uint32_t low, uint32_t half_shift, const uint16_t* s_lut) {
+  const bool refill = pos > 64u - kLimit;
+  const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
+  const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
+  // Refilling lanes below this one in its half: for the upper half the
+  // lower half's count (all of m_lo) is masked off before counting m_hi.
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u) & low);
+  const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(ab + 4u * below);
   const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
-  const uint32_t nlo = lane_select(take, lo, hi), nhi = lane_select(take, hi, w);
+  const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
+  pos = lane_select(mask, pos, pos - 32u);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
-  pos = pos + c2 - lane_select(b2, 0u, 32u);
-  ab += 4u * __builtin_amdgcn_ubfe(half_counts(b2), half_shift, 16u);
-  or_word<K / 2>(out, e);
+  const uint32_t counts = static_cast<uint32_t>(__popc(m_lo)) | (static_cast<uint32_t>(__popc(m_hi)) << 16);
+  ab += 4u * __builtin_amdgcn_ubfe(counts, half_shift, 16u);
+  const uint32_t idx = static_cast<uint32_t>(buf >> (pos & 63u)) & (XP_LUT_BYTES - 1);
+  const uint32_t e = s_lut[idx];
+  pos += e & 0xffu;
+  or_byte<K & 3>(out, e);
 }
 
 // v from lane (this lane xor D), D in {1, 2, 4}: a quad permute for 1 and
@@ -234,67 +197,67 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), (D << 10) | 0x1F));
 }
 
-// One stage of the 8-lane transpose of 16-byte pieces w[4j..4j+3]: lanes
-// whose bit D is clear swap their pieces j | D with the partner's pieces j.
-template <int D>
-__device__ __forceinline__ void butterfly(uint32_t (&w)[32], uint32_t q) {
+// One stage of the NP-lane transpose of 16-byte pieces w[4j..4j+3]
+// (j < NP): lanes whose bit D is clear swap their pieces j | D with the
+// partner's pieces j.
+template <int D, int NP>
+__device__ __forceinline__ void butterfly(uint32_t (&w)[4 * NP], uint32_t q) {
   // The selects are instructions on a lane mask: selecting between two
   // array elements would let the compiler index the array dynamically.
   const unsigned long long hi = __builtin_amdgcn_ballot_w64((q & static_cast<uint32_t>(D)) != 0);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 2 * NP; ++i) {
     const int jj = i >> 2, k = i & 3;
     const int j = ((jj & ~(D - 1)) << 1) | (jj & (D - 1));  // the pieces whose bit D is clear
-    {
-      const int ia = 4 * j + k, ib = 4 * (j | D) + k;
-      const uint32_t r = lane_xor<D>(lane_select(hi, w[ib], w[ia]));
-      w[ia] = lane_select(hi, w[ia], r);
-      w[ib] = lane_select(hi, r, w[ib]);
-    }
+    const int ia = 4 * j + k, ib = 4 * (j | D) + k;
+    const uint32_t r = lane_xor<D>(lane_select(hi, w[ib], w[ia]));
+    w[ia] = lane_select(hi, w[ia], r);
+    w[ib] = lane_select(hi, r, w[ib]);
   }
 }
 
-// Store of a lane's last F iterations (8F bytes at byte `off` of its chunk).
-// With F = 16 a lane holds one whole 128-byte line, and an 8-lane butterfly
-// over its 16-byte pieces (xor 1, 2, 4) leaves lane q of an octet with piece
-// q of the line of each of the octet's 8 chunks: store j of the octet then
-// writes the whole line of chunk j, so one store instruction covers 8 lines
-// rather than a 16-byte piece of 64. Every lane takes part in the exchange;
-// only valid streams store.
+// Store of a lane's last F iterations (8F bytes at byte `off` of its
+// chunk, NP = F/2 pieces of 16 bytes). For F of 8 or 16 an NP-lane butterfly
+// (xor 1, 2, 4) leaves lane q of each NP-lane set with piece q of each of the
+// set's NP chunks: store j of the set then writes 8F contiguous bytes of
+// chunk j (a whole 128-byte line for F = 16), so one store instruction
+// covers 64/NP runs rather than 64 separate 16-byte pieces. Every lane takes
+// part in the exchange; only valid streams store.
 template <int F>
 __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64_t chunk, uint32_t li, int64_t off,
                                       bool valid) {
-  if constexpr (F == 16) {
-    const uint32_t q = li & 7u;
-    uint32_t w[32];
+  constexpr int NP = F / 2;
+  if constexpr (NP == 4 || NP == 8) {
+    const uint32_t q = li & (NP - 1);
+    uint32_t w[4 * NP];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NP; ++j) {
       w[4 * j] = ob[j].x;
       w[4 * j + 1] = ob[j].y;
       w[4 * j + 2] = ob[j].z;
       w[4 * j + 3] = ob[j].w;
     }
-    butterfly<1>(w, q);
-    butterfly<2>(w, q);
-    butterfly<4>(w, q);
+    butterfly<1, NP>(w, q);
+    butterfly<2, NP>(w, q);
+    if constexpr (NP == 8) butterfly<4, NP>(w, q);
     if (valid) {
-      uint8_t* base = chunk0 + static_cast<int64_t>(li & ~7u) * chunk + off + 16 * q;
+      uint8_t* base = chunk0 + static_cast<int64_t>(li & ~(NP - 1u)) * chunk + off + 16 * q;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < NP; ++j)
         *reinterpret_cast<uint4*>(base + j * chunk) = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
     }
   } else {
     if (valid) {
       uint4* dst = reinterpret_cast<uint4*>(chunk0 + static_cast<int64_t>(li) * chunk + off);
 #pragma unroll
-      for (int i = 0; i < F / 2; ++i) dst[i] = ob[i];
+      for (int i = 0; i < NP; ++i) dst[i] = ob[i];
     }
   }
 }
 
 template <int F>
 __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
-  __shared__ uint32_t s_pair[XP_LUT_BYTES];
+  __shared__ uint16_t s_lut[XP_LUT_BYTES];
   __shared__ uint32_t s_ring[kGroupsPerBlock][kRingPad];
 
   const int j = blockIdx.x / a.blocks_per_row;
@@ -314,16 +277,14 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 
   const int tid = threadIdx.x;
   const uint8_t* lut = a.lut + (e * a.num_names + name) * XP_LUT_BYTES;
-  // Pair table from the row's 9-bit table (entry = symbol << 4 | length).
-  // Lengths are clamped to [1, LIMIT], which leaves a valid table as it is
-  // and keeps the refill bound (and so every ring read in range) for any.
+  // The row's 9-bit table (entry = symbol << 4 | length) as length |
+  // (exponent field << 3) << 8. Lengths are clamped to [1, LIMIT], which
+  // leaves a valid table as it is and keeps the refill bound (and so every
+  // ring read in range) for any table.
   for (int i = tid; i < XP_LUT_BYTES; i += kThreads) {
     const uint32_t ent = lut[i];
-    const uint32_t l1 = min(max(ent & 15u, 1u), static_cast<uint32_t>(kLimit));
-    const uint32_t ent2 = lut[static_cast<uint32_t>(i) >> l1];
-    const uint32_t l2 = min(max(ent2 & 15u, 1u), static_cast<uint32_t>(kLimit));
-    const bool two = l1 + l2 <= static_cast<uint32_t>(kLimit);
-    s_pair[i] = l1 | (two ? (l1 + l2) << 4 : 0u) | ((ent >> 4) << 19) | (two ? (ent2 >> 4) << 27 : 0u);
+    const uint32_t len = min(max(ent & 15u, 1u), static_cast<uint32_t>(kLimit));
+    s_lut[i] = static_cast<uint16_t>(len | (((ent >> 4) << 3) << 8));
   }
 
   const int wave = tid >> 6, lane = tid & 63;
@@ -390,19 +351,11 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   __syncthreads();
   // The refill before symbol 0: every lane of a group takes one word, in
   // lane order.
-#pragma unroll
-  for (int c = 0; c < kChains; ++c) {
-    Chain& h = ch[c];
-    h.buf = static_cast<uint64_t>(h.ring[li]) << 32;
-    h.pos = 32u;
-    h.rp = 32u;
-  }
 
   // Output: a lane's chunk is contiguous, produced 8 bytes per iteration.
-  // F iterations (one 128-byte line when F is 16) are gathered in registers
-  // and stored together (see flush): lines written piecemeal far apart in
-  // time leave the caches as partial writes, which costs more than the
-  // decode itself.
+  // F iterations (8F bytes) are gathered in registers and stored together
+  // (see flush): lines written in 16-byte pieces far apart in time leave the
+  // caches as partial writes, which cost more than the decode itself.
   uint4 ob[kChains][F / 2];
 #pragma unroll
   for (int c = 0; c < kChains; ++c)
@@ -428,13 +381,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int c = 0; c < kChains; ++c) decode_pair<0>(ch[c].buf, ch[c].pos, ab[c], o[c].x, low, half_shift, s_pair);
+        for (int k = 0; k < 2; ++k) {
 #pragma unroll
-        for (int c = 0; c < kChains; ++c) decode_pair<2>(ch[c].buf, ch[c].pos, ab[c], o[c].x, low, half_shift, s_pair);
-#pragma unroll
-        for (int c = 0; c < kChains; ++c) decode_pair<0>(ch[c].buf, ch[c].pos, ab[c], o[c].y, low, half_shift, s_pair);
-#pragma unroll
-        for (int c = 0; c < kChains; ++c) decode_pair<2>(ch[c].buf, ch[c].pos, ab[c], o[c].y, low, half_shift, s_pair);
+          for (int c = 0; c < kChains; ++c) {
+            uint32_t& ow = k ? o[c].y : o[c].x;
+            decode_symbol<0>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
+            decode_symbol<1>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
+            decode_symbol<2>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
+            decode_symbol<3>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
+          }
+        }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int c = 0; c < kChains; ++c) half_end(ch[c], li, ab[c]);
@@ -510,9 +466,9 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
   a.blocks_per_row = per_row;
   const int64_t grid = K * per_row;
   XP_REQUIRE(grid <= (int64_t(1) << 31) - 1, "xp_decode_rows: grid too large");
-  // Whole 128-byte lines per lane and store when the chunk allows it.
-  if (chunk % 128 == 0)
-    hipLaunchKernelGGL(decode_kernel<16>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
+  // 64 bytes per lane and store (4-lane runs) when the chunk allows it.
+  if (chunk % 64 == 0)
+    hipLaunchKernelGGL(decode_kernel<8>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
   else
     hipLaunchKernelGGL(decode_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
   return check_launch("decode_kernel");
