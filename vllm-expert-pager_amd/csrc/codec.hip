@@ -159,29 +159,41 @@ __device__ __forceinline__ void or_byte(uint32_t& out, uint32_t e) {
         : "+v"(out) : "v"(e));
 }
 
+// pos + (byte 0 of e) as one byte-select add.
+__device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
+  uint32_t r;
+  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+      : "=v"(r) : "v"(e), "v"(pos));
+  return r;
+}
+
 // One symbol of one stream, without branches: every lane reads a ring word
-// at its refill address and keeps it only if it refills. `low` is all ones
-// in the lower half-wave and zero in the upper one; s_lut holds
-// len | (symbol << 3) << 8 per 9-bit code.
+// at its refill address and keeps it only if it refills. s_lut holds
+// len | (symbol << 3) << 8 per 9-bit code. off_lo and off_hi are the LDS
+// byte addresses of the next unread ring word of the groups of the lower
+// and upper half-wave (wave-uniform, so they advance in scalar registers).
+// A lane's refill word is (refilling lanes below it in its half) words on;
+// mbcnt over the whole ballot also counts, for an upper-half lane, every
+// refilling lane of the lower half, so that half's base is lowered by as
+// many words and one bit-field extract picks each lane's base.
 template <int K>
-__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& ab, uint32_t& out,
-                                              uint32_t low, uint32_t half_shift, const uint16_t* s_lut) {
-  const bool refill = pos > 64u - kLimit;
-  const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
+__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& off_lo, uint32_t& off_hi,
+                                              uint32_t& out, uint32_t half_shift, const uint16_t* s_lut) {
+  const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 64u - kLimit);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
-  // Refilling lanes below this one in its half: for the upper half the
-  // lower half's count (all of m_lo) is masked off before counting m_hi.
-  const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u) & low);
-  const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(ab + 4u * below);
+  const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
+  const uint32_t bases = off_lo | ((off_hi - 4u * n_lo) << 16);
+  const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u));
+  const uint32_t addr = __builtin_amdgcn_ubfe(bases, half_shift, 16u) + 4u * below;
+  const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(addr);
+  off_lo += 4u * n_lo;
+  off_hi += 4u * n_hi;
   const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
   const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
-  pos = lane_select(mask, pos, pos - 32u);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
-  const uint32_t counts = static_cast<uint32_t>(__popc(m_lo)) | (static_cast<uint32_t>(__popc(m_hi)) << 16);
-  ab += 4u * __builtin_amdgcn_ubfe(counts, half_shift, 16u);
-  const uint32_t idx = static_cast<uint32_t>(buf >> (pos & 63u)) & (XP_LUT_BYTES - 1);
-  const uint32_t e = s_lut[idx];
-  pos += e & 0xffu;
+  const uint32_t pr = pos + lane_select(mask, 0u, ~31u);  // pos - 32 in refilling lanes
+  const uint32_t e = s_lut[static_cast<uint32_t>(buf >> (pr & 63u)) & (XP_LUT_BYTES - 1)];
+  pos = add_byte0(pr, e);
   or_byte<K & 3>(out, e);
 }
 
@@ -291,7 +303,6 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   const bool upper = lane >= 32;
   const uint32_t li = lane & 31;
   const uint32_t half_shift = upper ? 16u : 0u;
-  const uint32_t low = upper ? 0u : ~0u;
   const int G = nm.G;
   const int msteps = a.chunk / 8;
   const uint32_t* rec = reinterpret_cast<const uint32_t*>(nm.stg + int64_t(j) * nm.pitch);
@@ -373,11 +384,13 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
         o[c] = nibble_template(x);
       }
       {
-        uint32_t ab[kChains];
+        // The next unread ring word of each half's group, in scalar registers.
+        uint32_t off_lo[kChains], off_hi[kChains];
 #pragma unroll
         for (int c = 0; c < kChains; ++c) {
           half_begin(ch[c], li);
-          ab[c] = ch[c].ab0;
+          off_lo[c] = __builtin_amdgcn_readlane(ch[c].ab0, 0);
+          off_hi[c] = __builtin_amdgcn_readlane(ch[c].ab0, 32);
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -385,15 +398,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 #pragma unroll
           for (int c = 0; c < kChains; ++c) {
             uint32_t& ow = k ? o[c].y : o[c].x;
-            decode_symbol<0>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
-            decode_symbol<1>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
-            decode_symbol<2>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
-            decode_symbol<3>(ch[c].buf, ch[c].pos, ab[c], ow, low, half_shift, s_lut);
+            decode_symbol<0>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
+            decode_symbol<1>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
+            decode_symbol<2>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
+            decode_symbol<3>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
           }
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int c = 0; c < kChains; ++c) half_end(ch[c], li, ab[c]);
+        for (int c = 0; c < kChains; ++c)
+          half_end(ch[c], li, __builtin_amdgcn_ubfe(off_lo[c] | (off_hi[c] << 16), half_shift, 16u));
       }
 #pragma unroll
       for (int c = 0; c < kChains; ++c) {
