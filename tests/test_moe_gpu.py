@@ -201,6 +201,22 @@ def test_chunked_equals_one_shot_prefill_2048x8():
     _check_close(one[sample].float().cpu().numpy(), ref, "prefill sample")
 
 
+def test_small_batches_match_a_large_batch():
+    """A token's output depends on its own pairs only: batches of 1 and 5 tokens
+    (small-batch kernels) give the bits of the same tokens in a 300-token batch
+    (prefill kernels)."""
+    moe = _moe()
+    E, H, I, T, topk = 64, 2048, 512, 300, 8
+    x, tw, ids, w13, w13s, w2, w2s = _case(11, E, H, I, T, topk)
+    xb = _bf16(x)
+    tw_t, ids_t, w13_t, w13s_t, w2_t, w2s_t = _dev(tw, ids, w13, w13s, w2, w2s)
+    big = moe.fused_moe(xb, tw_t, ids_t, w13_t, w13s_t, w2_t, w2s_t)
+    for a, b in ((0, 1), (7, 8), (100, 105), (295, 300)):
+        small = moe.fused_moe(xb[a:b].contiguous(), tw_t[a:b].contiguous(), ids_t[a:b].contiguous(),
+                              w13_t, w13s_t, w2_t, w2s_t)
+        assert torch.equal(small.view(torch.int16), big[a:b].view(torch.int16)), (a, b)
+
+
 @pytest.mark.parametrize("T, topk, E, slots", [(1, 8, 256, 32), (37, 4, 20, 12), (513, 8, 64, 64)])
 def test_quant_route_matches_separate_calls(T, topk, E, slots):
     moe = _moe()

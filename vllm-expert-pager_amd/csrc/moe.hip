@@ -294,6 +294,7 @@ inline int64_t work_layout(int64_t npairs, int64_t I, Work* w, uint8_t* base) {
 constexpr int kC1 = 32;       // activation columns per narrow gemm1 workgroup
 constexpr int kWideTiles = 64;  // tile bound from which gemm1 uses the wide workgroups
 constexpr int kWideNW = 8;      // waves (16 activation columns each) of a wide gemm1 workgroup
+constexpr int kNarrowChunk = 4; // K blocks per load chunk of the small-batch GEMMs
 constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I <= 8192)
 
 constexpr int kAPitch = 144;  // LDS bytes per staged A row (128 + 16 against bank conflicts)
@@ -467,6 +468,235 @@ __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restric
     if (p >= 0)
       *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
           *reinterpret_cast<const u32x4*>(s_o + row * NC + piece * 8);
+  }
+}
+
+// Operands of one K block of a 16-row subtile for one wave: the A rows (the
+// lane's row j, bytes 32q..32q+31) and two 16-row blocks of B rows.
+struct KBlock {
+  u32x4 a[2];
+  u32x4 b[2][2];
+};
+
+// CH consecutive K blocks from kb0, the block index clamped at KB - 1 so
+// that the loads are unconditional (a clamped block is loaded, not used).
+template <int CH>
+__device__ __forceinline__ void load_chunk(KBlock (&c)[CH], const uint8_t* arow, const uint8_t* const (&brow)[2],
+                                           int kb0, int KB) {
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int kb = kb0 + i < KB ? kb0 + i : KB - 1;
+    load32(arow + kb * kKB, c[i].a);
+    load32(brow[0] + kb * kKB, c[i].b[0]);
+    load32(brow[1] + kb * kKB, c[i].b[1]);
+  }
+}
+
+// The rows of one 16-row subtile (r0 = its first row in the tile): the
+// pair of each row (-1 for padding) and the operand row it reads (padding
+// repeats the subtile's first pair).
+__device__ __forceinline__ void subtile_rows(const Tile& tile, int r0, const int32_t* pairs, int div, int* s_pair,
+                                             int* s_row) {
+  const int tid = threadIdx.x;
+  if (tid < 16) {
+    const int n = tile.count - r0;
+    const int p = pairs[tile.first + r0 + (tid < n ? tid : 0)];
+    s_pair[tid] = tid < n ? p : -1;
+    s_row[tid] = p / div;
+  }
+}
+
+// Runs the K blocks of a subtile through `step`, CH blocks per chunk, the
+// next chunk's loads in flight while the current one is multiplied.
+template <int CH, typename Step>
+__device__ __forceinline__ void run_chunks(const uint8_t* arow, const uint8_t* const (&brow)[2], int KB, Step step) {
+  KBlock c0[CH], c1[CH];
+  load_chunk<CH>(c0, arow, brow, 0, KB);
+  if (KB <= CH) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      if (i < KB) step(c0[i], i);
+    return;
+  }
+  for (int kc = 0; kc < KB; kc += 2 * CH) {
+    load_chunk<CH>(c1, arow, brow, kc + CH, KB);
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      if (kc + i < KB) step(c0[i], kc + i);
+    load_chunk<CH>(c0, arow, brow, kc + 2 * CH, KB);
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      if (kc + CH + i < KB) step(c1[i], kc + CH + i);
+  }
+}
+
+// GEMM1 for small batches (decode): one 16-row subtile of a tile x 32
+// activation columns, 2 waves x 16 columns. Every operand is loaded straight
+// from global memory, CH K blocks ahead of the MFMAs, so a lone wave is not
+// bound by one load latency per K block. Each column's sum runs over the K
+// blocks in the same order and with the same scaling as in gemm1_kernel,
+// so the bits are the same. 1-D grid in XCD order over (subtile, column
+// block) items.
+template <int CH>
+__global__ void __launch_bounds__(128) gemm1_narrow_kernel(const uint8_t* __restrict__ xq,
+                                                           const float* __restrict__ xs, int64_t H, int64_t I,
+                                                           int topk, const uint8_t* __restrict__ w13,
+                                                           const float* __restrict__ w13_scale,
+                                                           const int32_t* __restrict__ offsets,
+                                                           const int32_t* __restrict__ pairs,
+                                                           const int32_t* __restrict__ tiles, Work work) {
+  __shared__ int s_row[16];
+  __shared__ int s_pair[16];
+  __shared__ float s_xs[16 * kMaxKB];
+  __shared__ float s_sw[2][kMaxKB];
+  __shared__ float s_m[2][16];
+  __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * 32];
+
+  const int ncb = static_cast<int>(I / 32);
+  Tile tile;
+  int ti, item;
+  xcd_item(4 * ncb, ti, item);
+  if (!load_tile_at(ti, tiles, offsets, tile)) return;
+  const int sub = item / ncb, r0 = 16 * sub;
+  if (r0 >= tile.count) return;
+  const int c0 = (item - sub * ncb) * 32;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const int KB = static_cast<int>(H / kKB);
+
+  subtile_rows(tile, r0, pairs, topk, s_pair, s_row);
+  __syncthreads();
+  for (int i = tid; i < 16 * KB; i += 128) {
+    const int r = i / KB, kb = i - r * KB;
+    s_xs[i] = xs[static_cast<int64_t>(s_row[r]) * KB + kb];
+  }
+  {
+    const float* sg = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + c0 / kKB) * KB;
+    const float* su = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
+    for (int i = tid; i < 2 * KB; i += 128) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
+  }
+  const uint8_t* arow = xq + static_cast<int64_t>(s_row[j]) * H + 32 * q;
+  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
+  const int64_t n = c0 + 16 * wave + j;
+  const uint8_t* const brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
+  __syncthreads();  // s_xs, s_sw
+
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  run_chunks<CH>(arow, brow, KB, [&](const KBlock& k, int kb) {
+    const float g = s_sw[0][kb], u = s_sw[1][kb];
+    float sc[2][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float sa = s_xs[(4 * q + r) * KB + kb];
+      sc[0][r] = sa * g;
+      sc[1][r] = sa * u;
+    }
+#pragma unroll
+    for (int si = 0; si < 2; ++si) {
+      const f32x4 part = mfma_k128(k.a, k.b[si]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[si][r] = fmaf(part[r], sc[si][r], acc[si][r]);
+    }
+  });
+
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
+    const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+    float m = fabsf(a);
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+    const int row = 4 * q + r;
+    if (j == 0) s_m[wave][row] = m;
+    s_o[row * 32 + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(a));
+  }
+  __syncthreads();
+  if (tid < 16) {
+    const int p = s_pair[tid];
+    if (p >= 0) work.amax32[static_cast<int64_t>(p) * (I / 32) + c0 / 32] = fmaxf(s_m[0][tid], s_m[1][tid]);
+  }
+  if (tid < 64) {  // 16 rows x 4 pieces of 16 bytes
+    const int row = tid >> 2, piece = tid & 3;
+    const int p = s_pair[row];
+    if (p >= 0)
+      *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
+          *reinterpret_cast<const u32x4*>(s_o + row * 32 + piece * 8);
+  }
+}
+
+// GEMM2 for small batches: one 16-row subtile x 128 output columns (4 waves
+// x 32), operands straight from global memory CH K blocks ahead; same sums
+// and rounding as gemm2_kernel.
+template <int CH>
+__global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64_t I,
+                                                                const float* __restrict__ topk_weight,
+                                                                const uint8_t* __restrict__ w2,
+                                                                const float* __restrict__ w2_scale,
+                                                                const int32_t* __restrict__ offsets,
+                                                                const int32_t* __restrict__ pairs,
+                                                                const int32_t* __restrict__ tiles, Work work,
+                                                                uint16_t* __restrict__ out) {
+  __shared__ int s_row[16];
+  __shared__ int s_pair[16];
+  __shared__ float s_as[16 * kMaxKB];
+  __shared__ float s_w[16];
+  __shared__ float s_sw[kMaxKB];
+  __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * kBN];
+
+  const int ncb = static_cast<int>(H / kBN);
+  Tile tile;
+  int ti, item;
+  xcd_item(4 * ncb, ti, item);
+  if (!load_tile_at(ti, tiles, offsets, tile)) return;
+  const int sub = item / ncb, r0 = 16 * sub;
+  if (r0 >= tile.count) return;
+  const int n0 = (item - sub * ncb) * kBN;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const int KB = static_cast<int>(I / kKB);
+
+  subtile_rows(tile, r0, pairs, 1, s_pair, s_row);
+  __syncthreads();
+  for (int i = tid; i < 16 * KB; i += kThreads) {
+    const int r = i / KB, kb = i - r * KB;
+    s_as[i] = work.acts[static_cast<int64_t>(s_row[r]) * KB + kb];
+  }
+  if (tid < 16) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
+  if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
+  const uint8_t* arow = work.act + static_cast<int64_t>(s_row[j]) * I + 32 * q;
+  const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
+  const uint8_t* const brow[2] = {wslot + static_cast<int64_t>(n0 + 32 * wave + j) * I + 32 * q,
+                                  wslot + static_cast<int64_t>(n0 + 32 * wave + 16 + j) * I + 32 * q};
+  __syncthreads();  // s_as, s_w, s_sw
+
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  run_chunks<CH>(arow, brow, KB, [&](const KBlock& k, int kb) {
+    const float w = s_sw[kb];
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = s_as[(4 * q + r) * KB + kb] * w;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f32x4 part = mfma_k128(k.a, k.b[t]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(part[r], sc[r], acc[t][r]);
+    }
+  });
+
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * q + r;
+    const float wgt = s_w[row];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) s_o[row * kBN + 32 * wave + 16 * t + j] = static_cast<uint16_t>(bf16_bits(acc[t][r] * wgt));
+  }
+  __syncthreads();
+  {  // 16 rows x 16 pieces of 16 bytes: one pass of the 256 threads
+    const int row = tid >> 4, col = (tid & 15) * 8;
+    const int p = s_pair[row];
+    if (p >= 0)
+      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
+          *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
   }
 }
 
@@ -745,22 +975,32 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   // Prefill-sized calls take 16*kWideNW activation columns per workgroup
   // (token rows shared by more waves), small calls 32 (more workgroups for
   // few pairs). Every column is computed the same way in both.
-  if (bound >= kWideTiles && I % (16 * kWideNW) == 0) {
+  const bool narrow = bound < kWideTiles;
+  if (!narrow && I % (16 * kWideNW) == 0) {
     const int64_t g1w = tiles8 * (I / (16 * kWideNW));
     hipLaunchKernelGGL(gemm1_kernel<kWideNW>, dim3(static_cast<unsigned>(g1w)), dim3(64 * kWideNW), 0,
                        as_stream(stream), xq, xs,
                        H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
-  } else {
+  } else if (!narrow) {
     hipLaunchKernelGGL(gemm1_kernel<2>, dim3(static_cast<unsigned>(g1)), dim3(128), 0, as_stream(stream), xq, xs, H,
                        I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
+  } else {
+    // Few pairs: 16-row subtiles, operands loaded several K blocks ahead.
+    hipLaunchKernelGGL(gemm1_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(4 * g1)), dim3(128), 0,
+                       as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs,
+                       tiles, w);
   }
   int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles, w);
   rc = check_launch("act_quant_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, as_stream(stream), H, I,
-                     topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
+  if (narrow)
+    hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(4 * g2)), dim3(kThreads), 0,
+                       as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
+  else
+    hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, as_stream(stream), H, I,
+                       topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
   return check_launch("gemm2_kernel");
 }
 
