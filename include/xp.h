@@ -234,6 +234,20 @@ int xp_encode_row(const uint8_t* raw, int64_t n, int64_t chunk,
                   uint8_t* record, int64_t pitch, uint8_t* lut,
                   int64_t* needed);
 
+/* GPU encoder: compress `rows` device rows (raw + r*raw_stride, n values
+ * each, n a multiple of chunk*32, chunk a power of two in 16..1024) into
+ * records + r*pitch (zero padded) and luts + r*lut_stride (512 bytes), the
+ * bytes xp_encode_row writes. needed[r] (device) receives each record's used
+ * bytes; a row whose needed[r] exceeds pitch writes only its LUT, and the
+ * caller reports it as xp_encode_row's XP_E_PITCH. All pointers are device
+ * memory; enqueued on `stream`.
+ * Replaces encode (codec.py:125-198), called per row at load time
+ * (store.py:588). */
+int xp_encode_rows(const uint8_t* raw, int64_t rows, int64_t raw_stride,
+                   int64_t n, int64_t chunk, uint8_t* records, int64_t pitch,
+                   uint8_t* luts, int64_t lut_stride, int64_t* needed,
+                   void* stream);
+
 /* Code of a 16-symbol histogram: lengths[16], bit-reversed codes[16] and
  * lut[512] ((sym << 4) | len). Replaces code_lengths / Code
  * (codec.py:61-114). */

@@ -39,9 +39,9 @@ GPU_FLAGS = [
 ]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
-GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "moe.hip"]
-HIP_HOST_SOURCES = ["host.cpp"]  # uses the HIP runtime API
-HOST_SOURCES = ["codec_host.cpp", "ssd.cpp"]
+GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "encode.hip", "moe.hip"]
+HIP_HOST_SOURCES = ["host.cpp", "codec_host.cpp"]  # HIP runtime API or headers
+HOST_SOURCES = ["ssd.cpp"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

@@ -2,11 +2,8 @@
 //
 // The record layout, the code construction and the Huffman word order are
 // fixed by the format, so this follows the reference's rules step for step:
-//   - length-limited Huffman lengths: merge the two lightest (count, id)
-//     nodes, new ids from 16 up; if a length exceeds LIMIT, raise every count
-//     to sum / 2^(LIMIT - k) and retry (codec.py:61-87);
-//   - canonical codes in (length, symbol) order, stored bit-reversed, and a
-//     512-entry LUT of (symbol << 4) | length (codec.py:90-114);
+//   - the code (lengths, canonical bit-reversed codes, LUT) as in
+//     code_build.h (codec.py:61-114);
 //   - record = int32 gstart[G+1] | sign/mantissa nibble words in
 //     (group, word, lane) order | Huffman words per group in refill order
 //     (codec.py:125-193).
@@ -14,13 +11,12 @@
 // whenever fewer than LIMIT bits are buffered) over each chunk's code
 // lengths, which yields the same (symbol index, lane) order as the
 // reference's searchsorted formulation.
-#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <vector>
 
-#include "../../include/xp.h"
+#include "code_build.h"
 
 namespace xp {
 int fail(int code, const char* fmt, ...);
@@ -28,77 +24,11 @@ int fail(int code, const char* fmt, ...);
 
 namespace {
 
-constexpr int kSyms = 16;
-
-void huffman_lengths(const double* counts, int32_t* lengths) {
-  struct Node {
-    double c;
-    int id;
-    uint32_t members;  // bit s set: symbol s is under this node
-  };
-  std::vector<Node> heap;
-  for (int i = 0; i < kSyms; ++i) heap.push_back(Node{counts[i], i, 1u << i});
-  for (int i = 0; i < kSyms; ++i) lengths[i] = 0;
-  int next_id = kSyms;
-  auto lighter = [](const Node& a, const Node& b) { return a.c < b.c || (a.c == b.c && a.id < b.id); };
-  while (heap.size() > 1) {
-    Node pick[2];
-    for (int t = 0; t < 2; ++t) {
-      size_t best = 0;
-      for (size_t i = 1; i < heap.size(); ++i)
-        if (lighter(heap[i], heap[best])) best = i;
-      pick[t] = heap[best];
-      heap.erase(heap.begin() + static_cast<long>(best));
-    }
-    const uint32_t m = pick[0].members | pick[1].members;
-    for (int s = 0; s < kSyms; ++s)
-      if (m & (1u << s)) ++lengths[s];
-    heap.push_back(Node{pick[0].c + pick[1].c, next_id++, m});
-  }
-}
-
-void code_lengths(const int64_t* hist, int32_t* lengths) {
-  double counts[kSyms];
-  for (int i = 0; i < kSyms; ++i) counts[i] = static_cast<double>(hist[i] > 1 ? hist[i] : 1);
-  for (int k = 0;; ++k) {
-    if (k > 0) {
-      double sum = 0.0;
-      for (int i = 0; i < kSyms; ++i) sum += counts[i];
-      const double floor_c = sum / std::ldexp(1.0, XP_LIMIT - k);
-      for (int i = 0; i < kSyms; ++i) counts[i] = counts[i] > floor_c ? counts[i] : floor_c;
-    }
-    huffman_lengths(counts, lengths);
-    int mx = 0;
-    for (int i = 0; i < kSyms; ++i) mx = lengths[i] > mx ? lengths[i] : mx;
-    if (mx <= XP_LIMIT) return;
-  }
-}
+constexpr int kSyms = xp::code::kSyms;
 
 int build_code(const int64_t* hist, int32_t* lengths, int32_t* codes, uint8_t* lut) {
-  code_lengths(hist, lengths);
-  int order[kSyms];
-  for (int i = 0; i < kSyms; ++i) order[i] = i;
-  for (int i = 1; i < kSyms; ++i)  // insertion sort by (length, symbol)
-    for (int k = i; k > 0 && (lengths[order[k]] < lengths[order[k - 1]] ||
-                              (lengths[order[k]] == lengths[order[k - 1]] && order[k] < order[k - 1]));
-         --k) {
-      int t = order[k];
-      order[k] = order[k - 1];
-      order[k - 1] = t;
-    }
-  uint32_t canon[kSyms] = {0};
-  uint32_t code = 0;
-  for (int i = 0; i < kSyms; ++i) {
-    const int s = order[i];
-    if (i) code = (code + 1) << (lengths[s] - lengths[order[i - 1]]);
-    canon[s] = code;
-  }
-  for (int s = 0; s < kSyms; ++s) {
-    uint32_t rev = 0;
-    for (int b = 0; b < lengths[s]; ++b)
-      if (canon[s] & (1u << b)) rev |= 1u << (lengths[s] - 1 - b);
-    codes[s] = static_cast<int32_t>(rev);
-  }
+  xp::code::code_lengths(hist, lengths);
+  xp::code::canonical_codes(lengths, codes);
   int16_t table[XP_LUT_BYTES];
   for (int i = 0; i < XP_LUT_BYTES; ++i) table[i] = -1;
   for (int s = 0; s < kSyms; ++s) {

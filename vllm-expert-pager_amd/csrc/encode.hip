@@ -1,0 +1,262 @@
+// Batched GPU encoder of the fp8 exponent Huffman row format
+// (encode, codec.py:125-198), one workgroup per row, producing the bytes of
+// the host encoder (codec_host.cpp) and of the reference.
+//
+// Per row:
+//   1. exponent histogram: per-thread counters in LDS, then summed;
+//   2. the code (code_build.h) by one thread, the 512-entry LUT by all;
+//   3. Huffman words per chunk: the decoder loads a word before symbol i
+//      whenever fewer than LIMIT bits are left, so a chunk whose last symbol
+//      starts at bit b needs (b + LIMIT - 1) / 32 + 1 words; summed per
+//      group and scanned into gstart;
+//   4. each 32-lane half-wave encodes one group: its lanes walk their chunks
+//      in lockstep, run the decoder's refill rule, and give each word the
+//      (symbol index, lane) rank of its refill -- the wave ballot's count of
+//      refilling lanes below, as the decoder computes it. A lane emits a
+//      word once its 32 bits are complete; at most two refills are waiting
+//      for their word. The lane also writes its sign/mantissa nibble words.
+// The record is written whole: gstart, nibbles, Huffman words and a zero
+// tail up to the pitch. A row that does not fit its pitch writes nothing
+// but its LUT and needed bytes.
+#include "code_build.h"
+#include "common.h"
+
+namespace xp {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxGroups = 4096;  // groups per row a workgroup scans in LDS
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct EncodeArgs {
+  const uint8_t* raw;
+  int64_t raw_stride;  // bytes between rows of raw
+  int64_t n;           // values per row
+  int chunk;           // values per lane chunk (a power of two, 16..1024)
+  int G;               // groups per row
+  uint8_t* rec;
+  int64_t pitch;       // bytes between records, the record size
+  uint8_t* lut;
+  int64_t lut_stride;  // bytes between LUTs
+  int64_t* needed;     // record bytes each row needs
+};
+
+// Lengths of the four bytes of w as a sum, from 16 4-bit lengths packed
+// in lens (symbol s in bits 4s..4s+3).
+__device__ __forceinline__ uint32_t sum_lengths4(uint32_t w, uint64_t lens) {
+  uint32_t t = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) t += static_cast<uint32_t>(lens >> (4 * ((w >> (8 * b + 3)) & 15u))) & 15u;
+  return t;
+}
+
+__global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
+  __shared__ uint32_t s_hist[code::kSyms][kThreads];  // per-thread counters
+  __shared__ int32_t s_len[code::kSyms];
+  __shared__ uint32_t s_tab[code::kSyms];              // code | length << 16
+  __shared__ int32_t s_words[kMaxGroups + 1];          // words per group, then gstart
+  __shared__ int64_t s_total;
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const uint8_t* raw = a.raw + static_cast<int64_t>(row) * a.raw_stride;
+  uint8_t* rec = a.rec + static_cast<int64_t>(row) * a.pitch;
+  const int64_t n = a.n;
+  const int chunk = a.chunk, G = a.G;
+
+  // 1. Histogram of the exponent fields.
+  for (int s = 0; s < code::kSyms; ++s) s_hist[s][tid] = 0;
+  for (int64_t off = int64_t(tid) * 16; off < n; off += int64_t(kThreads) * 16) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(raw + off);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) ++s_hist[(w[k] >> (8 * b + 3)) & 15u][tid];
+  }
+  __syncthreads();
+
+  // 2. The code, and the LUT.
+  if (tid < code::kSyms) {
+    uint32_t t = 0;
+    for (int i = 0; i < kThreads; ++i) t += s_hist[tid][i];
+    s_hist[tid][0] = t;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int64_t hist[code::kSyms];
+    for (int s = 0; s < code::kSyms; ++s) hist[s] = s_hist[s][0];
+    int32_t lengths[code::kSyms], codes[code::kSyms];
+    code::code_lengths(hist, lengths);
+    code::canonical_codes(lengths, codes);
+    for (int s = 0; s < code::kSyms; ++s) {
+      s_len[s] = lengths[s];
+      s_tab[s] = static_cast<uint32_t>(codes[s]) | (static_cast<uint32_t>(lengths[s]) << 16);
+    }
+  }
+  __syncthreads();
+  {
+    int32_t lengths[code::kSyms], codes[code::kSyms];
+    for (int s = 0; s < code::kSyms; ++s) {
+      lengths[s] = s_len[s];
+      codes[s] = static_cast<int32_t>(s_tab[s] & 0xffffu);
+    }
+    uint8_t* lut = a.lut + static_cast<int64_t>(row) * a.lut_stride;
+    for (int x = tid; x < XP_LUT_BYTES; x += kThreads) lut[x] = static_cast<uint8_t>(code::lut_entry(lengths, codes, x));
+  }
+  uint64_t lens = 0;
+  for (int s = 0; s < code::kSyms; ++s) lens |= static_cast<uint64_t>(s_len[s]) << (4 * s);
+
+  // 3. Words per chunk: (start bit of its last symbol + LIMIT - 1) / 32 + 1.
+  // The chunk's 16-byte pieces are spread over consecutive threads, so each
+  // chunk is summed by a power-of-two set of lanes of one wave.
+  const int per = chunk / 16;  // threads per chunk
+  for (int g = tid; g < G; g += kThreads) s_words[g] = 0;
+  __syncthreads();
+  for (int64_t off = int64_t(tid) * 16; off < n; off += int64_t(kThreads) * 16) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(raw + off);
+    uint32_t bits = sum_lengths4(v.x, lens) + sum_lengths4(v.y, lens) + sum_lengths4(v.z, lens) +
+                    sum_lengths4(v.w, lens);
+    const bool last = ((off + 16) % chunk) == 0;
+    if (last) bits -= static_cast<uint32_t>(lens >> (4 * ((v.w >> 27) & 15u))) & 15u;  // not the last symbol
+    for (int d = 1; d < per; d <<= 1) bits += __shfl_xor(bits, d, per);
+    if (last) atomicAdd(&s_words[off / (int64_t(chunk) * XP_LANES)], static_cast<int32_t>((bits + XP_LIMIT - 1) / 32 + 1));
+  }
+  __syncthreads();
+  if (tid == 0) {  // exclusive scan into gstart
+    int64_t t = 0;
+    for (int g = 0; g < G; ++g) {
+      const int32_t w = s_words[g];
+      s_words[g] = static_cast<int32_t>(t);
+      t += w;
+    }
+    s_words[G] = static_cast<int32_t>(t);
+    s_total = t;
+  }
+  __syncthreads();
+  const int64_t head = 4 * (int64_t(G) + 1) + n / 2;
+  const int64_t nbytes = head + 4 * s_total;
+  if (tid == 0) a.needed[row] = nbytes;
+  if (nbytes > a.pitch) return;
+
+  int32_t* gstart = reinterpret_cast<int32_t*>(rec);
+  for (int g = tid; g <= G; g += kThreads) gstart[g] = s_words[g];
+  // Zero tail (nbytes and the pitch are multiples of 4).
+  for (int64_t i = nbytes / 4 + tid; i < a.pitch / 4; i += kThreads) reinterpret_cast<uint32_t*>(rec)[i] = 0;
+
+  // 4. Groups, one per half-wave.
+  uint32_t* fixed = reinterpret_cast<uint32_t*>(rec + 4 * (int64_t(G) + 1));
+  uint32_t* huff = reinterpret_cast<uint32_t*>(rec + head);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const bool upper = lane >= 32;
+  const uint32_t li = lane & 31;
+  const uint32_t low = upper ? 0u : ~0u;
+  const int mwords = chunk / 8;
+  const uint32_t total = static_cast<uint32_t>(s_total);  // every word position is below it
+  for (int g0 = 2 * wave; g0 < G; g0 += 2 * (kThreads / 64)) {
+    const int g = g0 + (upper ? 1 : 0);
+    const bool live = g < G;  // a spare half-wave walks the last group and writes nothing
+    const int gg = live ? g : G - 1;
+    const uint8_t* src = raw + (int64_t(gg) * XP_LANES + li) * chunk;
+    uint32_t* fx = fixed + int64_t(gg) * mwords * XP_LANES + li;
+    // Word positions of the two half-waves' groups, uniform per half.
+    uint32_t base_lo = static_cast<uint32_t>(s_words[g0]);
+    uint32_t base_hi = static_cast<uint32_t>(s_words[g0 + 1 < G ? g0 + 1 : G - 1]);
+    uint32_t level = 0;         // bits the decoder has buffered
+    uint64_t acc = 0;           // bits of the lane's stream not yet emitted
+    uint32_t accbits = 0;
+    uint32_t q0 = 0, q1 = 0;    // positions of words refilled but not yet emitted
+    uint32_t qn = 0;
+    for (int i0 = 0; i0 < chunk; i0 += 16) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(src + i0);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t e = (w[k] >> (8 * b + 3)) & 15u;
+          const bool refill = level < static_cast<uint32_t>(XP_LIMIT);
+          const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
+          const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
+          const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u) & low);
+          if (refill) {
+            const uint32_t pos = (upper ? base_hi : base_lo) + below;
+            if (qn == 0)
+              q0 = pos;
+            else
+              q1 = pos;
+            ++qn;
+            level += 32;
+          }
+          base_lo += static_cast<uint32_t>(__popc(m_lo));
+          base_hi += static_cast<uint32_t>(__popc(m_hi));
+          const uint32_t t = s_tab[e];
+          const uint32_t len = t >> 16;
+          acc |= static_cast<uint64_t>(t & 0xffffu) << accbits;
+          accbits += len;
+          level -= len;
+          if (accbits >= 32) {  // word q0 is complete
+            if (live && q0 < total) huff[q0] = static_cast<uint32_t>(acc);
+            acc >>= 32;
+            accbits -= 32;
+            q0 = q1;
+            --qn;
+          }
+        }
+        if (k & 1) {  // 8 values: one nibble word, value j in bits 4j..4j+3
+          const uint32_t x0 = w[k - 1], x1 = w[k];
+          uint32_t nib = 0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t byte = ((j < 4 ? x0 : x1) >> (8 * (j & 3))) & 0xffu;
+            nib |= (((byte >> 7) << 3) | (byte & 7u)) << (4 * j);
+          }
+          if (live) fx[int64_t((i0 + 8 * (k >> 1)) / 8) * XP_LANES] = nib;
+        }
+      }
+    }
+    // Words whose refill came but whose bits ran out: the rest of the stream,
+    // then zeros.
+    while (__builtin_amdgcn_ballot_w64(qn > 0)) {
+      if (qn > 0) {
+        if (live && q0 < total) huff[q0] = static_cast<uint32_t>(acc);
+        acc >>= 32;
+        q0 = q1;
+        --qn;
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace xp
+
+using namespace xp;
+
+extern "C" {
+
+int xp_encode_rows(const uint8_t* raw, int64_t rows, int64_t raw_stride, int64_t n, int64_t chunk, uint8_t* records,
+                   int64_t pitch, uint8_t* luts, int64_t lut_stride, int64_t* needed, void* stream) {
+  XP_REQUIRE(rows >= 0 && rows <= INT32_MAX, "xp_encode_rows: rows=%lld", (long long)rows);
+  if (rows == 0) return XP_OK;
+  XP_REQUIRE(raw && records && luts && needed, "xp_encode_rows: null argument");
+  XP_REQUIRE(chunk >= 16 && chunk <= 1024 && (chunk & (chunk - 1)) == 0,
+             "xp_encode_rows: chunk=%lld (a power of two, 16..1024)", (long long)chunk);
+  const int64_t group = chunk * XP_LANES;
+  if (n <= 0 || n % group)
+    return fail(XP_E_SHAPE, "row of %lld values is not a multiple of %lld", (long long)n, (long long)group);
+  const int64_t G = n / group;
+  XP_REQUIRE(G <= kMaxGroups, "xp_encode_rows: %lld groups per row (at most %d)", (long long)G, kMaxGroups);
+  XP_REQUIRE(raw_stride >= n && raw_stride % 16 == 0 && aligned16(raw),
+             "xp_encode_rows: raw rows must be 16-byte aligned with a stride of at least n");
+  XP_REQUIRE(pitch >= 4 * (G + 1) + n / 2 && pitch % 16 == 0 && aligned16(records),
+             "xp_encode_rows: pitch %lld cannot hold the record header or is not 16-byte aligned", (long long)pitch);
+  XP_REQUIRE(lut_stride >= XP_LUT_BYTES, "xp_encode_rows: lut_stride=%lld", (long long)lut_stride);
+  EncodeArgs a{raw, raw_stride, n, static_cast<int>(chunk), static_cast<int>(G), records, pitch,
+               luts, lut_stride, needed};
+  hipLaunchKernelGGL(encode_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, as_stream(stream), a);
+  return check_launch("encode_kernel");
+}
+
+}  // extern "C"

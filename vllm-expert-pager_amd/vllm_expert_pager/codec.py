@@ -72,8 +72,51 @@ def encode_into(raw: np.ndarray, record: np.ndarray, lut: np.ndarray, chunk: int
     return needed.value
 
 
+def encode_rows(raw: torch.Tensor, pitch: int, chunk: int = CHUNK, records: torch.Tensor | None = None,
+                luts: torch.Tensor | None = None, check: bool = True) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Compress the uint8 rows ``raw`` (R, N) on the GPU, one workgroup per row (codec.py:125-193).
+
+    Returns ``(records (R, pitch), luts (R, 512), needed (R,) int64)`` on raw's
+    device, byte for byte what ``encode_into`` writes. With ``check`` (it
+    synchronises), a row that does not fit the pitch raises ValueError as
+    codec.py:160-166 does; otherwise that row's record is left unwritten and
+    ``needed`` tells.
+    """
+    nat.require_device(raw, "raw")
+    if raw.dtype != torch.uint8 or raw.dim() != 2 or raw.stride(1) != 1:
+        raise ValueError(f"raw must be a (rows, N) uint8 tensor with unit column stride, got {raw.dtype} {tuple(raw.shape)}")
+    R, N = raw.shape
+    if records is None:
+        records = torch.empty((R, pitch), dtype=torch.uint8, device=raw.device)
+    if luts is None:
+        luts = torch.empty((R, LUT_BYTES), dtype=torch.uint8, device=raw.device)
+    for t, name, cols in ((records, "records", pitch), (luts, "luts", LUT_BYTES)):
+        nat.require_device(t, name)
+        if t.dtype != torch.uint8 or t.dim() != 2 or t.shape[0] != R or t.shape[1] != cols or t.stride(1) != 1:
+            raise ValueError(f"{name} must be a ({R}, {cols}) uint8 tensor")
+    if records.stride(0) != pitch:
+        raise ValueError("records rows must be contiguous at the pitch")
+    needed = torch.empty((R,), dtype=torch.int64, device=raw.device)
+    nat.call("xp_encode_rows", raw.data_ptr(), R, raw.stride(0), N, chunk, records.data_ptr(), pitch,
+             luts.data_ptr(), luts.stride(0), needed.data_ptr(), nat.stream())
+    if check and R:
+        worst = int(needed.max().item())
+        if worst > pitch:
+            raise ValueError(
+                f"compressed row is {worst} B, pitch is {pitch} B; "
+                f"VLLM_EXPERT_PAGER_PITCH must be at least {worst / N:.4f}"
+            )
+    return records, luts, needed
+
+
 def encode(raw: torch.Tensor, pitch: int, chunk: int = CHUNK) -> tuple[torch.Tensor, torch.Tensor]:
-    """Compress a uint8 row (N,). Returns ``(record of pitch bytes, 512 B LUT)`` on raw's device (codec.py:125-193)."""
+    """Compress a uint8 row (N,). Returns ``(record of pitch bytes, 512 B LUT)`` on raw's device (codec.py:125-193).
+
+    A row on the GPU is encoded there (encode_rows); a host row by the host encoder.
+    """
+    if raw.is_cuda and chunk in (16, 32, 64, 128, 256, 512, 1024):
+        rec, lut, _ = encode_rows(raw.reshape(1, -1).to(torch.uint8).contiguous(), pitch, chunk)
+        return rec[0], lut[0]
     host = raw.reshape(-1).to(torch.uint8).contiguous().cpu().numpy()
     record = np.empty(pitch, np.uint8)
     lut = np.empty(LUT_BYTES, np.uint8)
