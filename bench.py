@@ -175,6 +175,71 @@ def bench_decode(args, dev, cores):
     }
 
 
+def bench_encode(args, dev, cores):
+    """GPU encoder (load time) over the synthetic experts of the decode leg, against the host
+    encoder on the host's cores; records checked byte for byte against the host on a sample."""
+    from vllm_expert_pager import codec
+
+    count = args.rows
+    raws = synthetic_experts(count, 4321, dev)
+    pitches = [codec.pitch_of(r.shape[1], PITCH_RATIO, 4096) for r in raws]
+    outs = [codec.encode_rows(r, p) for r, p in zip(raws, pitches)]
+    torch.cuda.synchronize()
+
+    def step():
+        for r, p, (rec, lut, _) in zip(raws, pitches, outs):
+            codec.encode_rows(r, p, records=rec, luts=lut, check=False)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    steps = max(1, args.steps // 4)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    raw_bytes = count * sum(r.shape[1] for r in raws)
+    out_bytes = sum(int(o[2].sum().item()) + count * codec.LUT_BYTES for o in outs)
+    # byte parity on a sample against the host encoder
+    sample = [0, count // 2, count - 1]
+    ok = True
+    for k, r in enumerate(raws):
+        host = r[sample].cpu().numpy()
+        for i, j in enumerate(sample):
+            rec = np.empty(pitches[k], np.uint8)
+            lut = np.empty(codec.LUT_BYTES, np.uint8)
+            codec.encode_into(host[i], rec, lut)
+            ok = ok and np.array_equal(outs[k][0][j].cpu().numpy(), rec) and np.array_equal(outs[k][1][j].cpu().numpy(), lut)
+    # CPU baseline: the host encoder over a sample of experts, all cores.
+    n_cpu = max(1, min(args.cpu_rows, count))
+    hosts = [r[:n_cpu].cpu().numpy() for r in raws]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        encode_batch(hosts, threads=max(1, cores))
+        reps += 1
+        if time.perf_counter() - t0 > args.cpu_seconds / 4:
+            break
+    cpu_s = (time.perf_counter() - t0) / reps
+    cpu_gbps = n_cpu * sum(r.shape[1] for r in raws) / cpu_s / 1e9
+    out = {
+        "workload": f"encode {count} experts (w13 fp8 1024x2048 + w2 fp8 2048x512 rows, block-scaled N(0,0.02)) "
+                    "at pitch 0.89, one launch per name",
+        "ms": round(ms, 4),
+        "raw_gbps": round(raw_bytes / (ms * 1e-3) / 1e9, 2),
+        "hbm_gbps": round((raw_bytes + out_bytes) / (ms * 1e-3) / 1e9, 2),
+        "hbm_frac": round((raw_bytes + out_bytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "bit_exact_sample": ok,
+        "cpu_baseline": {"value": round(cpu_gbps, 3), "unit": "GB/s of raw rows", "cores": cores, "kind": "port",
+                         "sample": f"host encoder (the reference's encode rule in C++), {n_cpu} experts x "
+                                   f"{reps} repetitions, threads over rows"},
+    }
+    log(f"encode: {out}")
+    return out
+
+
 def bench_gather(args, dev):
     """Slot gather from pinned host RAM vs the in-run host-link ceiling."""
     from vllm_expert_pager import gather
@@ -749,6 +814,7 @@ def main() -> None:
     ap.add_argument("--only-decode", action="store_true")
     ap.add_argument("--only-moe", action="store_true")
     ap.add_argument("--only-model", action="store_true")
+    ap.add_argument("--only-encode", action="store_true")
     ap.add_argument("--tiered", action="store_true",
                     help="run only the compressed-tier legs (2048-token prefill, decode trace; needs ~30 GB "
                          "of disk for the paging file)")
@@ -779,6 +845,9 @@ def main() -> None:
     if args.only_model:
         print(json.dumps({"model_decode": bench_model_decode(args, dev)}), flush=True)
         return
+    if args.only_encode:
+        print(json.dumps({"encode": bench_encode(args, dev, cores)}), flush=True)
+        return
     if args.tiered:
         print(json.dumps({"tiered": bench_tiered(args, dev)}), flush=True)
         return
@@ -795,6 +864,7 @@ def main() -> None:
         log(f"copy probe: 3 device copies and 3 elementwise passes of {args.copy_probe_mib} MiB")
     extras = {}
     if not args.only_decode:
+        extras["encode"] = bench_encode(args, dev, cores)
         extras["gather"] = bench_gather(args, dev)
         extras["acquire"] = bench_acquire(args, dev)
         extras["moe"] = bench_moe(args, dev)

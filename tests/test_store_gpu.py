@@ -315,6 +315,46 @@ def test_rejects_rows_over_pitch(tmp_path):
         s.close()
 
 
+def test_rows_over_pitch_on_the_gpu(tmp_path):
+    Store = _mods()[2]
+    s = Store(1, 2, 1, WORKING_ROWS, ROW_BYTES, True, 0.5, str(tmp_path / "expert_pager.bin"), torch.device("cuda"))
+    try:
+        row = torch.randint(-(2**31), 2**31 - 1, (ROW_BYTES["w2_weight"] // 4,), dtype=torch.int32).cuda()
+        with pytest.raises(ValueError, match="VLLM_EXPERT_PAGER_PITCH must be at least"):
+            s.write(0, 0, "w2_weight", row)
+        with pytest.raises(ValueError, match="VLLM_EXPERT_PAGER_PITCH must be at least"):
+            s.write_rows(0, "w2_weight", row.view(1, -1))
+    finally:
+        s.close()
+
+
+def test_gpu_rows_store_the_host_encoding(tmp_path):
+    """write_rows of GPU rows (GPU encoder) leaves the RAM tier, the LUTs and the
+    paging file byte-equal to per-expert writes of host rows (host encoder)."""
+    Store = _mods()[2]
+    dev = torch.device("cuda")
+    rng = np.random.default_rng(3)
+    rows = {}
+    for name, nb in ROW_BYTES.items():
+        exp = rng.choice(16, size=(E, nb), p=np.array([0] * 8 + [1, 2, 4, 8, 16, 32, 24, 13], float) / 100)
+        rows[name] = torch.from_numpy((exp.astype(np.uint8) << 3) | (rng.integers(0, 256, (E, nb), dtype=np.uint8) & 0x87))
+    a = Store(1, E, R, WORKING_ROWS, ROW_BYTES, True, PITCH, str(tmp_path / "a.bin"), dev)
+    b = Store(1, E, R, WORKING_ROWS, ROW_BYTES, True, PITCH, str(tmp_path / "b.bin"), dev)
+    try:
+        for name in ROW_BYTES:
+            for e in range(E):
+                a.write(0, e, name, rows[name][e])
+            b.write_rows(0, name, rows[name].to(dev))
+        torch.cuda.synchronize()
+        for name in ROW_BYTES:
+            assert torch.equal(a.pinned[name][:R].cpu(), b.pinned[name][:R].cpu()), name
+        assert torch.equal(a.lut.cpu(), b.lut.cpu())
+        assert (tmp_path / "a.bin").read_bytes() == (tmp_path / "b.bin").read_bytes()
+    finally:
+        a.close()
+        b.close()
+
+
 def test_settings_validation(tmp_path):
     Store = _mods()[2]
     with pytest.raises(ValueError, match="RAM_SLOTS"):

@@ -250,8 +250,10 @@ int xp_encode_rows(const uint8_t* raw, int64_t rows, int64_t raw_stride, int64_t
   XP_REQUIRE(G <= kMaxGroups, "xp_encode_rows: %lld groups per row (at most %d)", (long long)G, kMaxGroups);
   XP_REQUIRE(raw_stride >= n && raw_stride % 16 == 0 && aligned16(raw),
              "xp_encode_rows: raw rows must be 16-byte aligned with a stride of at least n");
-  XP_REQUIRE(pitch >= 4 * (G + 1) + n / 2 && pitch % 16 == 0 && aligned16(records),
-             "xp_encode_rows: pitch %lld cannot hold the record header or is not 16-byte aligned", (long long)pitch);
+  // A pitch below the header is a row that does not fit (needed > pitch), as
+  // in xp_encode_row, not an argument error.
+  XP_REQUIRE(pitch > 0 && pitch % 16 == 0 && aligned16(records),
+             "xp_encode_rows: pitch %lld is not a positive multiple of 16", (long long)pitch);
   XP_REQUIRE(lut_stride >= XP_LUT_BYTES, "xp_encode_rows: lut_stride=%lld", (long long)lut_stride);
   EncodeArgs a{raw, raw_stride, n, static_cast<int>(chunk), static_cast<int>(G), records, pitch,
                luts, lut_stride, needed};

@@ -298,15 +298,18 @@ class Store:
             raise ValueError(
                 f"{name}: expert {expert} of layer {layer} has {raw.numel()} B, expected {self.row_bytes[name]}"
             )
-        raw_np = raw.cpu().numpy()
-        if self.compress:
+        if self.compress and raw.is_cuda:  # encoded on the GPU, as the reference's torch encode is
+            rec, lut, _ = codec.encode_rows(raw.view(1, -1), self.pitch[name])
+            self.lut[layer, expert, self.names.index(name)] = lut[0].to(self.device)
+            words = rec[0].cpu().numpy()
+        elif self.compress:
             record = np.empty(self.pitch[name], np.uint8)
             lut = np.empty(codec.LUT_BYTES, np.uint8)
-            codec.encode_into(raw_np, record, lut)
+            codec.encode_into(raw.cpu().numpy(), record, lut)
             self.lut[layer, expert, self.names.index(name)] = torch.from_numpy(lut).to(self.device)
             words = record
         else:
-            words = raw_np
+            words = raw.cpu().numpy()
         if expert < self.ram_slots:
             self.pinned[name][layer * self.ram_slots + expert].copy_(torch.from_numpy(words.view(np.int32)))
         if self.fd_w is not None:
@@ -317,9 +320,10 @@ class Store:
         """Put experts 0..n-1 of ``layer`` at once, as ``write`` would place each of them.
 
         ``rows`` is ``(n, row_bytes)`` of any 1-byte dtype on any device.
-        Compressed tiers encode the rows in a thread pool (the encoder
-        releases the GIL); RAM-tier slots 0..min(n, R)-1 of the layer are
-        filled with one copy and each expert's record goes to the paging
+        Compressed tiers encode the rows on the GPU when they are there
+        (one launch for all of them), else in a thread pool (the host
+        encoder releases the GIL); RAM-tier slots 0..min(n, R)-1 of the layer
+        are filled with one copy and each expert's record goes to the paging
         file.
         """
         raw = rows.contiguous().view(torch.uint8)
@@ -330,6 +334,16 @@ class Store:
         base = layer * self.ram_slots
         if not self.compress and self.fd_w is None:
             self.pinned[name][base : base + r].view(torch.uint8).copy_(raw[:r])
+            return
+        if self.compress and raw.is_cuda:
+            recs, luts, _ = codec.encode_rows(raw, self.pitch[name])
+            self.lut[layer, :n, self.names.index(name)] = luts.to(self.device)
+            self.pinned[name][base : base + r].view(torch.uint8).copy_(recs[:r])
+            if self.fd_w is not None:
+                words = recs.cpu().numpy()
+                for e in range(n):
+                    offset = (layer * self.num_experts + e) * self.record_bytes + self.offset[name]
+                    os.pwrite(self.fd_w, memoryview(words[e]), offset)
             return
         host = raw.cpu().numpy()
         if self.compress:
