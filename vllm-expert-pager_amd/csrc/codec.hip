@@ -2,9 +2,9 @@
 //
 // One 64-lane wave decodes TWO 32-lane groups side by side (lanes 0-31 and
 // 32-63). Each lane owns one chunk and keeps the last two Huffman words it
-// loaded as a 64-bit funnel {hi, lo} with a bit position pos; the
-// reference's fill level is 64 - pos, so its refill rule "fewer than LIMIT
-// bits left" (codec.py:227-237) becomes pos > 64 - LIMIT. At each symbol the
+// loaded as a 64-bit funnel {hi, lo} with a bit position p (kept as p - 1);
+// the reference's fill level is 64 - p, so its refill rule "fewer than LIMIT
+// bits left" (codec.py:227-237) becomes p > 64 - LIMIT. At each symbol the
 // refilling lanes of a group take consecutive words from the group's read
 // position, a lane's offset being the number of refilling lanes below it in
 // its half of the wave ballot (mbcnt) -- exactly the encoder's
@@ -83,7 +83,9 @@ __device__ __forceinline__ void ring_put(uint32_t* ring, uint32_t w_index, uint3
 // state of that group's ring (uniform over the half).
 struct Chain {
   uint64_t buf;      // {hi, lo}: the last two words loaded
-  uint32_t pos;      // next bit in buf; the fill level is 64 - pos
+  uint32_t pos;      // next bit in buf minus one (the window shift then scales the LUT
+                     // index to a byte offset); the fill level is 63 - pos. At least 1
+                     // bit is always consumed before a window is read, so it never wraps.
   uint32_t rp;       // words of the group consumed
   uint32_t fe;       // ring holds words [rp, fe)
   uint32_t q;        // words requested so far (landed or in flight)
@@ -179,7 +181,8 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
 template <int K>
 __device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& off_lo, uint32_t& off_hi,
                                               uint32_t& out, uint32_t half_shift, const uint16_t* s_lut) {
-  const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 64u - kLimit);
+  // pos is the next bit's index minus one (see Chain::pos).
+  const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 63u - kLimit);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
   const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
   const uint32_t bases = off_lo | ((off_hi - 4u * n_lo) << 16);
@@ -192,7 +195,9 @@ __device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint
   const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
   const uint32_t pr = pos + lane_select(mask, 0u, ~31u);  // pos - 32 in refilling lanes
-  const uint32_t e = s_lut[static_cast<uint32_t>(buf >> (pr & 63u)) & (XP_LUT_BYTES - 1)];
+  // The window's 9 bits shifted up by one: the byte offset of its 16-bit entry.
+  const uint32_t e = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(s_lut) +
+                                                          (static_cast<uint32_t>(buf >> (pr & 63u)) & (2u * XP_LUT_BYTES - 2)));
   pos = add_byte0(pr, e);
   or_byte<K & 3>(out, e);
 }
@@ -333,7 +338,7 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
     h.ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(h.ring));
     h.nib = rec + (G + 1) + (int64_t(g) * msteps) * 32 + li;
     h.buf = 0;
-    h.pos = 64u;  // nothing loaded: the first symbol refills every lane
+    h.pos = 63u;  // nothing loaded: the first symbol refills every lane
     h.rp = 0;
     h.a_n = h.b_n = 0;
     h.a_base = h.b_base = h.a_val = h.b_val = 0;
