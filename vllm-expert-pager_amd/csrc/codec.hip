@@ -171,26 +171,26 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
 
 // One symbol of one stream, without branches: every lane reads a ring word
 // at its refill address and keeps it only if it refills. s_lut holds
-// len | (symbol << 3) << 8 per 9-bit code. off_lo and off_hi are the LDS
-// byte addresses of the next unread ring word of the groups of the lower
-// and upper half-wave (wave-uniform, so they advance in scalar registers).
+// len | (symbol << 3) << 8 per 9-bit code. offs packs the LDS byte
+// addresses of the next unread ring word of the groups of the lower and
+// upper half-wave (low | high << 16; both below 2^16): wave-uniform, so it
+// advances in a scalar register.
 // A lane's refill word is (refilling lanes below it in its half) words on;
 // mbcnt over the whole ballot also counts, for an upper-half lane, every
 // refilling lane of the lower half, so that half's base is lowered by as
 // many words and one bit-field extract picks each lane's base.
 template <int K>
-__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& off_lo, uint32_t& off_hi,
-                                              uint32_t& out, uint32_t half_shift, const uint16_t* s_lut) {
+__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& offs, uint32_t& out,
+                                              uint32_t half_shift, const uint16_t* s_lut) {
   // pos is the next bit's index minus one (see Chain::pos).
   const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 63u - kLimit);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
   const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
-  const uint32_t bases = off_lo | ((off_hi - 4u * n_lo) << 16);
+  const uint32_t bases = offs - (n_lo << 18);  // the upper half's base lowered by n_lo words
   const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u));
   const uint32_t addr = __builtin_amdgcn_ubfe(bases, half_shift, 16u) + 4u * below;
   const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(addr);
-  off_lo += 4u * n_lo;
-  off_hi += 4u * n_hi;
+  offs += (n_lo << 2) + (n_hi << 18);
   const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
   const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
@@ -389,13 +389,12 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
         o[c] = nibble_template(x);
       }
       {
-        // The next unread ring word of each half's group, in scalar registers.
-        uint32_t off_lo[kChains], off_hi[kChains];
+        // The next unread ring word of each half's group, packed in a scalar register.
+        uint32_t offs[kChains];
 #pragma unroll
         for (int c = 0; c < kChains; ++c) {
           half_begin(ch[c], li);
-          off_lo[c] = __builtin_amdgcn_readlane(ch[c].ab0, 0);
-          off_hi[c] = __builtin_amdgcn_readlane(ch[c].ab0, 32);
+          offs[c] = __builtin_amdgcn_readlane(ch[c].ab0, 0) | (__builtin_amdgcn_readlane(ch[c].ab0, 32) << 16);
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -403,16 +402,16 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
 #pragma unroll
           for (int c = 0; c < kChains; ++c) {
             uint32_t& ow = k ? o[c].y : o[c].x;
-            decode_symbol<0>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
-            decode_symbol<1>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
-            decode_symbol<2>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
-            decode_symbol<3>(ch[c].buf, ch[c].pos, off_lo[c], off_hi[c], ow, half_shift, s_lut);
+            decode_symbol<0>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
+            decode_symbol<1>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
+            decode_symbol<2>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
+            decode_symbol<3>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
           }
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int c = 0; c < kChains; ++c)
-          half_end(ch[c], li, __builtin_amdgcn_ubfe(off_lo[c] | (off_hi[c] << 16), half_shift, 16u));
+          half_end(ch[c], li, __builtin_amdgcn_ubfe(offs[c], half_shift, 16u));
       }
 #pragma unroll
       for (int c = 0; c < kChains; ++c) {
