@@ -377,8 +377,9 @@ __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restric
     const float* su = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
     for (int i = tid; i < 2 * KB; i += NT) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
   }
-  AStage<NT> st;
-  st.init(xq, H, s_row);
+  AStage<NT> st0, st1;  // token rows of two K blocks in flight
+  st0.init(xq, H, s_row);
+  st1.init(xq, H, s_row);
 
   const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
   const int64_t n = c0 + 16 * wave + j;
@@ -417,25 +418,83 @@ __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restric
     }
   };
 
-  // Every step issues the next block's loads (the index clamped at the last
-  // block, so the loads are unconditional) before multiplying the current.
+  // Token rows are loaded two K blocks ahead of their multiply and stored to
+  // LDS one block ahead; weight rows one block ahead. Block indices are
+  // clamped at the last block, so the loads are unconditional.
+  auto clampk = [&](int k) { return k < KB ? k : KB - 1; };
   __syncthreads();  // s_row, s_xs, s_sw
-  st.load(0);
+  st0.load(0);
+  st1.load(clampk(1));
   load_b(b0, 0);
-  st.store(s_a[0]);
+  st0.store(s_a[0]);
   __syncthreads();
   for (int kb = 0; kb < KB; kb += 2) {
-    const int k1 = kb + 1 < KB ? kb + 1 : KB - 1, k2 = kb + 2 < KB ? kb + 2 : KB - 1;
-    st.load(k1);
-    load_b(b1, k1);
+    st0.load(clampk(kb + 2));
+    load_b(b1, clampk(kb + 1));
     compute(s_a[0], b0, kb);
-    st.store(s_a[1]);
+    st1.store(s_a[1]);
     __syncthreads();
-    st.load(k2);
-    load_b(b0, k2);
+    st1.load(clampk(kb + 3));
+    load_b(b0, clampk(kb + 2));
     if (kb + 1 < KB) compute(s_a[1], b1, kb + 1);
-    st.store(s_a[0]);
+    st0.store(s_a[0]);
     __syncthreads();
+  }
+
+  if constexpr (NC == kKB) {
+    // 128 columns: one whole scale group of the activations, so they are
+    // quantised here (s = max(max |a|, 1e-10) / 448, q = rne(clamp(a / s)),
+    // the rule of act_quant_kernel, on the same bf16 values).
+    float av[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      if (mi >= nmi) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float g = bf16_round(acc[mi][0][r]), u = bf16_round(acc[mi][1][r]);
+        const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+        av[mi][r] = a;
+        float m = fabsf(a);
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+        if (j == 0) s_m[wave][16 * mi + 4 * q + r] = m;
+      }
+    }
+    __syncthreads();
+    float* s_q = s_m[0];  // row scales, written over wave 0's maxima after all are read
+    float qs = 0.f;
+    if (tid < kBM) {
+      float m = s_m[0][tid];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) m = fmaxf(m, s_m[w][tid]);
+      qs = quant_scale(m);
+    }
+    __syncthreads();
+    if (tid < kBM) {
+      s_q[tid] = qs;
+      const int p = s_pair[tid];
+      if (p >= 0) work.acts[static_cast<int64_t>(p) * (I / kKB) + c0 / kKB] = qs;
+    }
+    __syncthreads();
+    uint8_t* s_act = s_a[0];  // [kBM][128] fp8
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      if (mi >= nmi) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * q + r;
+        s_act[row * kKB + 16 * wave + j] = static_cast<uint8_t>(to_fp8(clamp_fp8(av[mi][r] / s_q[row])));
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < kBM * (kKB / 16); i += NT) {  // 16-byte pieces
+      const int row = i / (kKB / 16), piece = i - row * (kKB / 16);
+      const int p = s_pair[row];
+      if (p >= 0)
+        *reinterpret_cast<u32x4*>(work.act + static_cast<int64_t>(p) * I + c0 + piece * 16) =
+            *reinterpret_cast<const u32x4*>(s_act + row * kKB + piece * 16);
+    }
+    return;
   }
 
   uint16_t* s_o = reinterpret_cast<uint16_t*>(s_a);  // [kBM][NC] bf16
@@ -777,8 +836,9 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
   }
   if (tid < kBM) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
   if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
-  AStage<kThreads> st;
-  st.init(work.act, I, s_row);
+  AStage<kThreads> st0, st1;  // activation rows of two K blocks in flight
+  st0.init(work.act, I, s_row);
+  st1.init(work.act, I, s_row);
 
   const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
   const uint8_t* brow[2];
@@ -812,22 +872,24 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
     }
   };
 
+  // As in gemm1_kernel: activation rows two K blocks ahead, weights one.
+  auto clampk = [&](int k) { return k < KB ? k : KB - 1; };
   __syncthreads();  // s_row, s_as, s_w, s_sw
-  st.load(0);
+  st0.load(0);
+  st1.load(clampk(1));
   load_b(b0, 0);
-  st.store(s_a[0]);
+  st0.store(s_a[0]);
   __syncthreads();
   for (int kb = 0; kb < KB; kb += 2) {
-    const int k1 = kb + 1 < KB ? kb + 1 : KB - 1, k2 = kb + 2 < KB ? kb + 2 : KB - 1;
-    st.load(k1);
-    load_b(b1, k1);
+    st0.load(clampk(kb + 2));
+    load_b(b1, clampk(kb + 1));
     compute(s_a[0], b0, kb);
-    st.store(s_a[1]);
+    st1.store(s_a[1]);
     __syncthreads();
-    st.load(k2);
-    load_b(b0, k2);
+    st1.load(clampk(kb + 3));
+    load_b(b0, clampk(kb + 2));
     if (kb + 1 < KB) compute(s_a[1], b1, kb + 1);
-    st.store(s_a[0]);
+    st0.store(s_a[0]);
     __syncthreads();
   }
 
@@ -992,9 +1054,12 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   }
   int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles, w);
-  rc = check_launch("act_quant_kernel");
-  if (rc) return rc;
+  if (narrow || I % (16 * kWideNW) != 0 || 16 * kWideNW != kKB) {  // else gemm1 quantised the activations
+    hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles,
+                       w);
+    rc = check_launch("act_quant_kernel");
+    if (rc) return rc;
+  }
   if (narrow)
     hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(4 * g2)), dim3(kThreads), 0,
                        as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
