@@ -40,3 +40,14 @@ def test_every_symbol_has_a_python_signature():
     ssd = {"ssd_start", "ssd_stop", "ssd_stats", "ssd_error", "ssd_test_delay"}
     missing = [n for n in declared() if n not in sig and n not in ssd]
     assert not missing, f"no ctypes signature for {missing}"
+
+
+def test_roctx_ranges_are_free_when_off(monkeypatch):
+    from vllm_expert_pager import trace
+
+    monkeypatch.delenv("VLLM_EXPERT_PAGER_ROCTX", raising=False)
+    monkeypatch.setattr(trace, "_loaded", False)
+    monkeypatch.setattr(trace, "_lib", None)
+    with trace.range("x"):
+        pass
+    assert trace._lib is None

@@ -11,6 +11,8 @@ the raw RAM-only tier, prefill between decode steps, several layers sharing
 the working slab, and a decode step captured in a hipGraph.
 """
 
+import logging
+
 import numpy as np
 import pytest
 import torch
@@ -31,11 +33,11 @@ def _mods():
 class Model:
     """A pager with L layers of random block-fp8 experts, and the same weights on the GPU."""
 
-    def __init__(self, tmp_path, E, S, R, W, compress, L=1, seed=0):
+    def __init__(self, tmp_path, E, S, R, W, compress, L=1, seed=0, log_interval=0):
         moe, pager = _mods()
         settings = pager.Settings(
             cache_slots=S, ram_slots=R, ssd_path=str(tmp_path / "paging.bin") if R < E else None,
-            compress="on" if compress else "off", working_rows=W, log_interval=0,
+            compress="on" if compress else "off", working_rows=W, log_interval=log_interval,
         )
         self.pager = pager.Pager(settings, L, E, H, I, torch.device("cuda"))
         self.E = E
@@ -156,3 +158,28 @@ def test_decode_step_in_graph(model):
         torch.cuda.synchronize()
         assert same(sout, m.one_shot(0, x, tw, ids)), f"replay {step}"
     assert m.pager.store.failed is None
+
+
+def test_log_and_roctx_ranges(model, caplog, monkeypatch):
+    """Every log_interval eager calls a layer logs its hit rates and layer 0 the
+    SSD tier's stats (experts.py:613-649); VLLM_EXPERT_PAGER_ROCTX=1 marks the
+    steps as roctx ranges."""
+    from vllm_expert_pager import trace
+
+    monkeypatch.setenv("VLLM_EXPERT_PAGER_ROCTX", "1")
+    monkeypatch.setattr(trace, "_loaded", False)
+    monkeypatch.setattr(trace, "_lib", None)
+    m = model(64, 4, 16, 8, True, log_interval=5)
+    caplog.set_level(logging.INFO, logger="vllm.vllm_expert_pager.pager")
+    rng = np.random.default_rng(5)
+    layer = m.layers[0]
+    for _ in range(10):
+        x, tw, ids = routing(rng, 1, m.E, 4, zipf=0.5)
+        layer.forward(x, tw, ids)
+    x, tw, ids = routing(rng, 40, m.E, 4, zipf=0.5)
+    layer.forward(x, tw, ids)  # the prefill path's chunk ranges
+    torch.cuda.synchronize()
+    msgs = [r.getMessage() for r in caplog.records]
+    assert sum("layer 0: vram hit" in t for t in msgs) == 2, msgs
+    assert any(t.startswith("vllm-expert-pager ssd:") and "fetches" in t for t in msgs), msgs
+    assert trace._lib is not None

@@ -22,7 +22,7 @@ from dataclasses import dataclass
 
 import torch
 
-from vllm_expert_pager import moe
+from vllm_expert_pager import moe, trace
 from vllm_expert_pager.acquire import AcquirePair
 from vllm_expert_pager.codec import decode_rows
 from vllm_expert_pager.gather import as_rows, fetch_publish_rows, fetch_wait_rows, gather_rows
@@ -211,7 +211,8 @@ class PagedExperts:
             return self._forward_working(x, topk_weights, topk_ids)
 
         layer, E = self.layer, self.pager.num_experts
-        todo, ssd_todo = self.acquire(topk_ids)
+        with trace.range(f"expert_pager L{layer} acquire"):
+            todo, ssd_todo = self.acquire(topk_ids)
         dst_row, src_row = self.acquire.vram_slot, self.acquire.ram_slot
         cached_row = self.table.no_cache  # everything comes from the RAM tier
         base = layer * store.ram_slots
@@ -228,22 +229,29 @@ class PagedExperts:
         if store.path is None:
             # Every expert is in RAM (R = E): the RAM table always hits, so
             # there is never an SSD read and one copy does it all.
-            gather_rows(todo, dst_row, cached_row, src_row, base, *rows)
+            with trace.range(f"expert_pager L{layer} gather"):
+                gather_rows(todo, dst_row, cached_row, src_row, base, *rows)
             if store.compress:
-                decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut)
+                with trace.range(f"expert_pager L{layer} decode"):
+                    decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut)
         else:
             # One launch publishes the SSD request and copies the experts
             # that are in RAM while the host reads; then the ones read from SSD.
-            gather_rows(todo, dst_row, cached_row, src_row, base, *rows, fetch=(ssd_todo, layer, store))
+            with trace.range(f"expert_pager L{layer} gather + ssd wait"):
+                gather_rows(todo, dst_row, cached_row, src_row, base, *rows, fetch=(ssd_todo, layer, store))
             if store.compress:
-                decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut, skip=ssd_todo)
-            gather_rows(ssd_todo, dst_row, cached_row, src_row, base, *rows)
+                with trace.range(f"expert_pager L{layer} decode"):
+                    decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut, skip=ssd_todo)
+            with trace.range(f"expert_pager L{layer} gather ssd rows"):
+                gather_rows(ssd_todo, dst_row, cached_row, src_row, base, *rows)
             if store.compress:
-                decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
+                with trace.range(f"expert_pager L{layer} decode ssd rows"):
+                    decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
 
-        xq, xs, routing = moe.quant_route(x, topk_ids, self.expert_map, self.table.num_slots)
-        contrib = self._contrib(topk_weights, x)
-        self._run(self.cache_slab, xq, xs, topk_weights, topk_ids, contrib, routing)
+        with trace.range(f"expert_pager L{layer} experts"):
+            xq, xs, routing = moe.quant_route(x, topk_ids, self.expert_map, self.table.num_slots)
+            contrib = self._contrib(topk_weights, x)
+            self._run(self.cache_slab, xq, xs, topk_weights, topk_ids, contrib, routing)
         self._log()
         return moe.topk_sum(contrib, topk_ids, E)
 
@@ -301,13 +309,15 @@ class PagedExperts:
         N = maps.shape[0]
         fetch_publish_rows(chunk(ssd, 0), src_row, 0, layer, store, ticket(0))
         for k in range(N):
-            copy(chunk(todo, k))
-            if k + 1 < N:
-                fetch_publish_rows(chunk(ssd, k + 1), src_row, 0, layer, store, ticket(k + 1))
-            fetch_wait_rows(chunk(ssd, k), store, ticket(k))
-            copy(chunk(late, k))
-            self.expert_map.copy_(maps[k])
-            self._run(p.working_slab, xq, xs, topk_weights, topk_ids, contrib)
+            with trace.range(f"expert_pager L{layer} chunk {k}"):
+                copy(chunk(todo, k))
+                if k + 1 < N:
+                    fetch_publish_rows(chunk(ssd, k + 1), src_row, 0, layer, store, ticket(k + 1))
+                with trace.range(f"expert_pager L{layer} chunk {k} ssd wait"):
+                    fetch_wait_rows(chunk(ssd, k), store, ticket(k))
+                copy(chunk(late, k))
+                self.expert_map.copy_(maps[k])
+                self._run(p.working_slab, xq, xs, topk_weights, topk_ids, contrib)
         self._log()
         return moe.topk_sum(contrib, topk_ids, E)
 
@@ -349,3 +359,14 @@ class PagedExperts:
             100.0 * vh / (vh + vm) if vh + vm else 0.0, vh, vh + vm,
             100.0 * rh / (rh + rm) if rh + rm else 0.0, rh, rh + rm,
         )
+        # The SSD tier is shared by every layer, so layer 0 reports it.
+        store = self.store
+        if self.layer == 0 and store.path is not None:
+            fetches, reads, io_seconds, missed = store.stats()
+            if fetches:
+                logger.info(
+                    "vllm-expert-pager ssd: %d fetches, %d reads, %.3f s, %.2f ms/fetch, "
+                    "%d re-publishes, %d give-ups, %d missed",
+                    fetches, reads, io_seconds, 1e3 * io_seconds / fetches,
+                    int(store.req[store.retry_at]), int(store.req[store.giveup_at]), missed,
+                )

@@ -252,6 +252,10 @@ class Store:
                            ctypes.byref(io_seconds), ctypes.byref(missed))
         return fetches.value, reads.value, io_seconds.value, missed.value
 
+    def stats(self) -> tuple[int, int, float, int]:
+        """(requests served, experts read, seconds from request to done, requests missed)."""
+        return self._stats()
+
     @property
     def fetches(self) -> int:
         """Requests served."""
