@@ -13,19 +13,17 @@
 // Memory: the group's Huffman words stream through a 256-word ring in LDS
 // (plus a 128-word mirror of its head, so an iteration's reads never wrap),
 // filled with coalesced 32-word loads issued one 8-symbol iteration ahead
-// of use; the
-// 512-entry LUT is a 16-bit table in LDS (length, pre-shifted exponent); the
-// sign/mantissa nibbles arrive as coalesced 32-bit words
-// (8 values each), prefetched an iteration ahead.
+// of use; the 512-entry LUT is a 16-bit table in LDS (length, pre-shifted
+// exponent); the sign/mantissa nibbles arrive as coalesced 32-bit words
+// (8 values each), prefetched an iteration ahead. Output bytes are gathered
+// per lane and stored through a lane transpose in runs of 64 bytes (flush).
 #include "common.h"
 
 namespace xp {
 namespace {
 
 constexpr int kThreads = 256;                  // 4 waves
-constexpr int kChains = 1;                     // independent chunk streams per lane
-constexpr int kGroupsPerWave = 2 * kChains;    // lanes 0-31 and 32-63 of each chain
-constexpr int kGroupsPerBlock = kGroupsPerWave * kThreads / 64;  // 16
+constexpr int kGroupsPerBlock = 2 * kThreads / 64;  // 8: lanes 0-31 and 32-63 of each wave
 constexpr uint32_t kRing = 256;                // ring words per group
 constexpr uint32_t kHalf = 8;                  // symbols between ring maintenance (one nibble word)
 // Words a group may consume in kHalf symbols. A lane refills only when fewer
@@ -314,119 +312,88 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   const int64_t huff_off = (G + 1) + nm.N / 8;  // in words
   const int64_t maxw = nm.pitch / 4 - huff_off;
 
-  Chain ch[kChains];
-  bool valid[kChains];
-  uint8_t* out[kChains];  // chunk 0 of the stream's group
-#pragma unroll
-  for (int c = 0; c < kChains; ++c) {
-    const int gl = wave * kGroupsPerWave + 2 * c + (upper ? 1 : 0);
-    int g = r * kGroupsPerBlock + gl;
-    valid[c] = g < G;
-    if (!valid[c]) g = G - 1;  // a spare stream repeats the last group and stores nothing
-    int64_t gs = 0, ge = 0;
-    if (maxw > 0) {
-      gs = rec[g];
-      ge = rec[g + 1];
-      gs = gs < 0 ? 0 : (gs > maxw ? maxw : gs);
-      ge = ge < gs ? gs : (ge > maxw ? maxw : ge);
-    }
-    Chain& h = ch[c];
-    h.count = static_cast<uint32_t>(ge - gs);
-    h.wsrc = h.count ? rec + huff_off + gs : rec;
-    h.wlast = h.count ? h.count - 1 : 0;
-    h.ring = s_ring[gl];
-    h.ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(h.ring));
-    h.nib = rec + (G + 1) + (int64_t(g) * msteps) * 32 + li;
-    h.buf = 0;
-    h.pos = 63u;  // nothing loaded: the first symbol refills every lane
-    h.rp = 0;
-    h.a_n = h.b_n = 0;
-    h.a_base = h.b_base = h.a_val = h.b_val = 0;
-    out[c] = nm.dst + drow * nm.N + int64_t(g) * 32 * a.chunk;
+  const int gl = 2 * wave + (upper ? 1 : 0);  // the lane's group in the workgroup
+  int g = r * kGroupsPerBlock + gl;
+  const bool valid = g < G;
+  if (!valid) g = G - 1;  // a spare half-wave repeats the last group and stores nothing
+  int64_t gs = 0, ge = 0;
+  if (maxw > 0) {
+    gs = rec[g];
+    ge = rec[g + 1];
+    gs = gs < 0 ? 0 : (gs > maxw ? maxw : gs);
+    ge = ge < gs ? gs : (ge > maxw ? maxw : ge);
   }
-  // Initial fill of both rings: the first kRing words (8 loads per lane each).
-#pragma unroll
-  for (int c = 0; c < kChains; ++c) {
-    Chain& h = ch[c];
-    const uint32_t fill = h.count < kRing ? h.count : kRing;
+  Chain ch;
+  ch.count = static_cast<uint32_t>(ge - gs);
+  ch.wsrc = ch.count ? rec + huff_off + gs : rec;
+  ch.wlast = ch.count ? ch.count - 1 : 0;
+  ch.ring = s_ring[gl];
+  ch.ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ch.ring));
+  ch.nib = rec + (G + 1) + (int64_t(g) * msteps) * 32 + li;
+  ch.buf = 0;
+  ch.pos = 63u;  // nothing loaded: the first symbol refills every lane
+  ch.rp = 0;
+  ch.a_n = ch.b_n = 0;
+  ch.a_base = ch.b_base = ch.a_val = ch.b_val = 0;
+  uint8_t* out = nm.dst + drow * nm.N + int64_t(g) * 32 * a.chunk;  // chunk 0 of the group
+  // Initial fill of the ring: the group's first kRing words (8 loads per lane).
+  {
+    const uint32_t fill = ch.count < kRing ? ch.count : kRing;
     uint32_t v[kRing / 32];
 #pragma unroll
     for (uint32_t i = 0; i < kRing / 32; ++i) {
       const uint32_t w = li + 32 * i;
-      v[i] = h.wsrc[w < h.wlast ? w : h.wlast];
+      v[i] = ch.wsrc[w < ch.wlast ? w : ch.wlast];
     }
 #pragma unroll
     for (uint32_t i = 0; i < kRing / 32; ++i) {
       const uint32_t w = li + 32 * i;
-      h.ring[w] = v[i];
-      if (w < kMirror) h.ring[w + kRing] = v[i];
+      ch.ring[w] = v[i];
+      if (w < kMirror) ch.ring[w + kRing] = v[i];
     }
-    h.fe = h.q = fill;
-    h.x_next = h.nib[0];
+    ch.fe = ch.q = fill;
+    ch.x_next = ch.nib[0];
   }
   __syncthreads();
-  // The refill before symbol 0: every lane of a group takes one word, in
-  // lane order.
 
   // Output: a lane's chunk is contiguous, produced 8 bytes per iteration.
   // F iterations (8F bytes) are gathered in registers and stored together
   // (see flush): lines written in 16-byte pieces far apart in time leave the
   // caches as partial writes, which cost more than the decode itself.
-  uint4 ob[kChains][F / 2];
+  uint4 ob[F / 2];
 #pragma unroll
-  for (int c = 0; c < kChains; ++c)
-#pragma unroll
-    for (int i = 0; i < F / 2; ++i) ob[c][i] = make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < F / 2; ++i) ob[i] = make_uint4(0, 0, 0, 0);
   for (int m0 = 0; m0 < msteps; m0 += F) {
 #pragma unroll
     for (int u = 0; u < F; ++u) {
       const int m = m0 + u;
-      uint2 o[kChains];
-#pragma unroll
-      for (int c = 0; c < kChains; ++c) {
-        const uint32_t x = ch[c].x_next;
-        ch[c].x_next = ch[c].nib[(m + 1 < msteps ? m + 1 : m) * 32];
-        o[c] = nibble_template(x);
-      }
-      {
-        // The next unread ring word of each half's group, packed in a scalar register.
-        uint32_t offs[kChains];
-#pragma unroll
-        for (int c = 0; c < kChains; ++c) {
-          half_begin(ch[c], li);
-          offs[c] = __builtin_amdgcn_readlane(ch[c].ab0, 0) | (__builtin_amdgcn_readlane(ch[c].ab0, 32) << 16);
-        }
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-#pragma unroll
-          for (int c = 0; c < kChains; ++c) {
-            uint32_t& ow = k ? o[c].y : o[c].x;
-            decode_symbol<0>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
-            decode_symbol<1>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
-            decode_symbol<2>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
-            decode_symbol<3>(ch[c].buf, ch[c].pos, offs[c], ow, half_shift, s_lut);
-          }
-        }
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int c = 0; c < kChains; ++c)
-          half_end(ch[c], li, __builtin_amdgcn_ubfe(offs[c], half_shift, 16u));
-      }
-#pragma unroll
-      for (int c = 0; c < kChains; ++c) {
-        uint4& q = ob[c][u >> 1];
-        if (u & 1) {
-          q.z = o[c].x;
-          q.w = o[c].y;
-        } else {
-          q.x = o[c].x;
-          q.y = o[c].y;
-        }
+      const uint32_t x = ch.x_next;
+      ch.x_next = ch.nib[(m + 1 < msteps ? m + 1 : m) * 32];
+      uint2 o = nibble_template(x);
+      half_begin(ch, li);
+      // The next unread ring word of each half's group, packed in a scalar register.
+      uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
+      __builtin_amdgcn_wave_barrier();
+      decode_symbol<0>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
+      decode_symbol<1>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
+      decode_symbol<2>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
+      decode_symbol<3>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
+      decode_symbol<0>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
+      decode_symbol<1>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
+      decode_symbol<2>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
+      decode_symbol<3>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
+      __builtin_amdgcn_wave_barrier();
+      half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
+      uint4& q = ob[u >> 1];
+      if (u & 1) {
+        q.z = o.x;
+        q.w = o.y;
+      } else {
+        q.x = o.x;
+        q.y = o.y;
       }
     }
-#pragma unroll
-    for (int c = 0; c < kChains; ++c) flush<F>(ob[c], out[c], a.chunk, li, 8 * m0, valid[c]);
+    flush<F>(ob, out, a.chunk, li, 8 * m0, valid);
   }
 }
 
