@@ -804,8 +804,8 @@ def bench_tiered(args, dev):
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--rows", type=int, default=256)
     ap.add_argument("--cpu-rows", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)

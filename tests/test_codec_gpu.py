@@ -71,7 +71,8 @@ def test_golden_records():
 
 
 @pytest.mark.parametrize("dist", ["realistic", "uniform", "geometric", "constant", "long_codes"])
-@pytest.mark.parametrize("chunk", [64, 512])
+# 128-byte stores for chunks of 128 and 512, 64-byte for 64 and 192, plain for 32 and 96
+@pytest.mark.parametrize("chunk", [32, 64, 96, 128, 192, 512])
 def test_round_trip(dist, chunk):
     codec = _codec()
     n = 2 * chunk * 32

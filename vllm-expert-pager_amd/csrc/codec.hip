@@ -11,12 +11,14 @@
 // (symbol index, lane) word order.
 //
 // Memory: the group's Huffman words stream through a 256-word ring in LDS
-// (plus a 128-word mirror of its head, so an iteration's reads never wrap),
-// filled with coalesced 32-word loads issued one 8-symbol iteration ahead
-// of use; the 512-entry LUT is a 16-bit table in LDS (length, pre-shifted
-// exponent); the sign/mantissa nibbles arrive as coalesced 32-bit words
-// (8 values each), prefetched an iteration ahead. Output bytes are gathered
-// per lane and stored through a lane transpose in runs of 64 bytes (flush).
+// (plus a 224-word mirror of its head, so a step's reads never wrap), kept
+// at least 192 words ahead of the reads: each 16-symbol step issues a
+// coalesced 64-word load at its start and lands it at its end. The
+// 512-entry LUT is a 16-bit table in LDS (length, pre-shifted exponent); the
+// sign/mantissa nibbles arrive as coalesced 32-bit words (8 values each),
+// prefetched a step ahead. Output bytes are gathered per lane and stored
+// through a lane transpose in runs of 128 bytes (flush). The kernel is held
+// to 64 VGPRs, so that 8 waves share each SIMD.
 #include "common.h"
 
 namespace xp {
@@ -25,7 +27,7 @@ namespace {
 constexpr int kThreads = 256;                  // 4 waves
 constexpr int kGroupsPerBlock = 2 * kThreads / 64;  // 8: lanes 0-31 and 32-63 of each wave
 constexpr uint32_t kRing = 256;                // ring words per group
-constexpr uint32_t kHalf = 8;                  // symbols between ring maintenance (one nibble word)
+constexpr uint32_t kHalf = 16;                 // symbols between ring maintenance (two nibble words)
 // Words a group may consume in kHalf symbols. A lane refills only when fewer
 // than LIMIT bits are left and then holds at least 32; a symbol takes at most
 // LIMIT bits, so its next refill is at least ceil((32 - LIMIT + 1) / LIMIT) = 3
@@ -33,7 +35,7 @@ constexpr uint32_t kHalf = 8;                  // symbols between ring maintenan
 constexpr uint32_t kAhead = 32 * ((kHalf + 2) / 3);
 constexpr uint32_t kMirror = kAhead + 32;      // reads of a half never wrap
 constexpr uint32_t kRingPad = kRing + kMirror;
-constexpr uint32_t kFetch = 32;                // words requested per half-iteration
+constexpr uint32_t kFetch = 64;                // words requested per half-iteration (two per lane)
 constexpr int kLimit = XP_LIMIT;
 
 struct NameDev {
@@ -87,8 +89,7 @@ struct Chain {
   uint32_t rp;       // words of the group consumed
   uint32_t fe;       // ring holds words [rp, fe)
   uint32_t q;        // words requested so far (landed or in flight)
-  uint32_t a_base, a_n, a_val;  // request in flight, issued one half earlier
-  uint32_t b_base, b_n, b_val;  // request in flight, issued this half
+  uint32_t b_base, b_n, b_val0, b_val1;  // request in flight, issued at this half's start
   uint32_t ab0;      // byte address of word rp in LDS at the half's start
   uint32_t x_next;   // nibble word of the next iteration
   uint32_t count;    // Huffman words of the group
@@ -100,7 +101,7 @@ struct Chain {
 };
 
 // Start of a half-iteration: make sure the ring holds the next kAhead words,
-// then request up to kFetch more (landed by the end of the next half).
+// then request up to kFetch more (landed at the end of this half).
 __device__ __forceinline__ void half_begin(Chain& c, uint32_t li) {
   while (c.fe < c.count && c.fe < c.rp + kAhead) {  // slow path: the stream outran the requests
     const uint32_t w = c.fe + li;
@@ -116,21 +117,20 @@ __device__ __forceinline__ void half_begin(Chain& c, uint32_t li) {
   const uint32_t w = c.q + li;
   c.b_base = c.q;
   c.b_n = n;
-  c.b_val = c.wsrc[w < c.wlast ? w : c.wlast];
+  c.b_val0 = c.wsrc[w < c.wlast ? w : c.wlast];
+  c.b_val1 = c.wsrc[w + 32 < c.wlast ? w + 32 : c.wlast];
   c.q += n;
   c.ab0 = c.ring_addr + 4u * (c.rp & (kRing - 1));
 }
 
-// End of a half-iteration: land the older request in the ring (its slots
-// hold words already consumed) and shift the newer one down.
+// End of a half-iteration: land the request in the ring (its slots hold
+// words already consumed).
 __device__ __forceinline__ void half_end(Chain& c, uint32_t li, uint32_t ab) {
   c.rp += (ab - c.ab0) >> 2;
-  if (li < c.a_n) ring_put(c.ring, c.a_base + li, c.a_val);
-  const uint32_t landed = c.a_base + c.a_n;
+  if (li < c.b_n) ring_put(c.ring, c.b_base + li, c.b_val0);
+  if (li + 32 < c.b_n) ring_put(c.ring, c.b_base + 32 + li, c.b_val1);
+  const uint32_t landed = c.b_base + c.b_n;
   c.fe = c.fe > landed ? c.fe : landed;
-  c.a_base = c.b_base;
-  c.a_n = c.b_n;
-  c.a_val = c.b_val;
 }
 
 // mask[lane] ? if1 : if0, as one v_cndmask. Written as an instruction so
@@ -200,50 +200,52 @@ __device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint
   or_byte<K & 3>(out, e);
 }
 
-// v from lane (this lane xor D), D in {1, 2, 4}: a quad permute for 1 and
-// 2, a swizzle inside 32 lanes for 4.
-template <int D>
-__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
-  if constexpr (D == 1)
-    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, false));
-  else if constexpr (D == 2)
-    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4E, 0xF, 0xF, false));
-  else
-    return static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), (D << 10) | 0x1F));
-}
-
-// One stage of the NP-lane transpose of 16-byte pieces w[4j..4j+3]
-// (j < NP): lanes whose bit D is clear swap their pieces j | D with the
-// partner's pieces j.
-template <int D, int NP>
-__device__ __forceinline__ void butterfly(uint32_t (&w)[4 * NP], uint32_t q) {
-  // The selects are instructions on a lane mask: selecting between two
-  // array elements would let the compiler index the array dynamically.
-  const unsigned long long hi = __builtin_amdgcn_ballot_w64((q & static_cast<uint32_t>(D)) != 0);
+// One stage of the transpose of 16-byte pieces w[4j..4j+3] (j < NP) over
+// sets of lanes four apart: the lanes whose bit T (2, 3 or 4) is clear swap
+// their pieces j | D with pieces j of the partner lane (this lane + 2^T),
+// D = 2^(T-2). Within a 16-lane row the exchange is a pair of row shifts
+// whose bank masks write only the receiving lanes (a bank is lanes with
+// equal bits 3:2); across rows (T = 4) it is one row swap.
+template <int T, int NP>
+__device__ __forceinline__ void butterfly(uint32_t (&w)[4 * NP]) {
+  constexpr int D = 1 << (T - 2);
 #pragma unroll
   for (int i = 0; i < 2 * NP; ++i) {
     const int jj = i >> 2, k = i & 3;
     const int j = ((jj & ~(D - 1)) << 1) | (jj & (D - 1));  // the pieces whose bit D is clear
     const int ia = 4 * j + k, ib = 4 * (j | D) + k;
-    const uint32_t r = lane_xor<D>(lane_select(hi, w[ib], w[ia]));
-    w[ia] = lane_select(hi, w[ia], r);
-    w[ib] = lane_select(hi, r, w[ib]);
+    if constexpr (T == 4) {
+      // Odd rows of the first operand trade places with even rows of the second.
+      const auto r = __builtin_amdgcn_permlane16_swap(w[ia], w[ib], false, false);
+      w[ia] = r[0];
+      w[ib] = r[1];
+    } else {
+      constexpr int kShl = 0x100 | (1 << T), kShr = 0x110 | (1 << T);  // lane i <- i + 2^T, i - 2^T
+      constexpr int kClear = T == 2 ? 0x5 : 0x3, kSet = T == 2 ? 0xA : 0xC;
+      const uint32_t nb = static_cast<uint32_t>(
+          __builtin_amdgcn_update_dpp(static_cast<int>(w[ib]), static_cast<int>(w[ia]), kShl, 0xF, kClear, false));
+      const uint32_t na = static_cast<uint32_t>(
+          __builtin_amdgcn_update_dpp(static_cast<int>(w[ia]), static_cast<int>(w[ib]), kShr, 0xF, kSet, false));
+      w[ia] = na;
+      w[ib] = nb;
+    }
   }
 }
 
 // Store of a lane's last F iterations (8F bytes at byte `off` of its
-// chunk, NP = F/2 pieces of 16 bytes). For F of 8 or 16 an NP-lane butterfly
-// (xor 1, 2, 4) leaves lane q of each NP-lane set with piece q of each of the
-// set's NP chunks: store j of the set then writes 8F contiguous bytes of
-// chunk j (a whole 128-byte line for F = 16), so one store instruction
-// covers 64/NP runs rather than 64 separate 16-byte pieces. Every lane takes
-// part in the exchange; only valid streams store.
+// chunk, NP = F/2 pieces of 16 bytes). For F of 8 or 16 the lanes of a
+// half-wave form sets of NP lanes four apart (lane bits 2, 3 and, for 16, 4);
+// the transpose leaves set member q with piece q of each member's chunk, so
+// store j of the set writes 8F contiguous bytes of member j's chunk (a whole
+// 128-byte line for F = 16): one store instruction covers 64/NP runs rather
+// than 64 separate 16-byte pieces. Every lane takes part in the exchange;
+// only valid streams store.
 template <int F>
 __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64_t chunk, uint32_t li, int64_t off,
                                       bool valid) {
   constexpr int NP = F / 2;
   if constexpr (NP == 4 || NP == 8) {
-    const uint32_t q = li & (NP - 1);
+    const uint32_t q = (li >> 2) & (NP - 1);
     uint32_t w[4 * NP];
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
@@ -252,14 +254,14 @@ __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64
       w[4 * j + 2] = ob[j].z;
       w[4 * j + 3] = ob[j].w;
     }
-    butterfly<1, NP>(w, q);
-    butterfly<2, NP>(w, q);
-    if constexpr (NP == 8) butterfly<4, NP>(w, q);
+    butterfly<2, NP>(w);
+    butterfly<3, NP>(w);
+    if constexpr (NP == 8) butterfly<4, NP>(w);
     if (valid) {
-      uint8_t* base = chunk0 + static_cast<int64_t>(li & ~(NP - 1u)) * chunk + off + 16 * q;
+      uint8_t* base = chunk0 + static_cast<int64_t>(li & ~(4u * NP - 4u)) * chunk + off + 16 * q;
 #pragma unroll
       for (int j = 0; j < NP; ++j)
-        *reinterpret_cast<uint4*>(base + j * chunk) = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
+        *reinterpret_cast<uint4*>(base + 4 * j * chunk) = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
     }
   } else {
     if (valid) {
@@ -271,7 +273,7 @@ __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64
 }
 
 template <int F>
-__global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) decode_kernel(DecodeArgs a) {
   __shared__ uint16_t s_lut[XP_LUT_BYTES];
   __shared__ uint32_t s_ring[kGroupsPerBlock][kRingPad];
 
@@ -333,8 +335,8 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   ch.buf = 0;
   ch.pos = 63u;  // nothing loaded: the first symbol refills every lane
   ch.rp = 0;
-  ch.a_n = ch.b_n = 0;
-  ch.a_base = ch.b_base = ch.a_val = ch.b_val = 0;
+  ch.b_n = 0;
+  ch.b_base = ch.b_val0 = ch.b_val1 = 0;
   uint8_t* out = nm.dst + drow * nm.N + int64_t(g) * 32 * a.chunk;  // chunk 0 of the group
   // Initial fill of the ring: the group's first kRing words (8 loads per lane).
   {
@@ -365,33 +367,35 @@ __global__ void __launch_bounds__(kThreads) decode_kernel(DecodeArgs a) {
   for (int i = 0; i < F / 2; ++i) ob[i] = make_uint4(0, 0, 0, 0);
   for (int m0 = 0; m0 < msteps; m0 += F) {
 #pragma unroll
-    for (int u = 0; u < F; ++u) {
+    for (int u = 0; u < F; u += 2) {
       const int m = m0 + u;
-      const uint32_t x = ch.x_next;
-      ch.x_next = ch.nib[(m + 1 < msteps ? m + 1 : m) * 32];
-      uint2 o = nibble_template(x);
+      const uint32_t x0 = ch.x_next;
+      const uint32_t x1 = ch.nib[(m + 1) * 32];
+      ch.x_next = ch.nib[(m + 2 < msteps ? m + 2 : m) * 32];
+      uint2 o0 = nibble_template(x0), o1 = nibble_template(x1);
       half_begin(ch, li);
       // The next unread ring word of each half's group, packed in a scalar register.
       uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
       __builtin_amdgcn_wave_barrier();
-      decode_symbol<0>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
-      decode_symbol<1>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
-      decode_symbol<2>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
-      decode_symbol<3>(ch.buf, ch.pos, offs, o.x, half_shift, s_lut);
-      decode_symbol<0>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
-      decode_symbol<1>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
-      decode_symbol<2>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
-      decode_symbol<3>(ch.buf, ch.pos, offs, o.y, half_shift, s_lut);
+      decode_symbol<0>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
+      decode_symbol<1>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
+      decode_symbol<2>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
+      decode_symbol<3>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
+      decode_symbol<0>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
+      decode_symbol<1>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
+      decode_symbol<2>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
+      decode_symbol<3>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
+      decode_symbol<0>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
+      decode_symbol<1>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
+      decode_symbol<2>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
+      decode_symbol<3>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
+      decode_symbol<0>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
+      decode_symbol<1>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
+      decode_symbol<2>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
+      decode_symbol<3>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
       __builtin_amdgcn_wave_barrier();
       half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
-      uint4& q = ob[u >> 1];
-      if (u & 1) {
-        q.z = o.x;
-        q.w = o.y;
-      } else {
-        q.x = o.x;
-        q.y = o.y;
-      }
+      ob[u >> 1] = make_uint4(o0.x, o0.y, o1.x, o1.y);
     }
     flush<F>(ob, out, a.chunk, li, 8 * m0, valid);
   }
@@ -451,8 +455,10 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
   a.blocks_per_row = per_row;
   const int64_t grid = K * per_row;
   XP_REQUIRE(grid <= (int64_t(1) << 31) - 1, "xp_decode_rows: grid too large");
-  // 64 bytes per lane and store (4-lane runs) when the chunk allows it.
-  if (chunk % 64 == 0)
+  // Runs of 128 bytes per store (8-lane sets) when the chunk allows it, else 64 or 32.
+  if (chunk % 128 == 0)
+    hipLaunchKernelGGL(decode_kernel<16>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
+  else if (chunk % 64 == 0)
     hipLaunchKernelGGL(decode_kernel<8>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
   else
     hipLaunchKernelGGL(decode_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
