@@ -10,7 +10,7 @@ RAM against the in-run host-link ceiling (large pinned H2D copies), acquire
 microseconds per layer inside a captured hipGraph, and the oracle's CPU
 decoder on a bounded sample as the CPU baseline.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 50]
 """
 
 import argparse

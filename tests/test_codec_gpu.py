@@ -124,6 +124,40 @@ def test_follows_todo_and_skips():
         assert np.array_equal(dst[k][0].cpu().numpy(), raws[6][k])
 
 
+@pytest.mark.parametrize("chunk", [64, 512])
+def test_garbage_records_stay_in_bounds(chunk):
+    """Records and LUTs of random bytes (start words out of range, code
+    lengths 0-15) expand to arbitrary bytes in their own rows only: the
+    valid experts of the same launch are exact and a spare row stays zero."""
+    codec = _codec()
+    dev = torch.device("cuda")
+    ns = (4 * chunk * 32, 2 * chunk * 32)
+    pitches = [codec_ref.pitch_of(n, 1.25, 4096) for n in ns]
+    E = 6
+    rng = np.random.default_rng(7)
+    raws = {e: [rows(100 + 10 * e + k, n) for k, n in enumerate(ns)] for e in (0, 3)}
+    staging = [torch.from_numpy(rng.integers(0, 256, (E, p), dtype=np.uint8)).to(dev) for p in pitches]
+    lut_np = rng.integers(0, 256, (E, 2, 512), dtype=np.uint8)
+    lut_np[4] = 0x09  # every window a 9-bit code: a refill every 3 symbols
+    lut_np[5] = 0x00  # length 0, read as 1
+    for e in (0, 3):
+        for k in range(2):
+            rec, lt = codec_ref.encode(raws[e][k], pitches[k], chunk)
+            staging[k][e] = torch.from_numpy(rec).to(dev)
+            lut_np[e, k] = lt
+    lut = torch.from_numpy(lut_np).to(dev)
+    dst = [torch.zeros((E + 1, n), dtype=torch.uint8, device=dev) for n in ns]
+    todo = torch.arange(E, dtype=torch.int64, device=dev)
+    dst_row = torch.arange(E, dtype=torch.int64, device=dev)
+    cache_row = torch.full((E,), -1, dtype=torch.int64, device=dev)
+    codec.decode_rows(todo, dst_row, cache_row, staging, dst, lut, chunk=chunk)
+    torch.cuda.synchronize()
+    for k in range(2):
+        for e in (0, 3):
+            np.testing.assert_array_equal(dst[k][e].cpu().numpy(), raws[e][k])
+        assert not dst[k][E].any()
+
+
 def _expert_batch(codec, count, seed):
     """Compressed staging (count rows per name) for synthetic full-size experts, plus the raw rows."""
     shapes = ((1024, 2048), (2048, 512))

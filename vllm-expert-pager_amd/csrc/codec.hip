@@ -93,19 +93,18 @@ struct Chain {
   uint32_t ab0;      // byte address of word rp in LDS at the half's start
   uint32_t x_next;   // nibble word of the next iteration
   uint32_t count;    // Huffman words of the group
-  uint32_t wlast;    // last readable word index (0 for an empty group)
-  const uint32_t* wsrc;  // the group's words (a readable address if empty)
-  const uint32_t* nib;   // this lane's nibble words (stride 32 words)
+  uint32_t wsrc;     // byte offset in the record of the group's word li (this lane's column)
+  uint32_t nib;      // byte offset in the record of this lane's first nibble word
   uint32_t* ring;
   uint32_t ring_addr;
 };
 
 // Start of a half-iteration: make sure the ring holds the next kAhead words,
 // then request up to kFetch more (landed at the end of this half).
-__device__ __forceinline__ void half_begin(Chain& c, uint32_t li) {
+__device__ __forceinline__ void half_begin(Chain& c, uint32_t li, __amdgpu_buffer_rsrc_t rec) {
   while (c.fe < c.count && c.fe < c.rp + kAhead) {  // slow path: the stream outran the requests
     const uint32_t w = c.fe + li;
-    const uint32_t v = c.wsrc[w < c.wlast ? w : c.wlast];
+    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * c.fe, 0, 0);
     if (w < c.count) ring_put(c.ring, w, v);
     c.fe = c.fe + 32 < c.count ? c.fe + 32 : c.count;
   }
@@ -114,11 +113,12 @@ __device__ __forceinline__ void half_begin(Chain& c, uint32_t li) {
   const uint32_t want = c.count - c.q;
   uint32_t n = want < room ? want : room;
   n = n < kFetch ? n : kFetch;
-  const uint32_t w = c.q + li;
   c.b_base = c.q;
   c.b_n = n;
-  c.b_val0 = c.wsrc[w < c.wlast ? w : c.wlast];
-  c.b_val1 = c.wsrc[w + 32 < c.wlast ? w + 32 : c.wlast];
+  // Reads past the group's words return other bytes of the record (never
+  // used), past the record zeros: the buffer's range check bounds them.
+  c.b_val0 = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * c.q, 0, 0);
+  c.b_val1 = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * c.q + 128u, 0, 0);
   c.q += n;
   c.ab0 = c.ring_addr + 4u * (c.rp & (kRing - 1));
 }
@@ -327,11 +327,16 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   }
   Chain ch;
   ch.count = static_cast<uint32_t>(ge - gs);
-  ch.wsrc = ch.count ? rec + huff_off + gs : rec;
-  ch.wlast = ch.count ? ch.count - 1 : 0;
+  // The record as a raw buffer of pitch bytes (stride 0; word 3 of the
+  // descriptor 0x00020000 selects 32-bit data on gfx9-family chips): the
+  // hardware range check returns zero for loads beyond it, so the group's
+  // word and nibble loads need no clamps.
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(rec), 0, static_cast<int>(nm.pitch), 0x00020000);
+  ch.wsrc = static_cast<uint32_t>(4 * (huff_off + gs) + 4 * li);
   ch.ring = s_ring[gl];
   ch.ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ch.ring));
-  ch.nib = rec + (G + 1) + (int64_t(g) * msteps) * 32 + li;
+  ch.nib = static_cast<uint32_t>(4 * ((G + 1) + (int64_t(g) * msteps) * 32 + li));
   ch.buf = 0;
   ch.pos = 63u;  // nothing loaded: the first symbol refills every lane
   ch.rp = 0;
@@ -344,8 +349,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
     uint32_t v[kRing / 32];
 #pragma unroll
     for (uint32_t i = 0; i < kRing / 32; ++i) {
-      const uint32_t w = li + 32 * i;
-      v[i] = ch.wsrc[w < ch.wlast ? w : ch.wlast];
+      v[i] = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.wsrc + 128u * i, 0, 0);
     }
 #pragma unroll
     for (uint32_t i = 0; i < kRing / 32; ++i) {
@@ -354,7 +358,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
       if (w < kMirror) ch.ring[w + kRing] = v[i];
     }
     ch.fe = ch.q = fill;
-    ch.x_next = ch.nib[0];
+    ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 0, 0);
   }
   __syncthreads();
 
@@ -370,10 +374,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
     for (int u = 0; u < F; u += 2) {
       const int m = m0 + u;
       const uint32_t x0 = ch.x_next;
-      const uint32_t x1 = ch.nib[(m + 1) * 32];
-      ch.x_next = ch.nib[(m + 2 < msteps ? m + 2 : m) * 32];
+      const uint32_t x1 = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 1), 0);
+      ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 2 < msteps ? m + 2 : m), 0);
       uint2 o0 = nibble_template(x0), o1 = nibble_template(x1);
-      half_begin(ch, li);
+      half_begin(ch, li, rrec);
       // The next unread ring word of each half's group, packed in a scalar register.
       uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
       __builtin_amdgcn_wave_barrier();
@@ -436,6 +440,8 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
                "xp_decode_rows: name %d row of %lld values is not a multiple of %lld", n, (long long)s.row_bytes,
                (long long)group);
     const int64_t G = s.row_bytes / group;
+    XP_REQUIRE(s.pitch < (int64_t(1) << 31), "xp_decode_rows: name %d pitch %lld is 2 GiB or more", n,
+               (long long)s.pitch);
     XP_REQUIRE(s.pitch % 4 == 0 && s.pitch >= 4 * (G + 1) + s.row_bytes / 2,
                "xp_decode_rows: name %d pitch %lld cannot hold the record header", n, (long long)s.pitch);
     XP_REQUIRE(s.stg && s.dst, "xp_decode_rows: name %d has a null buffer", n);
