@@ -19,11 +19,13 @@
 //
 // Work decomposition: route lists the pairs of each slab slot in CSR form
 // and cuts them into tiles of 64 pairs of one slot. gemm1 takes one tile
-// and 32 activation columns per workgroup (so a decode step of 8 pairs
-// still spreads over 128 workgroups), act_quant one tile, gemm2 one tile and
-// 128 output columns. Launch grids are sized from the shapes alone (a bound
-// on the tile count), so the sequence is graph-capturable; workgroups past
-// the live tile count exit at once.
+// and 128 activation columns per workgroup at prefill sizes; for few pairs
+// it takes 16 rows and 16 columns, with the K blocks split over its waves
+// (so a decode step of 8 pairs spreads over 256 workgroups). act_quant takes
+// one tile, gemm2 one tile (or 16 rows) and 128 output columns. Launch grids
+// are sized from the shapes alone (a bound on the tile count), so the
+// sequence is graph-capturable; workgroups past the live tile count exit at
+// once.
 #include <hip/hip_bf16.h>
 
 #include "common.h"
@@ -268,11 +270,11 @@ __device__ __forceinline__ void tile_rows(const Tile& tile, const int32_t* pairs
   }
 }
 
-// Workspace of xp_moe_experts: bf16 activations, their per-32-column
+// Workspace of xp_moe_experts: bf16 activations, their per-16-column
 // maxima, the fp8 activations and their per-128-column scales.
 struct Work {
   uint16_t* a16;   // [npairs][I]
-  float* amax32;   // [npairs][I/32]
+  float* amax16;   // [npairs][I/16]
   uint8_t* act;    // [npairs][I]
   float* acts;     // [npairs][I/128]
 };
@@ -280,18 +282,17 @@ struct Work {
 inline int64_t align256(int64_t n) { return (n + 255) & ~int64_t(255); }
 
 inline int64_t work_layout(int64_t npairs, int64_t I, Work* w, uint8_t* base) {
-  const int64_t sz[4] = {align256(npairs * I * 2), align256(npairs * (I / 32) * 4), align256(npairs * I),
+  const int64_t sz[4] = {align256(npairs * I * 2), align256(npairs * (I / 16) * 4), align256(npairs * I),
                          align256(npairs * (I / kKB) * 4)};
   if (w) {
     w->a16 = reinterpret_cast<uint16_t*>(base);
-    w->amax32 = reinterpret_cast<float*>(base + sz[0]);
+    w->amax16 = reinterpret_cast<float*>(base + sz[0]);
     w->act = base + sz[0] + sz[1];
     w->acts = reinterpret_cast<float*>(base + sz[0] + sz[1] + sz[2]);
   }
   return sz[0] + sz[1] + sz[2] + sz[3];
 }
 
-constexpr int kC1 = 32;       // activation columns per narrow gemm1 workgroup
 constexpr int kWideTiles = 64;  // tile bound from which gemm1 uses the wide workgroups
 constexpr int kWideNW = 8;      // waves (16 activation columns each) of a wide gemm1 workgroup
 constexpr int kNarrowChunk = 4; // K blocks per load chunk of the small-batch GEMMs
@@ -332,13 +333,13 @@ __device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4
   a[1] = p[1];
 }
 
-// GEMM1: gate and up for NW*16 activation columns of one tile (1-D grid in
-// XCD order, see xcd_item); each wave owns 16 columns and runs the K blocks
-// in order, so a column's value does not depend on the workgroup width.
-// The tile's A rows are staged in LDS, double-buffered, one block ahead.
-// Then a = bf16(silu(bf16 gate) * bf16 up) is written as bf16 with the
-// maximum |a| of each row's 32-column blocks. Only the 16-row subtiles that
-// hold pairs are multiplied.
+// GEMM1: gate and up for NW*16 = 128 activation columns of one tile (1-D
+// grid in XCD order, see xcd_item); each wave owns 16 columns and runs the K
+// blocks in order, so a column's value does not depend on the workgroup
+// width. The tile's A rows are staged in LDS, double-buffered, one block
+// ahead. Then a = bf16(silu(bf16 gate) * bf16 up) is quantised to fp8 per
+// row over the workgroup's 128 columns, one scale group. Only the 16-row
+// subtiles that hold pairs are multiplied.
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
                                                         int64_t H, int64_t I, int topk,
@@ -441,7 +442,8 @@ __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restric
     __syncthreads();
   }
 
-  if constexpr (NC == kKB) {
+  static_assert(NC == kKB, "a workgroup covers one 128-column scale group of the activations");
+  {
     // 128 columns: one whole scale group of the activations, so they are
     // quantised here (s = max(max |a|, 1e-10) / 448, q = rne(clamp(a / s)),
     // the rule of act_quant_kernel, on the same bf16 values).
@@ -494,39 +496,6 @@ __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restric
         *reinterpret_cast<u32x4*>(work.act + static_cast<int64_t>(p) * I + c0 + piece * 16) =
             *reinterpret_cast<const u32x4*>(s_act + row * kKB + piece * 16);
     }
-    return;
-  }
-
-  uint16_t* s_o = reinterpret_cast<uint16_t*>(s_a);  // [kBM][NC] bf16
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    if (mi >= nmi) continue;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float g = bf16_round(acc[mi][0][r]), u = bf16_round(acc[mi][1][r]);
-      const float a = bf16_round(g / (1.0f + expf(-g)) * u);
-      float m = fabsf(a);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
-      const int row = 16 * mi + 4 * q + r;
-      if (j == 0) s_m[wave][row] = m;
-      s_o[row * NC + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(a));
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < kBM * (NW / 2); i += NT) {  // maxima of the 32-column blocks
-    const int row = i % kBM, k = i / kBM;
-    const int p = s_pair[row];
-    if (p >= 0)
-      work.amax32[static_cast<int64_t>(p) * (I / 32) + c0 / 32 + k] = fmaxf(s_m[2 * k][row], s_m[2 * k + 1][row]);
-  }
-  constexpr int kPieces = NC / 8;  // 16-byte pieces per row
-  for (int i = tid; i < kBM * kPieces; i += NT) {
-    const int row = i / kPieces, piece = i - row * kPieces;
-    const int p = s_pair[row];
-    if (p >= 0)
-      *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
-          *reinterpret_cast<const u32x4*>(s_o + row * NC + piece * 8);
   }
 }
 
@@ -539,16 +508,29 @@ struct KBlock {
 
 // CH consecutive K blocks from kb0, the block index clamped at KB - 1 so
 // that the loads are unconditional (a clamped block is loaded, not used).
+// The weight rows (B) and the token rows (A) load separately, so that the
+// weights can be requested before the tile's rows are looked up.
 template <int CH>
-__device__ __forceinline__ void load_chunk(KBlock (&c)[CH], const uint8_t* arow, const uint8_t* const (&brow)[2],
-                                           int kb0, int KB) {
+__device__ __forceinline__ void load_chunk_b(KBlock (&c)[CH], const uint8_t* const (&brow)[2], int kb0, int KB) {
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int kb = kb0 + i < KB ? kb0 + i : KB - 1;
-    load32(arow + kb * kKB, c[i].a);
     load32(brow[0] + kb * kKB, c[i].b[0]);
     load32(brow[1] + kb * kKB, c[i].b[1]);
   }
+}
+
+template <int CH>
+__device__ __forceinline__ void load_chunk_a(KBlock (&c)[CH], const uint8_t* arow, int kb0, int KB) {
+#pragma unroll
+  for (int i = 0; i < CH; ++i) load32(arow + (kb0 + i < KB ? kb0 + i : KB - 1) * kKB, c[i].a);
+}
+
+template <int CH>
+__device__ __forceinline__ void load_chunk(KBlock (&c)[CH], const uint8_t* arow, const uint8_t* const (&brow)[2],
+                                           int kb0, int KB) {
+  load_chunk_b<CH>(c, brow, kb0, KB);
+  load_chunk_a<CH>(c, arow, kb0, KB);
 }
 
 // The rows of one 16-row subtile (r0 = its first row in the tile): the
@@ -566,11 +548,12 @@ __device__ __forceinline__ void subtile_rows(const Tile& tile, int r0, const int
 }
 
 // Runs the K blocks of a subtile through `step`, CH blocks per chunk, the
-// next chunk's loads in flight while the current one is multiplied.
+// next chunk's loads in flight while the current one is multiplied. c0
+// arrives holding (or loading) blocks 0 .. CH-1.
 template <int CH, typename Step>
-__device__ __forceinline__ void run_chunks(const uint8_t* arow, const uint8_t* const (&brow)[2], int KB, Step step) {
-  KBlock c0[CH], c1[CH];
-  load_chunk<CH>(c0, arow, brow, 0, KB);
+__device__ __forceinline__ void run_chunks(KBlock (&c0)[CH], const uint8_t* arow, const uint8_t* const (&brow)[2],
+                                           int KB, Step step) {
+  KBlock c1[CH];
   if (KB <= CH) {
 #pragma unroll
     for (int i = 0; i < CH; ++i)
@@ -589,97 +572,120 @@ __device__ __forceinline__ void run_chunks(const uint8_t* arow, const uint8_t* c
   }
 }
 
-// GEMM1 for small batches (decode): one 16-row subtile of a tile x 32
-// activation columns, 2 waves x 16 columns. Every operand is loaded straight
-// from global memory, CH K blocks ahead of the MFMAs, so a lone wave is not
-// bound by one load latency per K block. Each column's sum runs over the K
-// blocks in the same order and with the same scaling as in gemm1_kernel,
-// so the bits are the same. 1-D grid in XCD order over (subtile, column
-// block) items.
-template <int CH>
-__global__ void __launch_bounds__(128) gemm1_narrow_kernel(const uint8_t* __restrict__ xq,
-                                                           const float* __restrict__ xs, int64_t H, int64_t I,
-                                                           int topk, const uint8_t* __restrict__ w13,
-                                                           const float* __restrict__ w13_scale,
-                                                           const int32_t* __restrict__ offsets,
-                                                           const int32_t* __restrict__ pairs,
-                                                           const int32_t* __restrict__ tiles, Work work) {
+// GEMM1 for small batches (decode): one 16-row subtile of a tile x 16
+// activation columns (gate rows n and up rows I + n) per workgroup. A lone
+// subtile is bound by load latency, so the 4 waves split each round of up to
+// kSplitRound K blocks, issue all their loads at once and park the raw
+// 16x16x128 products in LDS; wave 0 then scales them and sums them in K
+// order with one FMA per block and output, the arithmetic of gemm1_kernel,
+// so the bits do not depend on the split. 1-D grid in XCD order over
+// (subtile, column block) items.
+constexpr int kSplitRound = 16;  // K blocks per round, kSplitRound / 4 per wave
+
+__global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* __restrict__ xq,
+                                                                const float* __restrict__ xs, int64_t H, int64_t I,
+                                                                int topk, const uint8_t* __restrict__ w13,
+                                                                const float* __restrict__ w13_scale,
+                                                                const int32_t* __restrict__ offsets,
+                                                                const int32_t* __restrict__ pairs,
+                                                                const int32_t* __restrict__ tiles, int nsub,
+                                                                Work work) {
+  constexpr int kPerWave = kSplitRound / (kThreads / 64);
   __shared__ int s_row[16];
   __shared__ int s_pair[16];
   __shared__ float s_xs[16 * kMaxKB];
   __shared__ float s_sw[2][kMaxKB];
-  __shared__ float s_m[2][16];
-  __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * 32];
+  __shared__ float s_m[16];
+  __shared__ f32x4 s_part[kSplitRound][2][64];
+  __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * 16];
 
-  const int ncb = static_cast<int>(I / 32);
+  const int ncb = static_cast<int>(I / 16);
   Tile tile;
   int ti, item;
-  xcd_item(4 * ncb, ti, item);
+  xcd_item(nsub * ncb, ti, item);
   if (!load_tile_at(ti, tiles, offsets, tile)) return;
   const int sub = item / ncb, r0 = 16 * sub;
   if (r0 >= tile.count) return;
-  const int c0 = (item - sub * ncb) * 32;
+  const int c0 = (item - sub * ncb) * 16;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(H / kKB);
 
+  // The first round's weight rows depend on the slot alone: request them
+  // before the rows and scales are looked up.
+  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
+  const int64_t n = c0 + j;
+  const uint8_t* const brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
+  const int kw0 = wave * kPerWave;  // this wave's first block of each round, less the round's start
+  KBlock c[kPerWave];
+  load_chunk_b<kPerWave>(c, brow, kw0, KB);
+
   subtile_rows(tile, r0, pairs, topk, s_pair, s_row);
   __syncthreads();
-  for (int i = tid; i < 16 * KB; i += 128) {
+  for (int i = tid; i < 16 * KB; i += kThreads) {
     const int r = i / KB, kb = i - r * KB;
     s_xs[i] = xs[static_cast<int64_t>(s_row[r]) * KB + kb];
   }
   {
     const float* sg = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + c0 / kKB) * KB;
     const float* su = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
-    for (int i = tid; i < 2 * KB; i += 128) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
+    for (int i = tid; i < 2 * KB; i += kThreads) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
   }
   const uint8_t* arow = xq + static_cast<int64_t>(s_row[j]) * H + 32 * q;
-  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
-  const int64_t n = c0 + 16 * wave + j;
-  const uint8_t* const brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
+  load_chunk_a<kPerWave>(c, arow, kw0, KB);
   __syncthreads();  // s_xs, s_sw
 
-  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  run_chunks<CH>(arow, brow, KB, [&](const KBlock& k, int kb) {
-    const float g = s_sw[0][kb], u = s_sw[1][kb];
-    float sc[2][4];
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // wave 0's sums
+  for (int k0 = 0; k0 < KB; k0 += kSplitRound) {
+    const int kw = k0 + kw0;  // this wave's first block of the round
+    if (k0 > 0) load_chunk<kPerWave>(c, arow, brow, kw, KB);
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      if (kw + i >= KB) continue;
+      s_part[wave * kPerWave + i][0][lane] = mfma_k128(c[i].a, c[i].b[0]);
+      s_part[wave * kPerWave + i][1][lane] = mfma_k128(c[i].a, c[i].b[1]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int nk = KB - k0 < kSplitRound ? KB - k0 : kSplitRound;
+      for (int t = 0; t < nk; ++t) {
+        const int kb = k0 + t;
+        const float g = s_sw[0][kb], u = s_sw[1][kb];
+        const f32x4 pg = s_part[t][0][lane], pu = s_part[t][1][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sa = s_xs[(4 * q + r) * KB + kb];
+          acc[0][r] = fmaf(pg[r], sa * g, acc[0][r]);
+          acc[1][r] = fmaf(pu[r], sa * u, acc[1][r]);
+        }
+      }
+    }
+    __syncthreads();  // s_part is rewritten by the next round
+  }
+
+  if (wave == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float sa = s_xs[(4 * q + r) * KB + kb];
-      sc[0][r] = sa * g;
-      sc[1][r] = sa * u;
+      const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
+      const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+      float m = fabsf(a);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      const int row = 4 * q + r;
+      if (j == 0) s_m[row] = m;
+      s_o[row * 16 + j] = static_cast<uint16_t>(bf16_bits(a));
     }
-#pragma unroll
-    for (int si = 0; si < 2; ++si) {
-      const f32x4 part = mfma_k128(k.a, k.b[si]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[si][r] = fmaf(part[r], sc[si][r], acc[si][r]);
-    }
-  });
-
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
-    const float a = bf16_round(g / (1.0f + expf(-g)) * u);
-    float m = fabsf(a);
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
-    const int row = 4 * q + r;
-    if (j == 0) s_m[wave][row] = m;
-    s_o[row * 32 + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(a));
   }
   __syncthreads();
   if (tid < 16) {
     const int p = s_pair[tid];
-    if (p >= 0) work.amax32[static_cast<int64_t>(p) * (I / 32) + c0 / 32] = fmaxf(s_m[0][tid], s_m[1][tid]);
-  }
-  if (tid < 64) {  // 16 rows x 4 pieces of 16 bytes
-    const int row = tid >> 2, piece = tid & 3;
+    if (p >= 0) work.amax16[static_cast<int64_t>(p) * (I / 16) + c0 / 16] = s_m[tid];
+  } else if (tid < 48) {  // 16 rows x 2 pieces of 16 bytes
+    const int row = (tid - 16) >> 1, piece = tid & 1;
     const int p = s_pair[row];
     if (p >= 0)
       *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
-          *reinterpret_cast<const u32x4*>(s_o + row * 32 + piece * 8);
+          *reinterpret_cast<const u32x4*>(s_o + row * 16 + piece * 8);
   }
 }
 
@@ -693,8 +699,8 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
                                                                 const float* __restrict__ w2_scale,
                                                                 const int32_t* __restrict__ offsets,
                                                                 const int32_t* __restrict__ pairs,
-                                                                const int32_t* __restrict__ tiles, Work work,
-                                                                uint16_t* __restrict__ out) {
+                                                                const int32_t* __restrict__ tiles, int nsub,
+                                                                Work work, uint16_t* __restrict__ out) {
   __shared__ int s_row[16];
   __shared__ int s_pair[16];
   __shared__ float s_as[16 * kMaxKB];
@@ -705,7 +711,7 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   const int ncb = static_cast<int>(H / kBN);
   Tile tile;
   int ti, item;
-  xcd_item(4 * ncb, ti, item);
+  xcd_item(nsub * ncb, ti, item);
   if (!load_tile_at(ti, tiles, offsets, tile)) return;
   const int sub = item / ncb, r0 = 16 * sub;
   if (r0 >= tile.count) return;
@@ -713,6 +719,13 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(I / kKB);
+
+  // Weight rows of the first chunk first: they depend on the slot alone.
+  const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
+  const uint8_t* const brow[2] = {wslot + static_cast<int64_t>(n0 + 32 * wave + j) * I + 32 * q,
+                                  wslot + static_cast<int64_t>(n0 + 32 * wave + 16 + j) * I + 32 * q};
+  KBlock c0[CH];
+  load_chunk_b<CH>(c0, brow, 0, KB);
 
   subtile_rows(tile, r0, pairs, 1, s_pair, s_row);
   __syncthreads();
@@ -723,13 +736,11 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   if (tid < 16) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
   if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
   const uint8_t* arow = work.act + static_cast<int64_t>(s_row[j]) * I + 32 * q;
-  const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
-  const uint8_t* const brow[2] = {wslot + static_cast<int64_t>(n0 + 32 * wave + j) * I + 32 * q,
-                                  wslot + static_cast<int64_t>(n0 + 32 * wave + 16 + j) * I + 32 * q};
+  load_chunk_a<CH>(c0, arow, 0, KB);
   __syncthreads();  // s_as, s_w, s_sw
 
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  run_chunks<CH>(arow, brow, KB, [&](const KBlock& k, int kb) {
+  run_chunks<CH>(c0, arow, brow, KB, [&](const KBlock& k, int kb) {
     const float w = s_sw[kb];
     float sc[4];
 #pragma unroll
@@ -775,8 +786,11 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(int64_t I, const in
   for (int i = tid; i < tile.count * G; i += kThreads) {
     const int r = i / G, g = i - r * G;
     const int64_t p = s_p[r];
-    const float* m = work.amax32 + p * (I / 32) + 4 * g;
-    const float s = quant_scale(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3])));
+    const float* m = work.amax16 + p * (I / 16) + 8 * g;
+    float mx = m[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) mx = fmaxf(mx, m[k]);
+    const float s = quant_scale(mx);
     s_s[i] = s;
     work.acts[p * G + g] = s;
   }
@@ -1032,37 +1046,38 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
   const unsigned ty = static_cast<unsigned>(bound);
   const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
-  const int64_t g1 = tiles8 * (I / kC1), g2 = tiles8 * (H / kBN);
-  XP_REQUIRE(g1 <= INT32_MAX && g2 <= INT32_MAX, "xp_moe_experts: grid too large");
-  // Prefill-sized calls take 16*kWideNW activation columns per workgroup
-  // (token rows shared by more waves), small calls 32 (more workgroups for
-  // few pairs). Every column is computed the same way in both.
+  const int64_t g2 = tiles8 * (H / kBN);
+  XP_REQUIRE(g2 <= INT32_MAX, "xp_moe_experts: grid too large");
+  // Prefill-sized calls take 16*kWideNW = 128 activation columns of a tile
+  // per workgroup (token rows shared by more waves) and quantise them there;
+  // small calls take 16 rows x 16 columns (more workgroups for few pairs)
+  // and quantise in act_quant. Every column is computed the same way in both.
   const bool narrow = bound < kWideTiles;
-  if (!narrow && I % (16 * kWideNW) == 0) {
+  // 16-row subtiles a tile can have: a tile holds at most min(64, npairs) pairs.
+  const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
+  if (!narrow) {
     const int64_t g1w = tiles8 * (I / (16 * kWideNW));
     hipLaunchKernelGGL(gemm1_kernel<kWideNW>, dim3(static_cast<unsigned>(g1w)), dim3(64 * kWideNW), 0,
                        as_stream(stream), xq, xs,
                        H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
-  } else if (!narrow) {
-    hipLaunchKernelGGL(gemm1_kernel<2>, dim3(static_cast<unsigned>(g1)), dim3(128), 0, as_stream(stream), xq, xs, H,
-                       I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
   } else {
-    // Few pairs: 16-row subtiles, operands loaded several K blocks ahead.
-    hipLaunchKernelGGL(gemm1_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(4 * g1)), dim3(128), 0,
-                       as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs,
-                       tiles, w);
+    // Few pairs: 16-row subtiles x 16 columns, the K blocks split over 4 waves.
+    const int64_t g1n = tiles8 * nsub * (I / 16);
+    XP_REQUIRE(g1n <= INT32_MAX, "xp_moe_experts: grid too large");
+    hipLaunchKernelGGL(gemm1_narrow_kernel, dim3(static_cast<unsigned>(g1n)), dim3(kThreads), 0, as_stream(stream), xq,
+                       xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, nsub, w);
   }
   int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
-  if (narrow || I % (16 * kWideNW) != 0 || 16 * kWideNW != kKB) {  // else gemm1 quantised the activations
+  if (narrow) {  // else gemm1 quantised the activations
     hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles,
                        w);
     rc = check_launch("act_quant_kernel");
     if (rc) return rc;
   }
   if (narrow)
-    hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(4 * g2)), dim3(kThreads), 0,
-                       as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
+    hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(nsub * g2)), dim3(kThreads), 0,
+                       as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, nsub, w, out);
   else
     hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, as_stream(stream), H, I,
                        topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
