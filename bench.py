@@ -131,9 +131,10 @@ def bench_decode(args, dev, cores):
     raw_gbps = sum(n_bytes) * count / (ms * 1e-3) / 1e9
     log(f"decode: {ms:.3f} ms/launch, {gbps:.1f} GB/s algorithmic, {raw_gbps:.1f} GB/s raw output")
 
-    # Sweep of rows per launch (32..256): same kernel, shorter todo.
-    sweep = {}
-    for r in (32, 64, 128):
+    # Sweep of rows per launch (1..256): same kernel, shorter todo. A decode
+    # step expands the misses of one layer, about 1-2 rows per launch.
+    sweep, sweep_us = {}, {}
+    for r in (1, 2, 4, 8, 32, 64, 128):
         if r >= count:
             continue
         t = todo[:r]
@@ -147,7 +148,9 @@ def bench_decode(args, dev, cores):
         torch.cuda.synchronize()
         ms_r = e0.elapsed_time(e1) / 5
         sweep[str(r)] = round(algorithmic_bytes([s[:r] for s in stg_np], n_bytes) / (ms_r * 1e-3) / 1e9, 1)
+        sweep_us[str(r)] = round(ms_r * 1e3, 1)
     sweep[str(count)] = round(gbps, 1)
+    sweep_us[str(count)] = round(ms * 1e3, 1)
 
     # CPU baseline: the oracle's C decoder on a bounded sample, all cores.
     sample = max(1, min(args.cpu_rows, count))
@@ -169,6 +172,7 @@ def bench_decode(args, dev, cores):
         "raw_gbps": raw_gbps,
         "alg_bytes": alg,
         "sweep": sweep,
+        "sweep_us": sweep_us,
         "cpu": {"value": round(cpu_gbps, 3), "unit": "GB/s", "cores": cores, "kind": "port",
                 "sample": f"oracle C decoder (the reference's sequential decode rule), {sample} of the "
                           f"{count} experts (w13+w2 rows), {reps} repetitions, threads over groups"},
@@ -900,6 +904,7 @@ def main() -> None:
         "cpu_baseline": dec["cpu"],
         "decode_raw_output_gbps": round(dec["raw_gbps"], 2),
         "decode_gbps_by_rows": dec["sweep"],
+        "decode_us_by_rows": dec["sweep_us"],
         **extras,
     }
     print(json.dumps(line), flush=True)
