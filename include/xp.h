@@ -207,7 +207,7 @@ int xp_fetch_set_timing(int64_t retry_us, int64_t giveup);
 /* One weight name of a decode. */
 typedef struct xp_decode_name {
   const void* stg;    /* compressed rows, pitch bytes apart (HBM) */
-  int64_t pitch;
+  int64_t pitch;      /* multiple of 16, below 2 GiB */
   int64_t stg_rows;
   void* dst;          /* raw destination rows, row_bytes apart (HBM) */
   int64_t dst_rows;
@@ -217,7 +217,10 @@ typedef struct xp_decode_name {
 /* Expand staging row j (the j-th entry of todo) into dst row dst_row[e] for
  * every name. Skips -1 entries, experts with cache_row[e] >= 0 and (when
  * skip != NULL) experts listed in skip[K]. lut is the layer's
- * uint8[E][num_names][512]. chunk = values per lane (512 in production).
+ * uint8[E][num_names][512]. chunk = values per lane (512 in production;
+ * any multiple of 32 up to 4096). A record's reads stay inside its pitch
+ * whatever its contents, so a corrupt record yields wrong bytes in its own
+ * destination row only.
  * Replaces decode_rows (codec.py:297-327) and _decode_rows_kernel /
  * _decode_group (codec.py:204-289). */
 int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts,
