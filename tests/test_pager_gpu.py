@@ -122,6 +122,19 @@ def test_prefill_overflow_matches_one_shot(model, compress, R, T):
     assert m.pager.store.failed is None
 
 
+def test_paging_file_flushed_after_the_last_layer(model):
+    """Once every layer's weights are in, the pager flushes the paging file
+    (so that the server's reads do not wait on the page cache's write-back)
+    and the reads that follow still serve the right rows."""
+    m = model(64, 4, 16, 8, True, L=2)
+    assert m.pager.layers_ready == 2 and m.pager.store.synced is not None
+    rng = np.random.default_rng(5)
+    for i, layer in enumerate(m.layers):
+        x, tw, ids = routing(rng, 12, m.E, 4, zipf=0.3)
+        assert same(layer.forward(x, tw, ids), m.one_shot(i, x, tw, ids))
+    assert m.pager.store.failed is None
+
+
 def test_prefill_between_decode_steps_two_layers(model):
     """Layers share the working slab (and its head as decode staging)."""
     m = model(64, 4, 16, 8, True, L=2)

@@ -100,6 +100,8 @@ class Pager:
         if hidden % moe.BLOCK or intermediate % moe.BLOCK:
             raise ValueError(f"hidden={hidden} and intermediate={intermediate} must be multiples of {moe.BLOCK}")
         self.settings = s
+        self.num_layers = num_layers
+        self.layers_ready = 0
         self.num_experts, self.hidden, self.intermediate = E, hidden, intermediate
         dev = torch.device(device)
         if dev.type == "cuda" and dev.index is None:
@@ -133,6 +135,15 @@ class Pager:
 
     def add_layer(self) -> "PagedExperts":
         return PagedExperts(self)
+
+    def layer_ready(self) -> None:
+        """Count a layer whose weights are in; after the last one, flush the
+        paging file, so that serving reads do not share the disk with the
+        page cache's write-back of the load (not a reference step)."""
+        self.layers_ready += 1
+        if self.layers_ready == self.num_layers and self.store.path is not None:
+            seconds = self.store.sync()
+            logger.info("vllm-expert-pager: paging file flushed to disk in %.1f s", seconds)
 
 
 class PagedExperts:
@@ -195,6 +206,7 @@ class PagedExperts:
             if store.compress else None
         )
         self.ready = True
+        p.layer_ready()
 
     # ---- forward ----
 

@@ -21,6 +21,7 @@ import logging
 import os
 import signal
 import threading
+import time
 
 import numpy as np
 import torch
@@ -189,6 +190,7 @@ class Store:
 
         self.path = path if R < E else None
         self.fd_w = self.fd_r = None
+        self.synced: float | None = None  # seconds of the last sync()
         if self.path is not None:
             size = L * E * self.record_bytes
             if os.path.exists(path) and os.path.getsize(path) != size:
@@ -251,6 +253,23 @@ class Store:
         self._so.ssd_stats(ctypes.c_void_p(self._handle), ctypes.byref(fetches), ctypes.byref(reads),
                            ctypes.byref(io_seconds), ctypes.byref(missed))
         return fetches.value, reads.value, io_seconds.value, missed.value
+
+    def sync(self) -> float:
+        """Flush the paging file to the disk and drop it from the page cache;
+        returns the seconds it took (0 without a paging file).
+
+        The records are written through the page cache. Until the kernel has
+        written them back, the server's O_DIRECT reads share the disk with that
+        writeback (and a read of a range with dirty pages waits for it), so a
+        loader calls this once after the last layer.
+        """
+        if self.fd_w is None:
+            return 0.0
+        t0 = time.perf_counter()
+        os.fdatasync(self.fd_w)
+        os.posix_fadvise(self.fd_w, 0, 0, os.POSIX_FADV_DONTNEED)
+        self.synced = time.perf_counter() - t0
+        return self.synced
 
     def stats(self) -> tuple[int, int, float, int]:
         """(requests served, experts read, seconds from request to done, requests missed)."""
