@@ -296,6 +296,38 @@ def test_publish_and_wait_with_two_tickets(store):
             assert torch.equal(store.pinned[name][r], encoded(store, layer, e, name))
 
 
+def test_large_pinned_tier_is_allocated_at_its_size():
+    """Counterpart of the reference's test_large_pinned_is_not_rounded_to_pow2
+    (tests/test_store.py:360-371). There the RAM tier came from torch's
+    caching host allocator, which rounds large blocks up to a power of two.
+    Here each name's tier is one hipHostMalloc of exactly rows x pitch bytes:
+    a 1.5 GiB tier reports 1.5 GiB, and the GPU reads its last row."""
+    _, gather, Store, _ = _mods()
+    dev = torch.device("cuda")
+    row = 3 * 2**20
+    E = 511  # 511 RAM rows + 1 working row = 512 rows of 3 MiB
+    s = Store(1, E, E, 1, {"w13_weight": row}, False, 1.0, None, dev)
+    try:
+        assert [b.nbytes for b in s._buffers if b.nbytes >= row] == [3 * 2**29]
+        e = E - 1
+        want = torch.arange(row // 4, dtype=torch.int32) * 7 + 3
+        s.write(0, e, "w13_weight", want)
+        todo = torch.tensor([e], dtype=torch.int64, device=dev)
+        dst_row = torch.zeros((E,), dtype=torch.int64, device=dev)
+        cache_row = torch.full((E,), -1, dtype=torch.int64, device=dev)
+        src_row = torch.arange(E, dtype=torch.int64, device=dev)
+        cache = [torch.zeros((1, row // 4), dtype=torch.int32, device=dev)]
+        dst = [torch.zeros((1, row // 4), dtype=torch.int32, device=dev)]
+        scale = [torch.ones((E, 4), dtype=torch.int32, device=dev)]
+        sdst = [torch.zeros((1, 4), dtype=torch.int32, device=dev)]
+        gather.gather_rows(todo, dst_row, cache_row, src_row, 0, [s.view["w13_weight"]], cache, dst, None, scale,
+                           sdst)
+        torch.cuda.synchronize()
+        assert torch.equal(dst[0][0].cpu(), want)
+    finally:
+        s.close()
+
+
 def test_rejects_foreign_file(tmp_path):
     Store = _mods()[2]
     path = tmp_path / "expert_pager.bin"
