@@ -776,31 +776,26 @@ __global__ void __launch_bounds__(kThreads) act_quant_kernel(int64_t I, const in
                                                              const int32_t* __restrict__ pairs,
                                                              const int32_t* __restrict__ tiles, Work work) {
   __shared__ int s_p[kBM];
-  __shared__ float s_s[kBM * kMaxKB];
   Tile tile;
   if (!load_tile(tiles, offsets, tile)) return;
   const int tid = threadIdx.x;
   const int G = static_cast<int>(I / kKB);
   if (tid < tile.count) s_p[tid] = pairs[tile.first + tid];
   __syncthreads();
-  for (int i = tid; i < tile.count * G; i += kThreads) {
-    const int r = i / G, g = i - r * G;
+  // Each thread quantises 8 columns of one row; it reads that row's eight
+  // 16-column maxima of the group (the same values for the 16 threads of a
+  // group) together with its 8 activations, so no step waits on another.
+  const int per_row = static_cast<int>(I / 8);
+  for (int i = tid; i < tile.count * per_row; i += kThreads) {
+    const int r = i / per_row, c = (i - r * per_row) * 8, g = c / kKB;
     const int64_t p = s_p[r];
     const float* m = work.amax16 + p * (I / 16) + 8 * g;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c);
     float mx = m[0];
 #pragma unroll
     for (int k = 1; k < 8; ++k) mx = fmaxf(mx, m[k]);
     const float s = quant_scale(mx);
-    s_s[i] = s;
-    work.acts[p * G + g] = s;
-  }
-  __syncthreads();
-  const int per_row = static_cast<int>(I / 8);
-  for (int i = tid; i < tile.count * per_row; i += kThreads) {
-    const int r = i / per_row, c = (i - r * per_row) * 8;
-    const int64_t p = s_p[r];
-    const float s = s_s[r * G + c / kKB];
-    const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c);
+    if (c % kKB == 0) work.acts[p * G + g] = s;
     uint32_t q0 = 0, q1 = 0;
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -931,21 +926,35 @@ __global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, c
 
 // out[t] = bf16(sum over k of contrib[t*topk + k]) in fp32, k ascending,
 // over the pairs whose id is a valid expert.
+template <typename Id>
 __global__ void __launch_bounds__(256) topk_sum_kernel(const uint16_t* __restrict__ contrib, int64_t H, int topk,
-                                                       const void* ids, int eb, int E, uint16_t* __restrict__ out) {
+                                                       const Id* __restrict__ ids, int E, uint16_t* __restrict__ out) {
   const int64_t t = blockIdx.y;
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8;
   if (c >= H) return;
   float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < topk; ++k) {
-    const int64_t p = t * topk + k;
-    const int64_t e = load_id(ids, eb, p);
-    if (e < 0 || e >= E) continue;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(contrib + p * H + c);
+  // Eight pairs at a time: the ids and the contribution rows are loaded
+  // together (a row is read whatever its id, and skipped in the sum), so
+  // the loads do not wait on one another.
+  for (int k0 = 0; k0 < topk; k0 += 8) {
+    bool ok[8];
+    u32x4 v[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      s[2 * i] += bf16_value(v[i] & 0xffffu);
-      s[2 * i + 1] += bf16_value(v[i] >> 16);
+    for (int i = 0; i < 8; ++i) {
+      const int k = k0 + i < topk ? k0 + i : topk - 1;
+      const int64_t p = t * topk + k;
+      const int64_t e = ids[p];
+      ok[i] = k0 + i < topk && e >= 0 && e < E;
+      v[i] = *reinterpret_cast<const u32x4*>(contrib + p * H + c);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (!ok[i]) continue;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        s[2 * w] += bf16_value(v[i][w] & 0xffffu);
+        s[2 * w + 1] += bf16_value(v[i][w] >> 16);
+      }
     }
   }
   u32x4 o;
@@ -1094,8 +1103,14 @@ int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk, int64_t H,
   XP_REQUIRE(contrib && out && topk_ids && aligned16(contrib) && aligned16(out),
              "xp_moe_topk_sum: null or misaligned buffer");
   const unsigned bx = static_cast<unsigned>((H / 8 + 255) / 256);
-  hipLaunchKernelGGL(topk_sum_kernel, dim3(bx, static_cast<unsigned>(T)), dim3(256), 0, as_stream(stream), contrib, H,
-                     static_cast<int>(topk), topk_ids, topk_elem_bytes, static_cast<int>(num_experts), out);
+  if (topk_elem_bytes == 8)
+    hipLaunchKernelGGL(topk_sum_kernel<int64_t>, dim3(bx, static_cast<unsigned>(T)), dim3(256), 0, as_stream(stream),
+                       contrib, H, static_cast<int>(topk), static_cast<const int64_t*>(topk_ids),
+                       static_cast<int>(num_experts), out);
+  else
+    hipLaunchKernelGGL(topk_sum_kernel<int32_t>, dim3(bx, static_cast<unsigned>(T)), dim3(256), 0, as_stream(stream),
+                       contrib, H, static_cast<int>(topk), static_cast<const int32_t*>(topk_ids),
+                       static_cast<int>(num_experts), out);
   return check_launch("topk_sum_kernel");
 }
 
