@@ -33,13 +33,13 @@ def _mods():
 class Model:
     """A pager with L layers of random block-fp8 experts, and the same weights on the GPU."""
 
-    def __init__(self, tmp_path, E, S, R, W, compress, L=1, seed=0, log_interval=0):
+    def __init__(self, tmp_path, E, S, R, W, compress, L=1, seed=0, log_interval=0, declared=None):
         moe, pager = _mods()
         settings = pager.Settings(
             cache_slots=S, ram_slots=R, ssd_path=str(tmp_path / "paging.bin") if R < E else None,
             compress="on" if compress else "off", working_rows=W, log_interval=log_interval,
         )
-        self.pager = pager.Pager(settings, L, E, H, I, torch.device("cuda"))
+        self.pager = pager.Pager(settings, declared or L, E, H, I, torch.device("cuda"))
         self.E = E
         self.layers, self.weights = [], []
         rng = np.random.default_rng(seed)
@@ -133,6 +133,17 @@ def test_paging_file_flushed_after_the_last_layer(model):
         x, tw, ids = routing(rng, 12, m.E, 4, zipf=0.3)
         assert same(layer.forward(x, tw, ids), m.one_shot(i, x, tw, ids))
     assert m.pager.store.failed is None
+
+
+def test_paging_file_flushed_at_the_first_forward(model):
+    """A model with fewer MoE layers than layers (dense layers in between)
+    never reports its last layer: the flush then comes at the first forward."""
+    m = model(64, 4, 16, 8, True, L=1, declared=3)
+    assert m.pager.layers_ready == 1 and m.pager.store.synced is None
+    rng = np.random.default_rng(6)
+    x, tw, ids = routing(rng, 1, m.E, 4)
+    assert same(m.layers[0].forward(x, tw, ids), m.one_shot(0, x, tw, ids))
+    assert m.pager.store.synced is not None
 
 
 def test_prefill_between_decode_steps_two_layers(model):

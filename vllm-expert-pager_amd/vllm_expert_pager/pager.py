@@ -138,10 +138,17 @@ class Pager:
 
     def layer_ready(self) -> None:
         """Count a layer whose weights are in; after the last one, flush the
-        paging file, so that serving reads do not share the disk with the
-        page cache's write-back of the load (not a reference step)."""
+        paging file (``flush``)."""
         self.layers_ready += 1
-        if self.layers_ready == self.num_layers and self.store.path is not None:
+        if self.layers_ready == self.num_layers:
+            self.flush()
+
+    def flush(self) -> None:
+        """Flush the paging file to disk once, so that serving reads do not
+        share the disk with the page cache's write-back of the load (not a
+        reference step). Runs after the last layer's weights are in, or at
+        the first forward when the model has fewer MoE layers than layers."""
+        if self.store.path is not None and self.store.synced is None:
             seconds = self.store.sync()
             logger.info("vllm-expert-pager: paging file flushed to disk in %.1f s", seconds)
 
@@ -215,6 +222,8 @@ class PagedExperts:
         if not self.ready:
             raise RuntimeError(f"layer {self.layer}: setup() has not run")
         store = self.store
+        if store.path is not None and store.synced is None:
+            self.pager.flush()
         if store.failed is not None:
             raise RuntimeError(f"vllm-expert-pager: SSD read failed\n{store.failed}")
         # The path is chosen from the shape alone, so capture and replay of a
