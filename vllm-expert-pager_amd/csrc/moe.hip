@@ -21,8 +21,8 @@
 // and cuts them into tiles of 64 pairs of one slot. gemm1 takes one tile
 // and 128 activation columns per workgroup at prefill sizes; for few pairs
 // it takes 16 rows and 16 columns, with the K blocks split over its waves
-// (so a decode step of 8 pairs spreads over 256 workgroups). act_quant takes
-// one tile, gemm2 one tile (or 16 rows) and 128 output columns. Launch grids
+// (so a decode step of 8 pairs spreads over 256 workgroups). gemm2 takes
+// one tile (or 16 rows) and 128 output columns. Launch grids
 // are sized from the shapes alone (a bound on the tile count), so the
 // sequence is graph-capturable; workgroups past the live tile count exit at
 // once.
@@ -254,10 +254,6 @@ __device__ __forceinline__ bool load_tile_at(int i, const int32_t* tiles, const 
   return true;
 }
 
-__device__ __forceinline__ bool load_tile(const int32_t* tiles, const int32_t* offsets, Tile& t) {
-  return load_tile_at(blockIdx.y, tiles, offsets, t);
-}
-
 // Tile rows: the pair of each row (-1 for padding) and the A row it reads
 // (padding rows repeat the tile's first pair, so every load stays inside
 // the operand).
@@ -446,7 +442,7 @@ __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restric
   {
     // 128 columns: one whole scale group of the activations, so they are
     // quantised here (s = max(max |a|, 1e-10) / 448, q = rne(clamp(a / s)),
-    // the rule of act_quant_kernel, on the same bf16 values).
+    // the rule gemm2_narrow_kernel applies, on the same bf16 values).
     float av[4][4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
@@ -544,31 +540,6 @@ __device__ __forceinline__ void subtile_rows(const Tile& tile, int r0, const int
     const int p = pairs[tile.first + r0 + (tid < n ? tid : 0)];
     s_pair[tid] = tid < n ? p : -1;
     s_row[tid] = p / div;
-  }
-}
-
-// Runs the K blocks of a subtile through `step`, CH blocks per chunk, the
-// next chunk's loads in flight while the current one is multiplied. c0
-// arrives holding (or loading) blocks 0 .. CH-1.
-template <int CH, typename Step>
-__device__ __forceinline__ void run_chunks(KBlock (&c0)[CH], const uint8_t* arow, const uint8_t* const (&brow)[2],
-                                           int KB, Step step) {
-  KBlock c1[CH];
-  if (KB <= CH) {
-#pragma unroll
-    for (int i = 0; i < CH; ++i)
-      if (i < KB) step(c0[i], i);
-    return;
-  }
-  for (int kc = 0; kc < KB; kc += 2 * CH) {
-    load_chunk<CH>(c1, arow, brow, kc + CH, KB);
-#pragma unroll
-    for (int i = 0; i < CH; ++i)
-      if (kc + i < KB) step(c0[i], kc + i);
-    load_chunk<CH>(c0, arow, brow, kc + 2 * CH, KB);
-#pragma unroll
-    for (int i = 0; i < CH; ++i)
-      if (kc + CH + i < KB) step(c1[i], kc + CH + i);
   }
 }
 
@@ -690,8 +661,15 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
 }
 
 // GEMM2 for small batches: one 16-row subtile x 128 output columns (4 waves
-// x 32), operands straight from global memory CH K blocks ahead; same sums
-// and rounding as gemm2_kernel.
+// x 32). The subtile's activations arrive as bf16 rows with their
+// 16-column maxima (gemm1_narrow_kernel's output): the workgroup quantises
+// them itself, with the rule gemm1_kernel applies at prefill sizes, into
+// LDS, kQuantK columns per round, and multiplies them from there; the
+// weight rows come straight from global memory, CH K blocks per load chunk
+// (the first chunk requested before the rows are looked up). Same sums and
+// rounding as gemm2_kernel.
+constexpr int kQuantK = 2048;  // activation columns quantised per LDS round
+
 template <int CH>
 __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64_t I,
                                                                 const float* __restrict__ topk_weight,
@@ -701,11 +679,13 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
                                                                 const int32_t* __restrict__ pairs,
                                                                 const int32_t* __restrict__ tiles, int nsub,
                                                                 Work work, uint16_t* __restrict__ out) {
+  constexpr int kRoundKB = kQuantK / kKB;
   __shared__ int s_row[16];
   __shared__ int s_pair[16];
   __shared__ float s_as[16 * kMaxKB];
   __shared__ float s_w[16];
   __shared__ float s_sw[kMaxKB];
+  __shared__ __attribute__((aligned(16))) uint8_t s_act[16 * kQuantK];
   __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * kBN];
 
   const int ncb = static_cast<int>(H / kBN);
@@ -724,34 +704,64 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
   const uint8_t* const brow[2] = {wslot + static_cast<int64_t>(n0 + 32 * wave + j) * I + 32 * q,
                                   wslot + static_cast<int64_t>(n0 + 32 * wave + 16 + j) * I + 32 * q};
-  KBlock c0[CH];
-  load_chunk_b<CH>(c0, brow, 0, KB);
+  KBlock c[CH];
+  load_chunk_b<CH>(c, brow, 0, KB);
 
   subtile_rows(tile, r0, pairs, 1, s_pair, s_row);
   __syncthreads();
-  for (int i = tid; i < 16 * KB; i += kThreads) {
-    const int r = i / KB, kb = i - r * KB;
-    s_as[i] = work.acts[static_cast<int64_t>(s_row[r]) * KB + kb];
-  }
   if (tid < 16) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
   if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
-  const uint8_t* arow = work.act + static_cast<int64_t>(s_row[j]) * I + 32 * q;
-  load_chunk_a<CH>(c0, arow, 0, KB);
-  __syncthreads();  // s_as, s_w, s_sw
 
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  run_chunks<CH>(c0, arow, brow, KB, [&](const KBlock& k, int kb) {
-    const float w = s_sw[kb];
-    float sc[4];
+  for (int k0 = 0; k0 < KB; k0 += kRoundKB) {
+    const int nk = KB - k0 < kRoundKB ? KB - k0 : kRoundKB;
+    // Quantise columns [128 k0, 128 (k0 + nk)) of the 16 rows: per row and
+    // 128-column group s = max(max |a|, 1e-10) / 448 from the eight
+    // 16-column maxima, q = rne(clamp(a / s)); 8 columns per item.
+    const int per_row = nk * (kKB / 8);
+    for (int i = tid; i < 16 * per_row; i += kThreads) {
+      const int r = i / per_row, c8 = (i - r * per_row) * 8, g = k0 + c8 / kKB;
+      const int64_t p = s_row[r];
+      const float* m = work.amax16 + p * (I / 16) + 8 * g;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + kKB * k0 + c8);
+      float mx = m[0];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = s_as[(4 * q + r) * KB + kb] * w;
+      for (int k = 1; k < 8; ++k) mx = fmaxf(mx, m[k]);
+      const float sc = quant_scale(mx);
+      if (c8 % kKB == 0) s_as[r * KB + g] = sc;
+      uint32_t q0 = 0, q1 = 0;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const f32x4 part = mfma_k128(k.a, k.b[t]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(part[r], sc[r], acc[t][r]);
+      for (int k = 0; k < 2; ++k) {
+        q0 |= to_fp8(clamp_fp8(bf16_value(v[k] & 0xffffu) / sc)) << (16 * k);
+        q0 |= to_fp8(clamp_fp8(bf16_value(v[k] >> 16) / sc)) << (16 * k + 8);
+        q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + k] & 0xffffu) / sc)) << (16 * k);
+        q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + k] >> 16) / sc)) << (16 * k + 8);
+      }
+      *reinterpret_cast<uint2*>(s_act + r * kQuantK + c8) = make_uint2(q0, q1);
     }
-  });
+    __syncthreads();  // s_act, s_as (and s_w, s_sw)
+    for (int kc = 0; kc < nk; kc += CH) {
+      if (k0 + kc > 0) load_chunk_b<CH>(c, brow, k0 + kc, KB);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int kb = k0 + kc + i;
+        if (kc + i >= nk) continue;
+        const u32x4* pa = reinterpret_cast<const u32x4*>(s_act + j * kQuantK + (kb - k0) * kKB + 32 * q);
+        const u32x4 a[2] = {pa[0], pa[1]};
+        const float w = s_sw[kb];
+        float sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = s_as[(4 * q + r) * KB + kb] * w;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const f32x4 part = mfma_k128(a, c[i].b[t]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(part[r], sc[r], acc[t][r]);
+        }
+      }
+    }
+    __syncthreads();  // the next round rewrites s_act
+  }
 
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -767,44 +777,6 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
     if (p >= 0)
       *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
           *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
-  }
-}
-
-// The activations of one tile to fp8: per pair and 128-column group,
-// s = max(max |a|, 1e-10) / 448 and q = rne(clamp(a / s)). grid = (1, tile bound).
-__global__ void __launch_bounds__(kThreads) act_quant_kernel(int64_t I, const int32_t* __restrict__ offsets,
-                                                             const int32_t* __restrict__ pairs,
-                                                             const int32_t* __restrict__ tiles, Work work) {
-  __shared__ int s_p[kBM];
-  Tile tile;
-  if (!load_tile(tiles, offsets, tile)) return;
-  const int tid = threadIdx.x;
-  const int G = static_cast<int>(I / kKB);
-  if (tid < tile.count) s_p[tid] = pairs[tile.first + tid];
-  __syncthreads();
-  // Each thread quantises 8 columns of one row; it reads that row's eight
-  // 16-column maxima of the group (the same values for the 16 threads of a
-  // group) together with its 8 activations, so no step waits on another.
-  const int per_row = static_cast<int>(I / 8);
-  for (int i = tid; i < tile.count * per_row; i += kThreads) {
-    const int r = i / per_row, c = (i - r * per_row) * 8, g = c / kKB;
-    const int64_t p = s_p[r];
-    const float* m = work.amax16 + p * (I / 16) + 8 * g;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c);
-    float mx = m[0];
-#pragma unroll
-    for (int k = 1; k < 8; ++k) mx = fmaxf(mx, m[k]);
-    const float s = quant_scale(mx);
-    if (c % kKB == 0) work.acts[p * G + g] = s;
-    uint32_t q0 = 0, q1 = 0;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      q0 |= to_fp8(clamp_fp8(bf16_value(v[k] & 0xffffu) / s)) << (16 * k);
-      q0 |= to_fp8(clamp_fp8(bf16_value(v[k] >> 16) / s)) << (16 * k + 8);
-      q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + k] & 0xffffu) / s)) << (16 * k);
-      q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + k] >> 16) / s)) << (16 * k + 8);
-    }
-    *reinterpret_cast<uint2*>(work.act + p * I + c) = make_uint2(q0, q1);
   }
 }
 
@@ -1053,14 +1025,14 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   XP_REQUIRE(bound <= 65535, "xp_moe_experts: %lld tiles exceed the launch grid", (long long)bound);
   Work w;
   work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
-  const unsigned ty = static_cast<unsigned>(bound);
   const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
   const int64_t g2 = tiles8 * (H / kBN);
   XP_REQUIRE(g2 <= INT32_MAX, "xp_moe_experts: grid too large");
   // Prefill-sized calls take 16*kWideNW = 128 activation columns of a tile
   // per workgroup (token rows shared by more waves) and quantise them there;
   // small calls take 16 rows x 16 columns (more workgroups for few pairs)
-  // and quantise in act_quant. Every column is computed the same way in both.
+  // and the small-batch gemm2 quantises. Every column is computed the same
+  // way in both.
   const bool narrow = bound < kWideTiles;
   // 16-row subtiles a tile can have: a tile holds at most min(64, npairs) pairs.
   const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
@@ -1078,12 +1050,6 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   }
   int rc = check_launch("gemm1_kernel");
   if (rc) return rc;
-  if (narrow) {  // else gemm1 quantised the activations
-    hipLaunchKernelGGL(act_quant_kernel, dim3(1, ty), dim3(kThreads), 0, as_stream(stream), I, offsets, pairs, tiles,
-                       w);
-    rc = check_launch("act_quant_kernel");
-    if (rc) return rc;
-  }
   if (narrow)
     hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(nsub * g2)), dim3(kThreads), 0,
                        as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, nsub, w, out);
