@@ -142,27 +142,11 @@ __device__ __forceinline__ uint32_t lane_select(unsigned long long mask, uint32_
   return r;
 }
 
-// out |= (byte 1 of e) << 8k as one byte-select OR (byte k of out is zero).
-template <int K>
-__device__ __forceinline__ void or_byte(uint32_t& out, uint32_t e) {
-  if constexpr (K == 0)
-    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_0 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_0"
-        : "+v"(out) : "v"(e));
-  else if constexpr (K == 1)
-    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_1"
-        : "+v"(out) : "v"(e));
-  else if constexpr (K == 2)
-    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_2 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_2"
-        : "+v"(out) : "v"(e));
-  else
-    asm("v_or_b32_sdwa %0, %1, %0 dst_sel:BYTE_3 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1 src1_sel:BYTE_3"
-        : "+v"(out) : "v"(e));
-}
-
-// pos + (byte 0 of e) as one byte-select add.
+// pos + (byte 0 of e) as one byte-select add. Volatile, like the byte
+// selects of quad(), so that the compiler keeps those where they are written.
 __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
   uint32_t r;
-  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+  asm volatile("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
       : "=v"(r) : "v"(e), "v"(pos));
   return r;
 }
@@ -177,9 +161,8 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
 // mbcnt over the whole ballot also counts, for an upper-half lane, every
 // refilling lane of the lower half, so that half's base is lowered by as
 // many words and one bit-field extract picks each lane's base.
-template <int K>
-__device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& offs, uint32_t& out,
-                                              uint32_t half_shift, const uint16_t* s_lut) {
+__device__ __forceinline__ uint32_t decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& offs, uint32_t half_shift,
+                                                  const uint16_t* s_lut) {
   // pos is the next bit's index minus one (see Chain::pos).
   const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 63u - kLimit);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
@@ -197,7 +180,33 @@ __device__ __forceinline__ void decode_symbol(uint64_t& buf, uint32_t& pos, uint
   const uint32_t e = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(s_lut) +
                                                           (static_cast<uint32_t>(buf >> (pr & 63u)) & (2u * XP_LUT_BYTES - 2)));
   pos = add_byte0(pr, e);
-  or_byte<K & 3>(out, e);
+  return e;
+}
+
+// Byte select (v_perm) kept in program order with the symbol steps (all
+// volatile), so that the entries it reads are dead right after it instead
+// of being held for a select the compiler would defer.
+__device__ __forceinline__ uint32_t sel_bytes(uint32_t hi, uint32_t lo, uint32_t sel) {
+  uint32_t r;
+  asm volatile("v_perm_b32 %0, %1, %2, %3" : "=v"(r) : "v"(hi), "v"(lo), "s"(sel));
+  return r;
+}
+
+// Four symbols of one stream into one output word: the exponent field
+// (byte 1 of each entry) of symbol k goes to byte k, joined to the sign and
+// mantissa bits in tmpl. Two byte selects and a three-way OR per four
+// symbols.
+__device__ __forceinline__ uint32_t quad(Chain& ch, uint32_t& offs, uint32_t half_shift, const uint16_t* s_lut,
+                                         uint32_t tmpl) {
+  const uint32_t e0 = decode_symbol(ch.buf, ch.pos, offs, half_shift, s_lut);
+  const uint32_t e1 = decode_symbol(ch.buf, ch.pos, offs, half_shift, s_lut);
+  const uint32_t p01 = sel_bytes(e1, e0, 0x0c0c0501u);  // selector 0x0c gives a zero byte
+  const uint32_t e2 = decode_symbol(ch.buf, ch.pos, offs, half_shift, s_lut);
+  const uint32_t e3 = decode_symbol(ch.buf, ch.pos, offs, half_shift, s_lut);
+  const uint32_t p23 = sel_bytes(e3, e2, 0x05010c0cu);
+  uint32_t r;
+  asm volatile("v_or3_b32 %0, %1, %2, %3" : "=v"(r) : "v"(p01), "v"(p23), "v"(tmpl));
+  return r;
 }
 
 // One stage of the transpose of 16-byte pieces w[4j..4j+3] (j < NP) over
@@ -381,22 +390,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
       // The next unread ring word of each half's group, packed in a scalar register.
       uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
       __builtin_amdgcn_wave_barrier();
-      decode_symbol<0>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
-      decode_symbol<1>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
-      decode_symbol<2>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
-      decode_symbol<3>(ch.buf, ch.pos, offs, o0.x, half_shift, s_lut);
-      decode_symbol<0>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
-      decode_symbol<1>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
-      decode_symbol<2>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
-      decode_symbol<3>(ch.buf, ch.pos, offs, o0.y, half_shift, s_lut);
-      decode_symbol<0>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
-      decode_symbol<1>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
-      decode_symbol<2>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
-      decode_symbol<3>(ch.buf, ch.pos, offs, o1.x, half_shift, s_lut);
-      decode_symbol<0>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
-      decode_symbol<1>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
-      decode_symbol<2>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
-      decode_symbol<3>(ch.buf, ch.pos, offs, o1.y, half_shift, s_lut);
+      o0.x = quad(ch, offs, half_shift, s_lut, o0.x);
+      o0.y = quad(ch, offs, half_shift, s_lut, o0.y);
+      o1.x = quad(ch, offs, half_shift, s_lut, o1.x);
+      o1.y = quad(ch, offs, half_shift, s_lut, o1.y);
       __builtin_amdgcn_wave_barrier();
       half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
       ob[u >> 1] = make_uint4(o0.x, o0.y, o1.x, o1.y);
