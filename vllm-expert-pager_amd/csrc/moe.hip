@@ -153,6 +153,26 @@ __device__ __forceinline__ int2 block_scan2(int a, int b, int2* s_tot, int2* tot
 // per tile. Each wave counts a contiguous range of pairs into its own LDS
 // histogram (no contention between waves), so a slot's list is ordered by
 // wave range; dynamic LDS = 16 * slots ints.
+// Slots of the pairs p0, p0 + 64, ... (kRouteBatch of them; -1 for pairs
+// at or past hi, unknown experts and experts without a slot). All id loads
+// are issued before the first expert_map load, and all of those before any
+// is used, so a batch costs two memory round trips rather than two per pair.
+constexpr int kRouteBatch = 16;
+__device__ __forceinline__ void route_slots(const void* ids, int eb, int64_t p0, int64_t hi,
+                                            const int32_t* __restrict__ expert_map, int E, int slots,
+                                            int (&sl)[kRouteBatch]) {
+  int64_t e[kRouteBatch];
+#pragma unroll
+  for (int j = 0; j < kRouteBatch; ++j) {
+    const int64_t p = p0 + 64 * j;
+    e[j] = p < hi ? load_id(ids, eb, p) : -1;
+  }
+#pragma unroll
+  for (int j = 0; j < kRouteBatch; ++j) sl[j] = (e[j] >= 0 && e[j] < E) ? expert_map[e[j]] : -1;
+#pragma unroll
+  for (int j = 0; j < kRouteBatch; ++j) sl[j] = sl[j] < slots ? sl[j] : -1;
+}
+
 __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npairs,
                                             const int32_t* __restrict__ expert_map, int E, int slots,
                                             int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
@@ -164,10 +184,12 @@ __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npa
   const int64_t per = (npairs + kW - 1) / kW;
   const int64_t lo = wave * per, hi = lo + per < npairs ? lo + per : npairs;
   int* hist = s_hist + wave * slots;
-  for (int64_t p = lo + lane; p < hi; p += 64) {
-    const int64_t e = load_id(ids, eb, p);
-    const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
-    if (s >= 0 && s < slots) atomicAdd(&hist[s], 1);
+  for (int64_t b = lo; b < hi; b += 64 * kRouteBatch) {
+    int sl[kRouteBatch];
+    route_slots(ids, eb, b + lane, hi, expert_map, E, slots, sl);
+#pragma unroll
+    for (int j = 0; j < kRouteBatch; ++j)
+      if (sl[j] >= 0) atomicAdd(&hist[sl[j]], 1);
   }
   __syncthreads();
   int c = 0;
@@ -194,10 +216,12 @@ __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npa
     tiles[0] = total.y;
   }
   __syncthreads();
-  for (int64_t p = lo + lane; p < hi; p += 64) {
-    const int64_t e = load_id(ids, eb, p);
-    const int s = (e >= 0 && e < E) ? expert_map[e] : -1;
-    if (s >= 0 && s < slots) pairs[atomicAdd(&hist[s], 1)] = static_cast<int32_t>(p);
+  for (int64_t b = lo; b < hi; b += 64 * kRouteBatch) {
+    int sl[kRouteBatch];
+    route_slots(ids, eb, b + lane, hi, expert_map, E, slots, sl);
+#pragma unroll
+    for (int j = 0; j < kRouteBatch; ++j)
+      if (sl[j] >= 0) pairs[atomicAdd(&hist[sl[j]], 1)] = static_cast<int32_t>(b + lane + 64 * j);
   }
 }
 
