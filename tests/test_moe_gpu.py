@@ -81,7 +81,9 @@ def test_quant_tokens_bit_exact():
     assert np.array_equal(xs.cpu().numpy(), s)
 
 
-@pytest.mark.parametrize("T, topk, E, slots", [(50, 4, 20, 12), (300, 4, 6, 6), (1, 8, 64, 32)])
+# 5000 x 8 pairs: each of the 16 waves walks 2500 pairs, in batches of 1024
+# (the last one partial).
+@pytest.mark.parametrize("T, topk, E, slots", [(50, 4, 20, 12), (300, 4, 6, 6), (1, 8, 64, 32), (5000, 8, 256, 200)])
 def test_route_lists_mapped_pairs(T, topk, E, slots):
     moe = _moe()
     rng = np.random.default_rng(T)
@@ -98,10 +100,12 @@ def test_route_lists_mapped_pairs(T, topk, E, slots):
     pairs = r.pairs.cpu().numpy()
     tiles = r.tiles.cpu().numpy()
     flat = ids.reshape(-1)
+    valid = (flat >= 0) & (flat < E)
+    slot_of_pair = np.where(valid, emap[np.clip(flat, 0, E - 1)], -1)
     for s in range(slots):
         got = np.sort(pairs[offsets[s] : offsets[s + 1]])
-        want = [p for p in range(T * topk) if 0 <= flat[p] < E and emap[flat[p]] == s]
-        assert got.tolist() == want, f"slot {s}"
+        want = np.nonzero(slot_of_pair == s)[0]
+        assert got.tolist() == want.tolist(), f"slot {s}"
     counts = np.diff(offsets)
     n = int(tiles[0])
     assert n == int(sum((c + 63) // 64 for c in counts))
