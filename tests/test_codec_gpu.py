@@ -91,6 +91,31 @@ def test_round_trip(dist, chunk):
     np.testing.assert_array_equal(decode_one(codec, rec, lut, n, chunk), raw)
 
 
+@pytest.mark.parametrize("chunk", [64, 128, 512])
+@pytest.mark.parametrize("groups", [1, 3, 5, 9])
+def test_odd_group_counts(chunk, groups):
+    """A wave decodes two groups side by side; with an odd group count the
+    last wave's second group is a spare that must store nothing (the rows
+    around the decoded one stay zero)."""
+    codec = _codec()
+    n = groups * chunk * 32
+    raw = rows(20 + groups, n)
+    pitch = codec_ref.pitch_of(n, 1.6, 4096)
+    rec, lut = codec_ref.encode(raw, pitch, chunk)
+    dev = torch.device("cuda")
+    stg = [torch.from_numpy(rec.reshape(1, -1)).to(dev)]
+    dst = [torch.zeros((3, n), dtype=torch.uint8, device=dev)]
+    lut_t = torch.from_numpy(lut.reshape(1, 1, -1)).to(dev)
+    todo = torch.zeros((1,), dtype=torch.int64, device=dev)
+    rowmap = torch.ones((1,), dtype=torch.int64, device=dev)  # expert 0 -> row 1
+    cache_row = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    codec.decode_rows(todo, rowmap, cache_row, stg, dst, lut_t, chunk=chunk)
+    torch.cuda.synchronize()
+    got = dst[0].cpu().numpy()
+    np.testing.assert_array_equal(got[1], raw)
+    assert not got[0].any() and not got[2].any()
+
+
 def test_follows_todo_and_skips():
     """tests/test_codec.py:118-154 of the reference, restated."""
     codec = _codec()

@@ -17,7 +17,7 @@
 // 512-entry LUT is a 16-bit table in LDS (length, pre-shifted exponent); the
 // sign/mantissa nibbles arrive as coalesced 32-bit words (8 values each),
 // prefetched a step ahead. Output bytes are gathered per lane and stored
-// through a lane transpose in runs of 128 bytes (flush). The kernel is held
+// through a lane transpose in runs of 128 bytes (flush16). The kernel is held
 // to 64 VGPRs, so that 8 waves share each SIMD.
 #include "common.h"
 
@@ -210,11 +210,10 @@ __device__ __forceinline__ uint32_t quad(Chain& ch, uint32_t& offs, uint32_t hal
 }
 
 // One stage of the transpose of 16-byte pieces w[4j..4j+3] (j < NP) over
-// sets of lanes four apart: the lanes whose bit T (2, 3 or 4) is clear swap
+// sets of lanes four apart: the lanes whose bit T (2 or 3) is clear swap
 // their pieces j | D with pieces j of the partner lane (this lane + 2^T),
-// D = 2^(T-2). Within a 16-lane row the exchange is a pair of row shifts
-// whose bank masks write only the receiving lanes (a bank is lanes with
-// equal bits 3:2); across rows (T = 4) it is one row swap.
+// D = 2^(T-2). The exchange is a pair of row shifts whose bank masks write
+// only the receiving lanes (a bank is lanes with equal bits 3:2).
 template <int T, int NP>
 __device__ __forceinline__ void butterfly(uint32_t (&w)[4 * NP]) {
   constexpr int D = 1 << (T - 2);
@@ -223,37 +222,31 @@ __device__ __forceinline__ void butterfly(uint32_t (&w)[4 * NP]) {
     const int jj = i >> 2, k = i & 3;
     const int j = ((jj & ~(D - 1)) << 1) | (jj & (D - 1));  // the pieces whose bit D is clear
     const int ia = 4 * j + k, ib = 4 * (j | D) + k;
-    if constexpr (T == 4) {
-      // Odd rows of the first operand trade places with even rows of the second.
-      const auto r = __builtin_amdgcn_permlane16_swap(w[ia], w[ib], false, false);
-      w[ia] = r[0];
-      w[ib] = r[1];
-    } else {
-      constexpr int kShl = 0x100 | (1 << T), kShr = 0x110 | (1 << T);  // lane i <- i + 2^T, i - 2^T
-      constexpr int kClear = T == 2 ? 0x5 : 0x3, kSet = T == 2 ? 0xA : 0xC;
-      const uint32_t nb = static_cast<uint32_t>(
-          __builtin_amdgcn_update_dpp(static_cast<int>(w[ib]), static_cast<int>(w[ia]), kShl, 0xF, kClear, false));
-      const uint32_t na = static_cast<uint32_t>(
-          __builtin_amdgcn_update_dpp(static_cast<int>(w[ia]), static_cast<int>(w[ib]), kShr, 0xF, kSet, false));
-      w[ia] = na;
-      w[ib] = nb;
-    }
+    constexpr int kShl = 0x100 | (1 << T), kShr = 0x110 | (1 << T);  // lane i <- i + 2^T, i - 2^T
+    constexpr int kClear = T == 2 ? 0x5 : 0x3, kSet = T == 2 ? 0xA : 0xC;
+    const uint32_t nb = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(w[ib]), static_cast<int>(w[ia]), kShl, 0xF, kClear, false));
+    const uint32_t na = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(w[ia]), static_cast<int>(w[ib]), kShr, 0xF, kSet, false));
+    w[ia] = na;
+    w[ib] = nb;
   }
 }
 
 // Store of a lane's last F iterations (8F bytes at byte `off` of its
-// chunk, NP = F/2 pieces of 16 bytes). For F of 8 or 16 the lanes of a
-// half-wave form sets of NP lanes four apart (lane bits 2, 3 and, for 16, 4);
-// the transpose leaves set member q with piece q of each member's chunk, so
-// store j of the set writes 8F contiguous bytes of member j's chunk (a whole
-// 128-byte line for F = 16): one store instruction covers 64/NP runs rather
-// than 64 separate 16-byte pieces. Every lane takes part in the exchange;
-// only valid streams store.
+// chunk, NP = F/2 pieces of 16 bytes), for F of 4 or 8 (16: flush16). For
+// F = 8 the lanes of a half-wave form sets of 4 lanes four apart (lane bits
+// 2 and 3); the transpose leaves set member q with piece q of each member's
+// chunk, so store j of the set writes 64 contiguous bytes of member j's
+// chunk: one store instruction covers 16 runs rather than 64 separate
+// 16-byte pieces. Every lane takes part in the exchange; only valid streams
+// store.
 template <int F>
 __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64_t chunk, uint32_t li, int64_t off,
                                       bool valid) {
   constexpr int NP = F / 2;
-  if constexpr (NP == 4 || NP == 8) {
+  static_assert(NP == 2 || NP == 4, "flush16 stores 16 iterations");
+  if constexpr (NP == 4) {
     const uint32_t q = (li >> 2) & (NP - 1);
     uint32_t w[4 * NP];
 #pragma unroll
@@ -265,7 +258,6 @@ __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64
     }
     butterfly<2, NP>(w);
     butterfly<3, NP>(w);
-    if constexpr (NP == 8) butterfly<4, NP>(w);
     if (valid) {
       uint8_t* base = chunk0 + static_cast<int64_t>(li & ~(4u * NP - 4u)) * chunk + off + 16 * q;
 #pragma unroll
@@ -278,6 +270,68 @@ __device__ __forceinline__ void flush(uint4 (&ob)[F / 2], uint8_t* chunk0, int64
 #pragma unroll
       for (int i = 0; i < NP; ++i) dst[i] = ob[i];
     }
+  }
+}
+
+// Store of a lane's last 16 iterations (128 bytes at byte `off` of its
+// chunk, 8 pieces of 16 bytes) for the whole wave at once. The wave's 64
+// lanes hold 64 consecutive chunks (the upper half's group follows the
+// lower half's), starting at chunk0. Sets of eight lanes 8 apart (lane bits
+// 3, 4 and 5) trade pieces in three stages: a pair of row shifts over 8
+// lanes, a swap over 16 lanes and a swap over the wave's halves. Afterwards
+// set member q holds piece q of each member m's run in slot m, so store m
+// writes member m's whole 128-byte line per set. A half whose group is a
+// spare stores nothing.
+__device__ __forceinline__ void flush16(uint4 (&ob)[8], uint8_t* chunk0, int64_t chunk, uint32_t lane, int64_t off,
+                                        bool valid_lo, bool valid_hi) {
+  uint32_t w[32];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    w[4 * j] = ob[j].x;
+    w[4 * j + 1] = ob[j].y;
+    w[4 * j + 2] = ob[j].z;
+    w[4 * j + 3] = ob[j].w;
+  }
+  // Lanes with bit 3 set trade their piece j for piece j + 1 of the lane 8
+  // below: row shifts by 8 whose bank masks (banks are lane bits 3:2) write
+  // only the receiving lanes.
+#pragma unroll
+  for (int j = 0; j < 8; j += 2)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int ia = 4 * j + k, ib = 4 * (j + 1) + k;
+      const uint32_t nb = static_cast<uint32_t>(
+          __builtin_amdgcn_update_dpp(static_cast<int>(w[ib]), static_cast<int>(w[ia]), 0x108, 0xF, 0x3, false));
+      const uint32_t na = static_cast<uint32_t>(
+          __builtin_amdgcn_update_dpp(static_cast<int>(w[ia]), static_cast<int>(w[ib]), 0x118, 0xF, 0xC, false));
+      w[ia] = na;
+      w[ib] = nb;
+    }
+  // Lanes with bit 4 set trade their piece j for piece j + 2 of the lane 16 below.
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int j = (jj & 1) | ((jj & 2) << 1);  // 0, 1, 4, 5
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const auto r = __builtin_amdgcn_permlane16_swap(w[4 * j + k], w[4 * (j + 2) + k], false, false);
+      w[4 * j + k] = r[0];
+      w[4 * (j + 2) + k] = r[1];
+    }
+  }
+  // Lanes of the upper half trade their piece j for piece j + 4 of the lane 32 below.
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const auto r = __builtin_amdgcn_permlane32_swap(w[4 * j + k], w[4 * (j + 4) + k], false, false);
+      w[4 * j + k] = r[0];
+      w[4 * (j + 4) + k] = r[1];
+    }
+  uint8_t* base = chunk0 + static_cast<int64_t>(lane & 7) * chunk + off + 16 * (lane >> 3);
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    if (!(m < 4 ? valid_lo : valid_hi)) continue;
+    *reinterpret_cast<uint4*>(base + 8 * m * chunk) = make_uint4(w[4 * m], w[4 * m + 1], w[4 * m + 2], w[4 * m + 3]);
   }
 }
 
@@ -352,6 +406,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   ch.b_n = 0;
   ch.b_base = ch.b_val0 = ch.b_val1 = 0;
   uint8_t* out = nm.dst + drow * nm.N + int64_t(g) * 32 * a.chunk;  // chunk 0 of the group
+  // The wave's two groups as one run of 64 chunks (the 16-iteration flush).
+  const int g_lo = r * kGroupsPerBlock + 2 * __builtin_amdgcn_readfirstlane(wave);
+  uint8_t* out_wave = nm.dst + drow * nm.N + int64_t(g_lo) * 32 * a.chunk;
+  const bool valid_lo = g_lo < G, valid_hi = g_lo + 1 < G;
   // Initial fill of the ring: the group's first kRing words (8 loads per lane).
   {
     const uint32_t fill = ch.count < kRing ? ch.count : kRing;
@@ -398,7 +456,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
       half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
       ob[u >> 1] = make_uint4(o0.x, o0.y, o1.x, o1.y);
     }
-    flush<F>(ob, out, a.chunk, li, 8 * m0, valid);
+    if constexpr (F == 16)
+      flush16(ob, out_wave, a.chunk, static_cast<uint32_t>(lane), 8 * m0, valid_lo, valid_hi);
+    else
+      flush<F>(ob, out, a.chunk, li, 8 * m0, valid);
   }
 }
 
