@@ -55,8 +55,19 @@ def _dist(dist, n, seed):
 @pytest.mark.parametrize("dist", ["realistic", "uniform", "geometric", "constant", "long_codes", "one_symbol_rare"])
 @pytest.mark.parametrize("chunk", [64, 512])
 def test_matches_host_encoder(dist, chunk):
+    _matches_host_encoder(dist, chunk, 6)
+
+
+# The groups of a row are encoded 8 per workgroup: 9 and 17 groups leave a
+# last workgroup with one group (a spare upper half-wave), 11 one with three.
+@pytest.mark.parametrize("groups", [1, 9, 11, 17])
+def test_matches_host_encoder_group_counts(groups):
+    _matches_host_encoder("realistic", 64, groups)
+
+
+def _matches_host_encoder(dist, chunk, groups):
     codec = _codec()
-    n = 6 * chunk * 32
+    n = groups * chunk * 32
     raws = np.stack([_dist(dist, n, 10 * k) for k in range(3)])
     pitch = codec_ref.pitch_of(n, 1.6, 4096)
     rec, lut, needed = codec.encode_rows(torch.from_numpy(raws).cuda(), pitch, chunk)

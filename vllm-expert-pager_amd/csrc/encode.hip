@@ -1,23 +1,27 @@
 // Batched GPU encoder of the fp8 exponent Huffman row format
-// (encode, codec.py:125-198), one workgroup per row, producing the bytes of
-// the host encoder (codec_host.cpp) and of the reference.
+// (encode, codec.py:125-198), producing the bytes of the host encoder
+// (codec_host.cpp) and of the reference. Two launches:
 //
-// Per row:
+// encode_plan_kernel, one workgroup per row:
 //   1. exponent histogram: per-thread counters in LDS, then summed;
 //   2. the code (code_build.h) by one thread, the 512-entry LUT by all;
 //   3. Huffman words per chunk: the decoder loads a word before symbol i
 //      whenever fewer than LIMIT bits are left, so a chunk whose last symbol
 //      starts at bit b needs (b + LIMIT - 1) / 32 + 1 words; summed per
-//      group and scanned into gstart;
-//   4. each 32-lane half-wave encodes one group: its lanes walk their chunks
+//      group and scanned into gstart, written to the record's header.
+// encode_groups_kernel, one workgroup per 8 groups of a row:
+//   4. the code again, from the row's LUT (every symbol has a code of at
+//      most LIMIT bits, so each one appears in the 9-bit table with its
+//      length, and the canonical codes follow from the lengths); then each
+//      32-lane half-wave encodes one group: its lanes walk their chunks
 //      in lockstep, run the decoder's refill rule, and give each word the
 //      (symbol index, lane) rank of its refill -- the wave ballot's count of
 //      refilling lanes below, as the decoder computes it. A lane emits a
 //      word once its 32 bits are complete; at most two refills are waiting
 //      for their word. The lane also writes its sign/mantissa nibble words.
-// The record is written whole: gstart, nibbles, Huffman words and a zero
-// tail up to the pitch. A row that does not fit its pitch writes nothing
-// but its LUT and needed bytes.
+// The record is written whole: gstart and the zero tail up to the pitch by
+// the first launch, nibbles and Huffman words by the second. A row that does
+// not fit its pitch writes nothing but its LUT and needed bytes.
 #include "code_build.h"
 #include "common.h"
 
@@ -26,6 +30,12 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxGroups = 4096;  // groups per row a workgroup scans in LDS
+constexpr int kGroupsPerBlock = 2 * kThreads / 64;  // 8: one per half-wave
+// The plan's two passes over a row run in one workgroup per row: 16 waves,
+// each lane with four 16-byte loads in flight, so that a pass is not a
+// chain of load latencies.
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanUnroll = 4;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -51,10 +61,11 @@ __device__ __forceinline__ uint32_t sum_lengths4(uint32_t w, uint64_t lens) {
   return t;
 }
 
-__global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
+__global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a) {
+  constexpr int kThreads = kPlanThreads;  // this kernel's workgroup
   __shared__ uint32_t s_hist[code::kSyms][kThreads];  // per-thread counters
   __shared__ int32_t s_len[code::kSyms];
-  __shared__ uint32_t s_tab[code::kSyms];              // code | length << 16
+  __shared__ int32_t s_code[code::kSyms];
   __shared__ int32_t s_words[kMaxGroups + 1];          // words per group, then gstart
   __shared__ int64_t s_total;
 
@@ -67,21 +78,32 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
 
   // 1. Histogram of the exponent fields.
   for (int s = 0; s < code::kSyms; ++s) s_hist[s][tid] = 0;
-  for (int64_t off = int64_t(tid) * 16; off < n; off += int64_t(kThreads) * 16) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(raw + off);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  constexpr int64_t kStep = int64_t(kThreads) * 16;
+  for (int64_t off0 = int64_t(tid) * 16; off0 < n; off0 += kStep * kPlanUnroll) {
+    u32x4 v[kPlanUnroll];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int u = 0; u < kPlanUnroll; ++u)
+      if (off0 + u * kStep < n) v[u] = *reinterpret_cast<const u32x4*>(raw + off0 + u * kStep);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) ++s_hist[(w[k] >> (8 * b + 3)) & 15u][tid];
+    for (int u = 0; u < kPlanUnroll; ++u) {
+      if (off0 + u * kStep >= n) continue;
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) ++s_hist[(w[k] >> (8 * b + 3)) & 15u][tid];
+    }
   }
   __syncthreads();
 
-  // 2. The code, and the LUT.
-  if (tid < code::kSyms) {
+  // 2. The code, and the LUT. Wave w sums symbol w's counters.
+  static_assert(kThreads / 64 == code::kSyms, "one wave per symbol");
+  {
+    const int sym = tid >> 6, part = tid & 63;
     uint32_t t = 0;
-    for (int i = 0; i < kThreads; ++i) t += s_hist[tid][i];
-    s_hist[tid][0] = t;
+    for (int i = 0; i < kThreads / 64; ++i) t += s_hist[sym][part * (kThreads / 64) + i];
+    for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
+    if (part == 0) s_hist[sym][0] = t;
   }
   __syncthreads();
   if (tid == 0) {
@@ -92,7 +114,7 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
     code::canonical_codes(lengths, codes);
     for (int s = 0; s < code::kSyms; ++s) {
       s_len[s] = lengths[s];
-      s_tab[s] = static_cast<uint32_t>(codes[s]) | (static_cast<uint32_t>(lengths[s]) << 16);
+      s_code[s] = codes[s];
     }
   }
   __syncthreads();
@@ -100,7 +122,7 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
     int32_t lengths[code::kSyms], codes[code::kSyms];
     for (int s = 0; s < code::kSyms; ++s) {
       lengths[s] = s_len[s];
-      codes[s] = static_cast<int32_t>(s_tab[s] & 0xffffu);
+      codes[s] = s_code[s];
     }
     uint8_t* lut = a.lut + static_cast<int64_t>(row) * a.lut_stride;
     for (int x = tid; x < XP_LUT_BYTES; x += kThreads) lut[x] = static_cast<uint8_t>(code::lut_entry(lengths, codes, x));
@@ -114,14 +136,25 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
   const int per = chunk / 16;  // threads per chunk
   for (int g = tid; g < G; g += kThreads) s_words[g] = 0;
   __syncthreads();
-  for (int64_t off = int64_t(tid) * 16; off < n; off += int64_t(kThreads) * 16) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(raw + off);
-    uint32_t bits = sum_lengths4(v.x, lens) + sum_lengths4(v.y, lens) + sum_lengths4(v.z, lens) +
-                    sum_lengths4(v.w, lens);
-    const bool last = ((off + 16) % chunk) == 0;
-    if (last) bits -= static_cast<uint32_t>(lens >> (4 * ((v.w >> 27) & 15u))) & 15u;  // not the last symbol
-    for (int d = 1; d < per; d <<= 1) bits += __shfl_xor(bits, d, per);
-    if (last) atomicAdd(&s_words[off / (int64_t(chunk) * XP_LANES)], static_cast<int32_t>((bits + XP_LIMIT - 1) / 32 + 1));
+  // A chunk's pieces are all below n or all at or past it (n is a multiple
+  // of the chunk), so each set of lanes shuffles together.
+  for (int64_t off0 = int64_t(tid) * 16; off0 < n; off0 += kStep * kPlanUnroll) {
+    u32x4 v[kPlanUnroll];
+#pragma unroll
+    for (int u = 0; u < kPlanUnroll; ++u)
+      if (off0 + u * kStep < n) v[u] = *reinterpret_cast<const u32x4*>(raw + off0 + u * kStep);
+#pragma unroll
+    for (int u = 0; u < kPlanUnroll; ++u) {
+      const int64_t off = off0 + u * kStep;
+      if (off >= n) continue;
+      uint32_t bits = sum_lengths4(v[u].x, lens) + sum_lengths4(v[u].y, lens) + sum_lengths4(v[u].z, lens) +
+                      sum_lengths4(v[u].w, lens);
+      const bool last = ((off + 16) % chunk) == 0;
+      if (last) bits -= static_cast<uint32_t>(lens >> (4 * ((v[u].w >> 27) & 15u))) & 15u;  // not the last symbol
+      for (int d = 1; d < per; d <<= 1) bits += __shfl_xor(bits, d, per);
+      if (last)
+        atomicAdd(&s_words[off / (int64_t(chunk) * XP_LANES)], static_cast<int32_t>((bits + XP_LIMIT - 1) / 32 + 1));
+    }
   }
   __syncthreads();
   if (tid == 0) {  // exclusive scan into gstart
@@ -144,8 +177,39 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
   for (int g = tid; g <= G; g += kThreads) gstart[g] = s_words[g];
   // Zero tail (nbytes and the pitch are multiples of 4).
   for (int64_t i = nbytes / 4 + tid; i < a.pitch / 4; i += kThreads) reinterpret_cast<uint32_t*>(rec)[i] = 0;
+}
 
-  // 4. Groups, one per half-wave.
+__global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, int blocks_per_row) {
+  __shared__ int32_t s_len[code::kSyms];
+  __shared__ uint32_t s_tab[code::kSyms];  // code | length << 16
+
+  const int row = blockIdx.x / blocks_per_row, part = blockIdx.x % blocks_per_row;
+  const int tid = threadIdx.x;
+  if (a.needed[row] > a.pitch) return;  // the row does not fit: the plan wrote nothing either
+  const uint8_t* raw = a.raw + static_cast<int64_t>(row) * a.raw_stride;
+  uint8_t* rec = a.rec + static_cast<int64_t>(row) * a.pitch;
+  const int64_t n = a.n;
+  const int chunk = a.chunk, G = a.G;
+  const int32_t* gstart = reinterpret_cast<const int32_t*>(rec);
+
+  // 4. The code from the LUT (entry = symbol << 4 | length), then groups,
+  // one per half-wave.
+  const uint8_t* lut = a.lut + static_cast<int64_t>(row) * a.lut_stride;
+  for (int x = tid; x < XP_LUT_BYTES; x += kThreads) {
+    const uint32_t ent = lut[x];
+    s_len[ent >> 4] = static_cast<int32_t>(ent & 15u);  // every entry of a symbol holds the same length
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t lengths[code::kSyms], codes[code::kSyms];
+    for (int s = 0; s < code::kSyms; ++s) lengths[s] = s_len[s];
+    code::canonical_codes(lengths, codes);
+    for (int s = 0; s < code::kSyms; ++s)
+      s_tab[s] = static_cast<uint32_t>(codes[s]) | (static_cast<uint32_t>(lengths[s]) << 16);
+  }
+  __syncthreads();
+
+  const int64_t head = 4 * (int64_t(G) + 1) + n / 2;
   uint32_t* fixed = reinterpret_cast<uint32_t*>(rec + 4 * (int64_t(G) + 1));
   uint32_t* huff = reinterpret_cast<uint32_t*>(rec + head);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -153,23 +217,27 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
   const uint32_t li = lane & 31;
   const uint32_t low = upper ? 0u : ~0u;
   const int mwords = chunk / 8;
-  const uint32_t total = static_cast<uint32_t>(s_total);  // every word position is below it
-  for (int g0 = 2 * wave; g0 < G; g0 += 2 * (kThreads / 64)) {
+  const uint32_t total = static_cast<uint32_t>(gstart[G]);  // every word position is below it
+  {
+    const int g0 = part * kGroupsPerBlock + 2 * wave;
+    if (g0 >= G) return;
     const int g = g0 + (upper ? 1 : 0);
     const bool live = g < G;  // a spare half-wave walks the last group and writes nothing
     const int gg = live ? g : G - 1;
     const uint8_t* src = raw + (int64_t(gg) * XP_LANES + li) * chunk;
     uint32_t* fx = fixed + int64_t(gg) * mwords * XP_LANES + li;
     // Word positions of the two half-waves' groups, uniform per half.
-    uint32_t base_lo = static_cast<uint32_t>(s_words[g0]);
-    uint32_t base_hi = static_cast<uint32_t>(s_words[g0 + 1 < G ? g0 + 1 : G - 1]);
+    uint32_t base_lo = static_cast<uint32_t>(gstart[g0]);
+    uint32_t base_hi = static_cast<uint32_t>(gstart[g0 + 1 < G ? g0 + 1 : G - 1]);
     uint32_t level = 0;         // bits the decoder has buffered
     uint64_t acc = 0;           // bits of the lane's stream not yet emitted
     uint32_t accbits = 0;
     uint32_t q0 = 0, q1 = 0;    // positions of words refilled but not yet emitted
     uint32_t qn = 0;
+    u32x4 v_next = *reinterpret_cast<const u32x4*>(src);  // the next 16 values, loaded a step ahead
     for (int i0 = 0; i0 < chunk; i0 += 16) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(src + i0);
+      const u32x4 v = v_next;
+      if (i0 + 16 < chunk) v_next = *reinterpret_cast<const u32x4*>(src + i0 + 16);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -257,8 +325,14 @@ int xp_encode_rows(const uint8_t* raw, int64_t rows, int64_t raw_stride, int64_t
   XP_REQUIRE(lut_stride >= XP_LUT_BYTES, "xp_encode_rows: lut_stride=%lld", (long long)lut_stride);
   EncodeArgs a{raw, raw_stride, n, static_cast<int>(chunk), static_cast<int>(G), records, pitch,
                luts, lut_stride, needed};
-  hipLaunchKernelGGL(encode_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, as_stream(stream), a);
-  return check_launch("encode_kernel");
+  hipLaunchKernelGGL(encode_plan_kernel, dim3(static_cast<unsigned>(rows)), dim3(kPlanThreads), 0, as_stream(stream),
+                     a);
+  if (int rc = check_launch("encode_plan_kernel")) return rc;
+  const int64_t blocks = (G + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  XP_REQUIRE(rows * blocks <= INT32_MAX, "xp_encode_rows: %lld rows x %lld blocks", (long long)rows, (long long)blocks);
+  hipLaunchKernelGGL(encode_groups_kernel, dim3(static_cast<unsigned>(rows * blocks)), dim3(kThreads), 0,
+                     as_stream(stream), a, static_cast<int>(blocks));
+  return check_launch("encode_groups_kernel");
 }
 
 }  // extern "C"
