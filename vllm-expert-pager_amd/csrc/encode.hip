@@ -325,11 +325,11 @@ int xp_encode_rows(const uint8_t* raw, int64_t rows, int64_t raw_stride, int64_t
   XP_REQUIRE(lut_stride >= XP_LUT_BYTES, "xp_encode_rows: lut_stride=%lld", (long long)lut_stride);
   EncodeArgs a{raw, raw_stride, n, static_cast<int>(chunk), static_cast<int>(G), records, pitch,
                luts, lut_stride, needed};
+  const int64_t blocks = (G + kGroupsPerBlock - 1) / kGroupsPerBlock;
+  XP_REQUIRE(rows * blocks <= INT32_MAX, "xp_encode_rows: %lld rows x %lld blocks", (long long)rows, (long long)blocks);
   hipLaunchKernelGGL(encode_plan_kernel, dim3(static_cast<unsigned>(rows)), dim3(kPlanThreads), 0, as_stream(stream),
                      a);
   if (int rc = check_launch("encode_plan_kernel")) return rc;
-  const int64_t blocks = (G + kGroupsPerBlock - 1) / kGroupsPerBlock;
-  XP_REQUIRE(rows * blocks <= INT32_MAX, "xp_encode_rows: %lld rows x %lld blocks", (long long)rows, (long long)blocks);
   hipLaunchKernelGGL(encode_groups_kernel, dim3(static_cast<unsigned>(rows * blocks)), dim3(kThreads), 0,
                      as_stream(stream), a, static_cast<int>(blocks));
   return check_launch("encode_groups_kernel");
