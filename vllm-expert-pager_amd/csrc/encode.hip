@@ -62,8 +62,7 @@ __device__ __forceinline__ uint32_t sum_lengths4(uint32_t w, uint64_t lens) {
 }
 
 __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a) {
-  constexpr int kThreads = kPlanThreads;  // this kernel's workgroup
-  __shared__ uint32_t s_hist[code::kSyms][kThreads];  // per-thread counters
+  __shared__ uint32_t s_hist[code::kSyms][kPlanThreads];  // per-thread counters
   __shared__ int32_t s_len[code::kSyms];
   __shared__ int32_t s_code[code::kSyms];
   __shared__ int32_t s_words[kMaxGroups + 1];          // words per group, then gstart
@@ -78,7 +77,7 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
 
   // 1. Histogram of the exponent fields.
   for (int s = 0; s < code::kSyms; ++s) s_hist[s][tid] = 0;
-  constexpr int64_t kStep = int64_t(kThreads) * 16;
+  constexpr int64_t kStep = int64_t(kPlanThreads) * 16;
   for (int64_t off0 = int64_t(tid) * 16; off0 < n; off0 += kStep * kPlanUnroll) {
     u32x4 v[kPlanUnroll];
 #pragma unroll
@@ -97,11 +96,11 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
   __syncthreads();
 
   // 2. The code, and the LUT. Wave w sums symbol w's counters.
-  static_assert(kThreads / 64 == code::kSyms, "one wave per symbol");
+  static_assert(kPlanThreads / 64 == code::kSyms, "one wave per symbol");
   {
     const int sym = tid >> 6, part = tid & 63;
     uint32_t t = 0;
-    for (int i = 0; i < kThreads / 64; ++i) t += s_hist[sym][part * (kThreads / 64) + i];
+    for (int i = 0; i < kPlanThreads / 64; ++i) t += s_hist[sym][part * (kPlanThreads / 64) + i];
     for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, 64);
     if (part == 0) s_hist[sym][0] = t;
   }
@@ -125,7 +124,8 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
       codes[s] = s_code[s];
     }
     uint8_t* lut = a.lut + static_cast<int64_t>(row) * a.lut_stride;
-    for (int x = tid; x < XP_LUT_BYTES; x += kThreads) lut[x] = static_cast<uint8_t>(code::lut_entry(lengths, codes, x));
+    for (int x = tid; x < XP_LUT_BYTES; x += kPlanThreads)
+      lut[x] = static_cast<uint8_t>(code::lut_entry(lengths, codes, x));
   }
   uint64_t lens = 0;
   for (int s = 0; s < code::kSyms; ++s) lens |= static_cast<uint64_t>(s_len[s]) << (4 * s);
@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
   // The chunk's 16-byte pieces are spread over consecutive threads, so each
   // chunk is summed by a power-of-two set of lanes of one wave.
   const int per = chunk / 16;  // threads per chunk
-  for (int g = tid; g < G; g += kThreads) s_words[g] = 0;
+  for (int g = tid; g < G; g += kPlanThreads) s_words[g] = 0;
   __syncthreads();
   // A chunk's pieces are all below n or all at or past it (n is a multiple
   // of the chunk), so each set of lanes shuffles together.
@@ -174,9 +174,9 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
   if (nbytes > a.pitch) return;
 
   int32_t* gstart = reinterpret_cast<int32_t*>(rec);
-  for (int g = tid; g <= G; g += kThreads) gstart[g] = s_words[g];
+  for (int g = tid; g <= G; g += kPlanThreads) gstart[g] = s_words[g];
   // Zero tail (nbytes and the pitch are multiples of 4).
-  for (int64_t i = nbytes / 4 + tid; i < a.pitch / 4; i += kThreads) reinterpret_cast<uint32_t*>(rec)[i] = 0;
+  for (int64_t i = nbytes / 4 + tid; i < a.pitch / 4; i += kPlanThreads) reinterpret_cast<uint32_t*>(rec)[i] = 0;
 }
 
 __global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, int blocks_per_row) {
