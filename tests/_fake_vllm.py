@@ -3,8 +3,10 @@
 Installs modules ``vllm.config``, ``vllm.logger``,
 ``vllm.model_executor.layers.fused_moe.oracle.fp8`` and
 ``vllm.model_executor.layers.fused_moe.routed_experts`` into ``sys.modules``
-with a ``RoutedExperts`` base that creates block-fp8 expert parameters the
-way a w8a8 block-quantised MoE layer does: ``w13_weight (E, 2I, H)``,
+with a ``RoutedExperts`` base that carries the layer's ``activation``,
+``apply_router_weight_on_input`` and shared experts (as vLLM's MoE layers
+do) and creates block-fp8 expert parameters the way a w8a8 block-quantised
+MoE layer does: ``w13_weight (E, 2I, H)``,
 ``w2_weight (E, H, I)`` float8_e4m3fn, ``w13_weight_scale_inv`` and
 ``w2_weight_scale_inv`` float32 per 128x128 block. It holds no vLLM code.
 """
@@ -42,7 +44,8 @@ class RoutedExperts(torch.nn.Module):
     registered: list = []
 
     def __init__(self, num_experts, hidden_size, intermediate_size, *, use_ep=False, tp_size=1, device="cuda",
-                 backend=Fp8MoeBackend.TRITON, layer_name="model.layers.0.mlp.experts"):
+                 backend=Fp8MoeBackend.TRITON, layer_name="model.layers.0.mlp.experts", activation="silu",
+                 apply_router_weight_on_input=False, shared_experts=None, config_activation=None):
         super().__init__()
         E, H, I = num_experts, hidden_size, intermediate_size
         self.layer_name = layer_name
@@ -50,7 +53,12 @@ class RoutedExperts(torch.nn.Module):
         self.local_num_experts = E // 2 if use_ep else E
         self.use_ep = use_ep
         self.hidden_size, self.intermediate_size_per_partition = H, I
+        self.activation = activation
+        self.apply_router_weight_on_input = apply_router_weight_on_input
+        self._shared_experts = shared_experts
         self.moe_config = SimpleNamespace(moe_parallel_config=SimpleNamespace(tp_size=tp_size))
+        if config_activation is not None:  # newer layouts keep the activation on the config
+            self.moe_config.activation = config_activation
         self.quant_method = _QuantMethod(backend)
         fp8 = torch.float8_e4m3fn
         p = lambda shape, dt: torch.nn.Parameter(torch.zeros(shape, dtype=dt, device=device), requires_grad=False)

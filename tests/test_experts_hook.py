@@ -55,6 +55,47 @@ def test_refuses_expert_and_tensor_parallelism(hook):
         hook.ExpertPagerRoutedExperts(E, H, I, tp_size=2, device="cpu")
 
 
+class _Act(__import__("enum").Enum):
+    SILU = "silu"
+    GELU = "gelu"
+
+
+@pytest.mark.parametrize(
+    "kw, match",
+    [
+        (dict(activation="gelu"), "activation 'gelu'"),
+        (dict(activation=_Act.GELU), "activation 'gelu'"),
+        (dict(config_activation="swigluoai"), "activation 'swigluoai'"),
+        (dict(apply_router_weight_on_input=True), "apply_router_weight_on_input"),
+        (dict(shared_experts=object()), "shared experts"),
+    ],
+)
+def test_refuses_modes_the_kernels_do_not_compute(hook, kw, match):
+    """The expert FFN is this package's own (silu(gate) * up, routed weight on
+    the output, routed sum only); anything else vLLM's fused MoE would have
+    done for the reference (experts.py:594-600) is refused at construction."""
+    with pytest.raises(RuntimeError, match=match):
+        hook.ExpertPagerRoutedExperts(E, H, I, device="cpu", **kw)
+    assert hook._pager is None  # refused before any tier is allocated
+
+
+def test_accepts_silu_in_any_spelling(hook):
+    for act in ("silu", "SiLU", _Act.SILU):
+        assert hook._unsupported_modes(_fake_vllm.RoutedExperts(E, H, I, device="cpu", activation=act)) == []
+
+
+def test_shared_experts_passed_at_forward_are_refused(hook):
+    """A layer that hands shared experts to forward_modular is refused rather
+    than given the routed output alone (the shared output's contract is
+    vLLM's). Checked before any GPU work, so it runs without a GPU."""
+    layer = _fake_vllm.RoutedExperts(E, H, I, device="cpu")
+    layer.layer_name = "model.layers.3.mlp.experts"
+    x = torch.zeros((1, H), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="layers.3.*shared experts"):
+        hook.ExpertPagerRoutedExperts.forward_modular(layer, x, torch.ones((1, 4)), torch.zeros((1, 4)),
+                                                      shared_experts=lambda t: t)
+
+
 def test_settings_are_validated(hook):
     hook.SETTINGS.ram_slots = 2
     with pytest.raises(ValueError, match="RAM_SLOTS=2 must be >= VLLM_EXPERT_PAGER_CACHE_SLOTS=4"):

@@ -10,8 +10,11 @@ built right after it; ``forward_modular`` runs the decode or the prefill
 overflow path of the layer's ``PagedExperts`` (pager.py). The expert FFN is
 this package's own fp8 MFMA kernels (csrc/moe.hip) rather than vLLM's fused
 MoE, so no ``moe_sum`` intercept is needed: the top-k sum runs once by
-construction. Settings are the ``VLLM_EXPERT_PAGER_*`` environment
-variables, read at import.
+construction. Because those kernels compute only ``silu(gate) * up`` with the
+routed weight applied to each expert's output, layers that ask for another
+activation, for ``apply_router_weight_on_input`` or for shared experts are
+refused with ``RuntimeError``. Settings are the ``VLLM_EXPERT_PAGER_*``
+environment variables, read at import.
 
 Importing this module requires vLLM; ``plugin.register`` imports it only
 after vLLM has loaded.
@@ -35,6 +38,45 @@ SETTINGS = Settings.from_env()
 _pager: Pager | None = None
 
 
+def _mode_name(value) -> str:
+    """Lower-case name of a mode given as a string or an enum member."""
+    if isinstance(value, str):
+        return value.lower()
+    inner = getattr(value, "value", None)
+    if isinstance(inner, str):
+        return inner.lower()
+    return str(getattr(value, "name", value)).lower()
+
+
+def _unsupported_modes(layer) -> list[str]:
+    """What the layer asks of the expert FFN that csrc/moe.hip does not compute.
+
+    The kernels compute ``silu(gate) * up`` over w13's gate rows then up rows,
+    multiply each pair's output by its routed weight after ``w2`` and return
+    the routed sum alone. The reference leaves all of this to vLLM's fused MoE
+    (experts.py:594-600), which reads the layer's ``activation`` and
+    ``apply_router_weight_on_input`` (on the layer or its ``moe_config``) and
+    runs any shared experts. Each mode the kernels would get silently wrong is
+    listed here so construction can refuse it.
+    """
+    found = []
+    for owner in (layer, getattr(layer, "moe_config", None)):
+        if owner is None:
+            continue
+        act = getattr(owner, "activation", None)
+        if act is not None and _mode_name(act) != "silu":
+            found.append(f"activation {_mode_name(act)!r} (the kernels compute silu(gate) * up)")
+        if getattr(owner, "is_act_and_mul", True) is False:
+            found.append("an activation without the gate/up product")
+        if getattr(owner, "apply_router_weight_on_input", False):
+            found.append("apply_router_weight_on_input (the kernels weight each expert's output)")
+    for name in ("shared_experts", "_shared_experts"):
+        if getattr(layer, name, None) is not None:
+            found.append("shared experts (their output contract belongs to vLLM's modular kernel)")
+            break
+    return list(dict.fromkeys(found))
+
+
 class ExpertPagerRoutedExperts(RoutedExperts):
     """``RoutedExperts`` that references expert weights through a slab.
 
@@ -54,6 +96,12 @@ class ExpertPagerRoutedExperts(RoutedExperts):
             )
         if self.moe_config.moe_parallel_config.tp_size != 1:
             raise RuntimeError(f"{self.layer_name}: vllm-expert-pager does not support tensor parallelism")
+        unsupported = _unsupported_modes(self)
+        if unsupported:
+            raise RuntimeError(
+                f"{self.layer_name}: vllm-expert-pager runs its own fp8 expert kernels, which do not "
+                f"support {'; '.join(unsupported)}"
+            )
         E = self.global_num_experts
         params = {name: getattr(self, name) for name in PARAMS}
 
@@ -162,10 +210,15 @@ class ExpertPagerRoutedExperts(RoutedExperts):
         shared_experts=None,
         shared_experts_input: torch.Tensor | None = None,
     ) -> torch.Tensor:
-        # The shared experts run once per call (the reference hands them to
-        # the first chunk only); their output stays inside SharedExperts.
+        # The reference hands shared experts to vLLM's modular kernel, which
+        # keeps their output inside SharedExperts (experts.py:475-477, 594-600).
+        # That contract is vLLM's and is not reproduced here, so a layer that
+        # passes them is refused rather than given a routed-only result.
         if shared_experts is not None:
-            shared_experts(shared_experts_input if shared_experts_input is not None else x)
+            raise RuntimeError(
+                f"{self.layer_name}: vllm-expert-pager runs its own fp8 expert kernels, which do not "
+                "support shared experts (their output contract belongs to vLLM's modular kernel)"
+            )
         pager = self._expert_pager
         self._expert_pager_expert_map = pager.expert_map
         try:
