@@ -154,9 +154,11 @@ typedef struct xp_ring {
  * cache_row[e] to dst row dst_row[e]; otherwise from RAM-tier row
  * src_row[e] + base: to staging row j (its index in todo) when the name has
  * stg, else to dst row dst_row[e]. The scale row of e is copied to
- * scale_dst row dst_row[e]. With ring != NULL, the same launch publishes the
- * experts of ssd_todo[K] to the host ring for layer `layer`, waits for their
- * done, and skips them in the copy.
+ * scale_dst row dst_row[e]. An expert whose dst_row[e] is outside
+ * [0, dst_rows) is skipped (nothing of it is copied). With ring != NULL, the
+ * same launch publishes the experts of ssd_todo[K] (K <= ring->block) to the
+ * host ring for layer `layer`, waits for their done, and skips them in the
+ * copy.
  * Replaces gather_rows (gather.py:328-393) and _gather_rows_kernel
  * (gather.py:51-194). */
 int xp_gather_rows(const int64_t* todo, int64_t K, int64_t num_experts,
@@ -171,7 +173,9 @@ int xp_gather_rows(const int64_t* todo, int64_t K, int64_t num_experts,
 int xp_gather_set_blocks(int blocks);
 
 /* Publish the experts of todo[K] to the ring and wait for done. Expert e
- * lands in RAM-tier row row[e] + base. No-op if todo is empty.
+ * lands in RAM-tier row row[e] + base. No-op if todo is empty. A request slot
+ * holds ring->block entries: the fetch entry points read only
+ * todo[0 .. min(K, block)), as the reference's kernels do.
  * Replaces fetch_rows (gather.py:396-407). */
 int xp_fetch_rows(const int64_t* todo, int64_t K, int64_t num_experts,
                   const int64_t* row,
@@ -215,8 +219,9 @@ typedef struct xp_decode_name {
 } xp_decode_name;
 
 /* Expand staging row j (the j-th entry of todo) into dst row dst_row[e] for
- * every name. Skips -1 entries, experts with cache_row[e] >= 0 and (when
- * skip != NULL) experts listed in skip[K]. lut is the layer's
+ * every name. Skips -1 entries, experts with cache_row[e] >= 0, experts
+ * whose dst_row[e] is outside [0, dst_rows) and (when skip != NULL) experts
+ * listed in skip[K]. lut is the layer's
  * uint8[E][num_names][512]. chunk = values per lane (512 in production;
  * any multiple of 32 up to 4096). A record's reads stay inside its pitch
  * whatever its contents, so a corrupt record yields wrong bytes in its own

@@ -25,7 +25,12 @@ def gather_rows_ref(todo, dst_row, cache_row, src_row, base, src, cache, dst, st
     for j, e in enumerate(np.asarray(todo).tolist()):
         if e < 0 or e in skip_set:
             continue
-        drow = max(int(dst_row[e]), 0)
+        # The reference clamps a negative row to 0 (gather.py:130); the
+        # listings acquire and plan_chunks hand over never carry one, and this
+        # build skips such an expert (and a row past the destination) instead.
+        drow = int(dst_row[e])
+        if drow < 0 or drow >= dst[0].shape[0]:
+            continue
         for n in range(len(dst)):
             if cache_row[e] >= 0:
                 dst[n][drow] = cache[n][cache_row[e]]
@@ -42,7 +47,9 @@ def decode_rows_ref(todo, dst_row, cache_row, staging, dst, lut, skip=None, chun
     for j, e in enumerate(np.asarray(todo).tolist()):
         if e < 0 or e in skip_set or cache_row[e] >= 0:
             continue
-        drow = max(int(dst_row[e]), 0)
+        drow = int(dst_row[e])  # clamped to 0 by the reference (codec.py:272); skipped here
+        if drow < 0 or drow >= dst[0].shape[0]:
+            continue
         for n in range(len(dst)):
             N = dst[n].shape[1]
             dst[n][drow] = codec_ref.decode_fast(staging[n][j], lut[e, n], N, chunk)[0]

@@ -122,3 +122,48 @@ def test_out_of_range_rows_are_skipped():
     gather.gather_rows(todo, dst_row, cache_row, src_row, 0, src, cache, dst, None, scale, sdst)
     torch.cuda.synchronize()
     assert not dst[0].any()
+
+
+@pytest.mark.parametrize("compress", [True, False])
+def test_negative_destination_rows_are_skipped(compress):
+    """An expert whose dst_row is negative is skipped whole: no slab row, no
+    staging row and no scale row is written (the reference clamps it to row
+    0; a listing from acquire or plan_chunks never carries one). Both the
+    gather and the decode launch follow the rule."""
+    gather = _gather()
+    from vllm_expert_pager import codec
+
+    from oracle import codec_ref
+
+    dev = torch.device("cuda")
+    E, S, N = 4, 3, 16384
+    rng = np.random.default_rng(2)
+    raw = [(rng.integers(0, 256, N, dtype=np.uint8) & 0x87) | (rng.integers(9, 14, N, dtype=np.uint8) << 3)
+           for _ in range(E)]
+    P = codec_ref.pitch_of(N, 1.0, 4096) if compress else N
+    recs = [codec_ref.encode(r, P) for r in raw] if compress else None
+    src = [torch.from_numpy(np.stack([rc for rc, _ in recs] if compress else raw)).pin_memory()]
+    cache = [torch.zeros((S, N), dtype=torch.uint8, device=dev)]
+    dst = [torch.full((S, N), 0x5A, dtype=torch.uint8, device=dev)]
+    stg = [torch.full((S, P), 0x5A, dtype=torch.uint8, device=dev)] if compress else None
+    scale = [torch.arange(E * 4, dtype=torch.int32, device=dev).view(E, 4) + 1]
+    sdst = [torch.zeros((S, 4), dtype=torch.int32, device=dev)]
+    todo = torch.tensor([2, 0, 3], dtype=torch.int64, device=dev)
+    dst_row = torch.tensor([-1, 0, 2, -7], dtype=torch.int64, device=dev)  # experts 0 and 3: negative
+    no_cache = torch.full((E,), -1, dtype=torch.int64, device=dev)
+    src_row = torch.arange(E, dtype=torch.int64, device=dev)
+    gather.gather_rows(todo, dst_row, no_cache, src_row, 0, src, cache,
+                       [t.view(torch.int32) for t in dst] if not compress else dst,
+                       [t.view(torch.int32) for t in stg] if compress else None, scale, sdst)
+    if compress:
+        lut = torch.from_numpy(np.stack([l for _, l in recs])).view(E, 1, 512).to(dev)
+        codec.decode_rows(todo, dst_row, no_cache, stg, dst, lut)
+    torch.cuda.synchronize()
+    got = dst[0].cpu().numpy()
+    assert np.array_equal(got[2], raw[2])                      # expert 2 -> row 2
+    assert (got[0] == 0x5A).all() and (got[1] == 0x5A).all()   # rows 0 and 1 untouched
+    assert torch.equal(sdst[0][2], scale[0][2]) and not sdst[0][:2].any()
+    if compress:
+        s = stg[0].cpu().numpy()
+        assert np.array_equal(s[0], recs[2][0])                # todo entry 0 staged
+        assert (s[1] == 0x5A).all() and (s[2] == 0x5A).all()   # entries 1 and 2 (negative rows) not staged

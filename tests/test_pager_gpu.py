@@ -122,6 +122,23 @@ def test_prefill_overflow_matches_one_shot(model, compress, R, T):
     assert m.pager.store.failed is None
 
 
+@pytest.mark.parametrize("compress", [True, False])
+def test_prefill_with_more_working_rows_than_experts(model, compress):
+    """W = 64 working rows over 16 experts: a chunk's SSD listing (64 entries)
+    is longer than a ring slot (16 entries, the power of two >= E); its
+    experts sit below position 16, and only the slot's worth is published."""
+    m = model(16, 4, 8, 64, compress)
+    assert m.pager.store.block == 16
+    rng = np.random.default_rng(12)
+    layer = m.layers[0]
+    for T in (3, 10, 1, 10):
+        x, tw, ids = routing(rng, T, m.E, 4, zipf=0.3)
+        out = layer.forward(x, tw, ids)
+        assert same(out, m.one_shot(0, x, tw, ids)), f"T={T}"
+    assert m.pager.store.failed is None
+    assert m.pager.store.reads > 0
+
+
 def test_paging_file_flushed_after_the_last_layer(model):
     """Once every layer's weights are in, the pager flushes the paging file
     (so that the server's reads do not wait on the page cache's write-back)

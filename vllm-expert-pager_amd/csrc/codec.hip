@@ -352,8 +352,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   if (active && a.skip)
     for (int k = 0; k < a.K; ++k) active = active && a.skip[k] != e;
   if (!active || a.cache_row[e] >= 0) return;
-  const int64_t drow = a.dst_row[e] > 0 ? a.dst_row[e] : 0;
-  if (drow >= nm.dst_rows || j >= nm.stg_rows) return;
+  // A destination row outside [0, dst_rows) is skipped, never clamped.
+  const int64_t drow = a.dst_row[e];
+  if (drow < 0 || drow >= nm.dst_rows || j >= nm.stg_rows) return;
 
   const int tid = threadIdx.x;
   const uint8_t* lut = a.lut + (e * a.num_names + name) * XP_LUT_BYTES;

@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
     if (active && a.fetch)
       for (int k = 0; k < a.K; ++k) active = active && a.ssd[k] != e;
     if (!active) continue;
-    const int64_t drow = a.dst_row[e] > 0 ? a.dst_row[e] : 0;
+    const int64_t drow = a.dst_row[e];
     const int64_t crow = a.cache_row[e];
     const int64_t srow = a.src_row[e] + a.base;
     for (int n = 0; n < a.num_names; ++n) {
@@ -187,19 +187,22 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
       const uint8_t* src;
       uint8_t* dst;
       int64_t len;
+      // An expert whose destination row is outside [0, dst_rows) is not
+      // copied at all (rows, staging or scales).
+      const bool in_dst = drow >= 0 && drow < nm.dst_rows;
       bool ok;
       if (crow >= 0) {
-        ok = crow < nm.cache_rows && drow < nm.dst_rows;
+        ok = crow < nm.cache_rows && in_dst;
         src = nm.cache + crow * nm.row_bytes;
         dst = nm.dst + drow * nm.row_bytes;
         len = nm.row_bytes;
       } else if (nm.stg) {
-        ok = srow >= 0 && srow < nm.src_rows && j < nm.stg_rows;
+        ok = srow >= 0 && srow < nm.src_rows && j < nm.stg_rows && in_dst;
         src = nm.src + srow * nm.src_pitch;
         dst = nm.stg + int64_t(j) * nm.src_pitch;
         len = nm.src_pitch;
       } else {
-        ok = srow >= 0 && srow < nm.src_rows && drow < nm.dst_rows;
+        ok = srow >= 0 && srow < nm.src_rows && in_dst;
         src = nm.src + srow * nm.src_pitch;
         dst = nm.dst + drow * nm.row_bytes;
         len = nm.src_pitch;
@@ -213,7 +216,7 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(GatherArgs a) {
         }
         // The workgroup that copies chunk 0 also copies the scale row
         // (gather.py:86-99, 137-146).
-        if (item % nblocks == b && drow < nm.dst_rows)
+        if (item % nblocks == b)
           copy_bytes(nm.scale_dst + drow * nm.scale_bytes, nm.scale + e * nm.scale_bytes, nm.scale_bytes);
       }
       item += nchunks;
@@ -236,11 +239,10 @@ int g_blocks = 32;
 int64_t g_retry_us = 500000;
 int64_t g_giveup = 8;
 
-int to_ring(const xp_ring* r, RingDev* out, int64_t K, const char* what) {
+int to_ring(const xp_ring* r, RingDev* out, const char* what) {
   XP_REQUIRE(r && r->req && r->done && r->seq, "%s: ring pointers must be non-null", what);
   XP_REQUIRE(r->block >= 1 && r->ring >= 1, "%s: ring block=%lld ring=%lld", what, (long long)r->block,
              (long long)r->ring);
-  XP_REQUIRE(K <= r->block, "%s: %lld entries exceed the ring block %lld", what, (long long)K, (long long)r->block);
   *out = RingDev{r->req, r->done, r->seq, r->block, r->ring};
   return XP_OK;
 }
@@ -308,8 +310,12 @@ int xp_gather_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
   }
   int grid = g_blocks;
   if (ring) {
-    int rc = to_ring(ring, &a.ring, K, "xp_gather_rows");
+    int rc = to_ring(ring, &a.ring, "xp_gather_rows");
     if (rc) return rc;
+    // The copy skips every listed SSD expert, so all of them must be
+    // published: the list may not be longer than a ring slot.
+    XP_REQUIRE(K <= ring->block, "xp_gather_rows: %lld entries exceed the ring block %lld", (long long)K,
+               (long long)ring->block);
     XP_REQUIRE(ssd_todo != nullptr, "xp_gather_rows: a ring needs ssd_todo");
     a.fetch = 1;
     a.ssd = ssd_todo;
@@ -329,8 +335,14 @@ static int launch_fetch(const int64_t* todo, int64_t K, int64_t E, const int64_t
   if (K == 0) return XP_OK;
   XP_REQUIRE(todo && ticket && (!publish || row), "%s: null argument", what);
   RingDev r;
-  int rc = to_ring(ring, &r, K, what);
+  int rc = to_ring(ring, &r, what);
   if (rc) return rc;
+  // A request slot holds `block` entries: only todo[0 .. min(K, block)) is
+  // published and waited on, as the reference's kernels read
+  // todo[0 .. BLOCK) (gather.py:216, 254). A prefill chunk's SSD listing is
+  // W entries long, but its experts sit at chunk positions below E <= block
+  // (table.py:211-216), so nothing listed is dropped.
+  if (K > r.block) K = r.block;
   hipLaunchKernelGGL(fetch_kernel, dim3(1), dim3(kThreads), 0, as_stream(stream), todo, static_cast<int>(K),
                      static_cast<int>(E), row, base, layer, r, ticket, publish, wait,
                      g_retry_us * wallclock_ticks_per_us(), g_giveup);
