@@ -14,6 +14,8 @@ import time
 import numpy as np
 import pytest
 
+import _tiers
+
 RING, BLOCK = 4, 64
 L, E, R, W = 2, 40, 8, 2
 PITCH = (4096, 8192)
@@ -33,7 +35,7 @@ def aligned(nbytes, dtype=np.uint8):
 
 
 def pattern(layer, e, name):
-    return np.full(PITCH[name] // 4, layer * 1000 + e * 10 + name, np.int32)
+    return _tiers.expert_row(layer, e, name, PITCH[name]).view(np.int32)
 
 
 class Server:
