@@ -100,14 +100,60 @@ def dequant_weight(w: np.ndarray, ws: np.ndarray) -> np.ndarray:
     return _FP8[w] * np.kron(ws.astype(np.float64), np.ones((BLOCK, BLOCK)))
 
 
+# Planted mistakes for tests that show a set of inputs tells the rounding
+# sequence apart (expert_ffn's `variant`); each changes exactly one step.
+VARIANTS = (
+    "gate_up_unrounded",   # gate and up kept in fp32 instead of rounded to bf16
+    "gate_up_truncated",   # gate and up rounded to bf16 toward zero
+    "act_unrounded",       # silu(gate) * up not rounded to bf16 before quantisation
+    "quant_reciprocal",    # activation scale applied as a * (448 / amax) instead of a / (amax / 448)
+    "fp8_truncated",       # activations converted to fp8 toward zero
+    "weight_after_round",  # routed weight applied to bf16(y) rather than to y
+)
+
+
+def _bf16_toward_zero(v: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(v, np.float32).view(np.uint32) & np.uint32(0xFFFF0000)
+    return b.view(np.float32)
+
+
+def _fp8_toward_zero(v: np.ndarray) -> np.ndarray:
+    """fp8 codes of float32 values in [-448, 448], rounded toward zero."""
+    v = np.asarray(v, np.float32)
+    pos = np.sort(_FP8[:127])  # codes 0x00..0x7e: every finite non-negative value
+    mag = np.abs(v).astype(np.float64)
+    idx = np.searchsorted(pos, mag, side="right") - 1
+    code = np.argsort(_FP8[:127])[idx].astype(np.uint8)
+    return np.where(np.signbit(v) & (code != 0), code | 0x80, code).astype(np.uint8)
+
+
+def _quant_variant(x: np.ndarray, variant: str | None) -> tuple[np.ndarray, np.ndarray]:
+    if variant not in ("quant_reciprocal", "fp8_truncated"):
+        return quant_groups(x)
+    x = np.asarray(x, np.float32)
+    T, H = x.shape
+    g = x.reshape(T, H // BLOCK, BLOCK)
+    amax = np.abs(g).max(axis=2)
+    s = (np.maximum(amax, np.float32(EPS)) / np.float32(FP8_MAX)).astype(np.float32)
+    if variant == "quant_reciprocal":
+        inv = (np.float32(FP8_MAX) / np.maximum(amax, np.float32(EPS))).astype(np.float32)
+        q = np.clip(g * inv[:, :, None], -FP8_MAX, FP8_MAX).astype(np.float32)
+        return to_fp8(q).reshape(T, H), s
+    q = np.clip(g / s[:, :, None], np.float32(-FP8_MAX), np.float32(FP8_MAX)).astype(np.float32)
+    return _fp8_toward_zero(q).reshape(T, H), s
+
+
 def expert_ffn(x: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray, w13: np.ndarray, w13_scale: np.ndarray,
-               w2: np.ndarray, w2_scale: np.ndarray) -> np.ndarray:
+               w2: np.ndarray, w2_scale: np.ndarray, variant: str | None = None) -> np.ndarray:
     """bf16 contributions (T*topk, H) as float32; pairs with an id outside [0, E) are 0.
 
     x: (T, H) float32 holding bf16 values; w13: (E, 2I, H) fp8 codes (gate
     rows then up rows), w2: (E, H, I); scales (E, 2I/128, H/128) and
-    (E, H/128, I/128) float32.
+    (E, H/128, I/128) float32. `variant` (one of VARIANTS) plants one
+    mistake in the rounding sequence, for tests of test inputs only.
     """
+    if variant is not None and variant not in VARIANTS:
+        raise ValueError(f"unknown variant {variant!r}")
     x = np.asarray(x, np.float32)
     T, H = x.shape
     ids = np.asarray(topk_ids).reshape(T, -1)
@@ -125,14 +171,76 @@ def expert_ffn(x: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray, w1
         pairs = np.nonzero(flat == e)[0]
         tok = pairs // topk
         h = (xd[tok] @ dequant_weight(w13[e], w13_scale[e]).T).astype(np.float32)
-        gate, up = bf16(h[:, :I]), bf16(h[:, I:])
+        if variant == "gate_up_unrounded":
+            gate, up = h[:, :I], h[:, I:]
+        elif variant == "gate_up_truncated":
+            gate, up = _bf16_toward_zero(h[:, :I]), _bf16_toward_zero(h[:, I:])
+        else:
+            gate, up = bf16(h[:, :I]), bf16(h[:, I:])
         with np.errstate(over="ignore"):
             silu = (gate / (np.float32(1) + np.exp(-gate))).astype(np.float32)
-        a = bf16(silu * up)
-        aq, as_ = quant_groups(a)
+        a = (silu * up).astype(np.float32) if variant == "act_unrounded" else bf16(silu * up)
+        aq, as_ = _quant_variant(a, variant)
         y = (dequant_rows(aq, as_) @ dequant_weight(w2[e], w2_scale[e]).T).astype(np.float32)
-        out[pairs] = bf16(y * tw.reshape(-1)[pairs][:, None])
+        w = tw.reshape(-1)[pairs][:, None]
+        out[pairs] = bf16(bf16(y) * w) if variant == "weight_after_round" else bf16(y * w)
     return out
+
+
+def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk: int):
+    """A MoE case on which every sum is exact in fp32 and SiLU is exact, while
+    every rounding step of the sequence still rounds: the rounding sequence,
+    not summation order, decides the output bits.
+
+    - x: per token one or two active 128-column groups, each with one value
+      of +-448 * 2^a (so the group scale is exactly 2^a) and a few of +-1..3
+      * 2^a; the other groups are zero.
+    - w13 gate rows: only the first 128 (the first activation group) are
+      non-zero, with codes in {0, +-1, +-2} and block scale 2^10, so each
+      block dot is an integer below 2^10 and every gate is 0 or at least
+      1024 in magnitude: silu(g) is g or -0 whatever exp's last bit.
+      Up rows: codes in {0, +-1, +-2, +-3}, scale 2^-4.
+    - gate and up then carry up to 11 significant bits (bf16 keeps 8), and
+      a = bf16(gate * up) up to 16: both roundings round, ties included.
+    - w2 rows: one non-zero code in {+-1..+-4} per row, in the first
+      activation group, scale 2^-2: each dot is a single exact product, the
+      activation scale amax/448 is a general float and a / scale a general
+      quotient, so the requantisation's division and fp8 rounding are
+      exercised.
+    - routed weights: softmax over random logits.
+    Returns (x float32 holding bf16 values, topk_weights, topk_ids, w13,
+    w13_scale, w2, w2_scale) for fused_moe_ref.
+    """
+    G, GI = H // BLOCK, I // BLOCK
+    code = {v: int(to_fp8(np.array([v], np.float32))[0]) for v in (0, 1, 2, 3, 4, -1, -2, -3, -4)}
+
+    def codes(values, p, shape):
+        pick = rng.choice(len(values), size=shape, p=p)
+        return np.vectorize(lambda i: code[values[i]])(pick).astype(np.uint8)
+
+    w13 = np.zeros((E, 2 * I, H), np.uint8)
+    w13[:, :BLOCK] = codes([0, 1, -1, 2, -2], [0.8, 0.06, 0.06, 0.04, 0.04], (E, BLOCK, H))
+    w13[:, I:] = codes([0, 1, -1, 2, -2, 3, -3], [0.7, 0.08, 0.08, 0.05, 0.05, 0.02, 0.02], (E, I, H))
+    w13s = np.ones((E, 2 * GI, G), np.float32)
+    w13s[:, 0] = 2.0**10
+    w13s[:, GI:] = 2.0**-4
+    w2 = np.zeros((E, H, I), np.uint8)
+    cols = rng.integers(0, BLOCK, (E, H))
+    vals = codes([1, -1, 2, -2, 3, -3, 4, -4], [0.125] * 8, (E, H))
+    np.put_along_axis(w2, cols[:, :, None], vals[:, :, None], axis=2)
+    w2s = np.full((E, H // BLOCK, GI), 2.0**-2, np.float32)
+
+    x = np.zeros((T, H), np.float32)
+    for t in range(T):
+        for g in rng.choice(G, size=int(rng.integers(1, 3)), replace=False):
+            a = int(rng.integers(-3, 4))
+            cols_t = rng.choice(BLOCK, size=4, replace=False) + g * BLOCK
+            x[t, cols_t[0]] = rng.choice([-448.0, 448.0]) * 2.0**a
+            x[t, cols_t[1:]] = rng.choice([-3.0, -2.0, -1.0, 1.0, 2.0, 3.0], size=3) * 2.0**a
+    ids = np.stack([rng.permutation(E)[:topk] for _ in range(T)]).astype(np.int64)
+    logits = rng.standard_normal((T, topk)).astype(np.float32)
+    tw = (np.exp(logits) / np.exp(logits).sum(1, keepdims=True)).astype(np.float32)
+    return x, tw, ids, w13, w13s, w2, w2s
 
 
 def topk_sum(contrib: np.ndarray, topk_ids: np.ndarray, num_experts: int) -> np.ndarray:
@@ -149,9 +257,9 @@ def topk_sum(contrib: np.ndarray, topk_ids: np.ndarray, num_experts: int) -> np.
     return bf16(acc)
 
 
-def fused_moe_ref(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale) -> np.ndarray:
+def fused_moe_ref(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, variant=None) -> np.ndarray:
     """The layer output (T, H) as float32 holding bf16 values."""
-    contrib = expert_ffn(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale)
+    contrib = expert_ffn(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, variant)
     return topk_sum(contrib, topk_ids, w13.shape[0])
 
 

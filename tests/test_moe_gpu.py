@@ -3,7 +3,10 @@
 - quant_tokens: bit-exact codes and scales.
 - route: every mapped pair listed under its slot exactly once; tiles cover
   each slot's list in runs of at most 64.
-- fused_moe (one-shot): within the stated bf16 tolerance of the w8a8 oracle.
+- fused_moe on exact-arithmetic inputs: bit-exact against the w8a8 oracle
+  (the rounding sequence), for the prefill-sized and the decode-sized kernels.
+- fused_moe (one-shot) on random inputs: within the stated bf16 tolerance of
+  the w8a8 oracle.
 - chunked == one-shot, bit for bit: the experts run W at a time through a
   W-row slab with a per-chunk expert_map, the top-k sum once at the end
   (experts.py:455-577), at small shapes and at 2048 tokens x top-8 over 256
@@ -18,21 +21,26 @@ from oracle import moe_ref as M
 
 pytestmark = pytest.mark.gpu
 
-# Tolerance of the bf16 layer output against the oracle. The oracle takes
-# dot products in float64; the fp8 MFMA accumulates with about 2^-15 relative
-# precision, so a gate/up value can round to the neighbouring bf16 value, and
-# when that value is the maximum of its 128-column group the whole group is
-# re-quantised to fp8 with a slightly different scale. Such rare flips move
-# an output by up to a few percent of the output rms; a wrong operand, scale
-# block or index moves all of them by tens of percent. The checks:
-#   |got - ref| <= RTOL * |ref| + ATOL * rms(ref)      (every element)
-#   ||got - ref|| <= FRO * ||ref||                     (relative Frobenius)
-#   at least MIN_EXACT of the elements bit-identical (measured: 0.72-0.92;
-#   rounding by truncation instead of to nearest even leaves about half)
-RTOL = 1.6e-2
-ATOL = 0.125
-FRO = 2.0**-7
-MIN_EXACT = 0.6
+# Tolerance of the bf16 layer output against the oracle on random inputs.
+# The rounding sequence itself is pinned bit for bit by
+# test_exact_inputs_bit_exact; what is left on random inputs is the fp8
+# MFMA's block sum, which is not a correctly rounded fp32 sum (fp8 matrix
+# units accumulate with limited alignment precision; the oracle takes its dot
+# products in float64). So a gate or up value near a bf16 rounding boundary
+# can round to the neighbouring bf16 value, and when it is its group's
+# maximum the group is re-quantised with another scale; each such flip moves
+# the outputs of its token by a few percent of the output rms at most.
+# Measured over 30 random cases (5 shapes x 6 seeds, E 8-256, H 256-2048,
+# I 128-768, 1-96 tokens, top-4/8): bit-identical 0.68-0.97 of elements,
+# within 2 bf16 ulps 0.94-0.997, relative Frobenius error 0.6e-3 to 3.7e-3,
+# max |d| 0.011-0.053 of rms(ref). The bounds sit about 1.5x outside the
+# worst measured case; a wrong operand, scale block or index moves outputs
+# by tens of percent of rms and fails all four.
+RTOL = 1.6e-2       # two bf16 ulps of the element itself
+ATOL = 0.08         # of rms(ref): the flips' reach (measured max 0.053)
+FRO = 2.0**-7       # relative Frobenius (measured max 3.7e-3)
+MIN_EXACT = 0.6     # bit-identical fraction (measured min 0.68)
+MIN_ULP2 = 0.9      # fraction within 2 bf16 ulps (measured min 0.94)
 
 
 def _moe():
@@ -60,11 +68,33 @@ def _check_close(got: np.ndarray, ref: np.ndarray, what: str) -> None:
     exact = float(np.mean(got == ref))
     fro = float(np.sqrt((diff**2).sum() / (ref.astype(np.float64) ** 2).sum()))
     worst = float((diff / bound).max())
-    print(f"{what}: exact {exact:.4f}, rel fro {fro:.2e}, max |d|/rms {diff.max() / rms:.3e}, "
-          f"worst d/bound {worst:.3f}")
+    ulps = np.abs(got.astype(np.float32).view(np.int32) - ref.astype(np.float32).view(np.int32)) >> 16
+    ulp2 = float(np.mean(ulps <= 2))
+    print(f"{what}: exact {exact:.4f}, within 2 ulps {ulp2:.4f}, rel fro {fro:.2e}, "
+          f"max |d|/rms {diff.max() / rms:.3e}, worst d/bound {worst:.3f}")
     assert (diff <= bound).all(), f"{what}: {(diff > bound).sum()} elements outside tolerance"
     assert fro <= FRO, f"{what}: relative Frobenius error {fro:.3e} > {FRO:.3e}"
     assert exact >= MIN_EXACT, f"{what}: only {exact:.4f} of elements bit-exact"
+    assert ulp2 >= MIN_ULP2, f"{what}: only {ulp2:.4f} of elements within 2 bf16 ulps"
+
+
+@pytest.mark.parametrize("E, T, topk, seed", [(64, 150, 4, 0), (8, 8, 8, 108)], ids=["wide", "narrow"])
+def test_exact_inputs_bit_exact(E, T, topk, seed):
+    """On inputs where every sum is exact and SiLU is exact (moe_ref.exact_inputs),
+    the kernels' output is decided by their rounding sequence alone, and it
+    equals the oracle's bit for bit, for the prefill-sized kernels (tile bound
+    >= 64) and the decode-sized ones. test_oracle_moe.py shows that each
+    planted mistake in the sequence changes the oracle's output on these same
+    cases, so each step is pinned here."""
+    moe = _moe()
+    x, tw, ids, w13, w13s, w2, w2s = M.exact_inputs(np.random.default_rng(seed), E, 512, 256, T, topk)
+    bound = int(__import__("vllm_expert_pager._native", fromlist=["lib"]).lib().xp_moe_max_tiles(T * topk, E))
+    assert (bound >= 64) == (E == 64)  # which kernels run
+    xb = _bf16(x)
+    assert torch.equal(xb.float().cpu(), torch.from_numpy(x))  # x holds bf16 values
+    out = moe.fused_moe(xb, *_dev(tw, ids, w13, w13s, w2, w2s)).float().cpu().numpy()
+    ref = M.fused_moe_ref(x, tw, ids, w13, w13s, w2, w2s)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"{int((out != ref).sum())} elements differ"
 
 
 def test_quant_tokens_bit_exact():
@@ -131,11 +161,12 @@ def _case(seed, E, H, I, T, topk, softmax=True):
 
 @pytest.mark.parametrize(
     "E, H, I, T, topk",
-    [(8, 256, 128, 37, 4), (16, 2048, 512, 96, 8), (256, 2048, 512, 1, 8)],
+    [(8, 256, 128, 37, 4), (16, 2048, 512, 96, 8), (256, 2048, 512, 1, 8), (64, 2048, 768, 40, 8)],
 )
-def test_fused_moe_matches_oracle(E, H, I, T, topk):
+@pytest.mark.parametrize("seed", [0, 1])
+def test_fused_moe_matches_oracle(E, H, I, T, topk, seed):
     moe = _moe()
-    x, tw, ids, w13, w13s, w2, w2s = _case(E + T, E, H, I, T, topk)
+    x, tw, ids, w13, w13s, w2, w2s = _case(1000 * seed + E + T, E, H, I, T, topk)
     xb = _bf16(x)
     tw_t, ids_t, w13_t, w13s_t, w2_t, w2s_t = _dev(tw, ids, w13, w13s, w2, w2s)
     out = moe.fused_moe(xb, tw_t, ids_t, w13_t, w13s_t, w2_t, w2s_t).float().cpu().numpy()

@@ -126,3 +126,47 @@ def test_topk_sum_exact_and_skips_invalid():
     cc = c.reshape(T, K, H)
     ok = ((ids >= 0) & (ids < 4))[:, :, None]
     assert np.array_equal(got, (cc * ok).sum(axis=1))
+
+
+# (experts, tokens, top-k, seed) of the exact-input cases, shared with the GPU
+# test: 150 tokens x top-4 over 64 experts is a prefill-sized call (the wide
+# GEMM kernels), 8 x top-8 over 8 experts a decode-sized one (the narrow ones).
+EXACT_CASES = [(64, 150, 4, 0), (8, 8, 8, 108)]
+
+
+@pytest.mark.parametrize("E, T, topk, seed", EXACT_CASES)
+def test_exact_inputs_tell_every_rounding_step_apart(E, T, topk, seed):
+    """On exact_inputs every sum is exact and SiLU is exact, so the output is
+    decided by the rounding sequence alone; each planted mistake in that
+    sequence (M.VARIANTS) changes it. A GPU kernel that equals the oracle bit
+    for bit on these inputs (tests/test_moe_gpu.py) therefore rounds gate and
+    up to bf16 to nearest even, rounds silu(gate) * up to bf16, divides by
+    amax / 448, converts to fp8 to nearest even and weights y before its one
+    bf16 rounding."""
+    rng = np.random.default_rng(seed)
+    case = M.exact_inputs(rng, E, 512, 256, T, topk)
+    ref = M.fused_moe_ref(*case)
+    assert np.isfinite(ref).all() and (ref != 0).mean() > 0.1
+    for v in M.VARIANTS:
+        assert not np.array_equal(M.fused_moe_ref(*case, variant=v), ref), v
+
+
+def test_exact_inputs_keep_their_promises():
+    """Group scales of x are powers of two, every gate is 0 or of magnitude
+    >= 104 (exp(-|g|) below half an fp32 ulp of 1, exp(|g|) beyond fp32), and
+    every block dot is an integer below 2^11 (exact in any fp32 accumulation)."""
+    rng = np.random.default_rng(5)
+    x, tw, ids, w13, w13s, w2, w2s = M.exact_inputs(rng, 8, 512, 256, 64, 4)
+    xq, xs = M.quant_groups(x)
+    live = xs > 1e-9
+    assert np.all(np.log2(xs[live]) == np.round(np.log2(xs[live])))
+    fp8 = M.fp8_values()
+    xv = fp8[xq].reshape(64, 4, 128)
+    for e in range(8):
+        w = fp8[w13[e]].reshape(512, 4, 128)
+        dots = np.einsum("tgk,ngk->tng", xv, w)
+        assert np.all(dots == np.round(dots)) and np.abs(dots).max() < 2**11
+        gate = (M.dequant_rows(xq, xs) @ M.dequant_weight(w13[e], w13s[e]).T)[:, :256]
+        nz = gate[gate != 0]
+        assert nz.size and np.abs(nz).min() >= 104
+    assert ((w2 != 0).sum(axis=2) == 1).all()

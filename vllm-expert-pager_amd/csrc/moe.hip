@@ -1026,29 +1026,41 @@ int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I) {
   return work_layout(npairs, I, nullptr, nullptr);
 }
 
-int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
-                   int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
-                   int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, void* work,
-                   int64_t work_bytes, uint16_t* out, void* stream) {
+}  // extern "C"
+
+namespace xp {
+namespace {
+
+// Argument checks of xp_moe_experts (all but the workspace's).
+int check_experts(const char* what, const uint8_t* xq, const float* xs, int64_t T, int64_t topk,
+                  const float* topk_weight, int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale,
+                  const uint8_t* w2, const float* w2_scale, int64_t slots, const int32_t* offsets,
+                  const int32_t* pairs, const int32_t* tiles, const uint16_t* out) {
   XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0 && H <= kKB * kMaxKB && I <= kKB * kMaxKB,
-             "xp_moe_experts: H=%lld and I=%lld must be multiples of %d, at most %d", (long long)H, (long long)I,
-             kBN, kKB * kMaxKB);
+             "%s: H=%lld and I=%lld must be multiples of %d, at most %d", what, (long long)H, (long long)I, kBN,
+             kKB * kMaxKB);
   XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX && slots >= 1 && slots <= kMaxRouteSlots,
-             "xp_moe_experts: T=%lld, topk=%lld, slots=%lld", (long long)T, (long long)topk, (long long)slots);
+             "%s: T=%lld, topk=%lld, slots=%lld", what, (long long)T, (long long)topk, (long long)slots);
   if (T == 0) return XP_OK;
-  XP_REQUIRE(xq && xs && topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && work && out,
-             "xp_moe_experts: null argument");
-  XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(out) &&
-                 (reinterpret_cast<uintptr_t>(work) & 255) == 0,
-             "xp_moe_experts: fp8 and output buffers must be 16-byte aligned, the workspace 256-byte aligned");
+  XP_REQUIRE(xq && xs && topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && out,
+             "%s: null argument", what);
+  XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(out),
+             "%s: fp8 and output buffers must be 16-byte aligned", what);
+  const int64_t bound = xp_moe_max_tiles(T * topk, slots);
+  XP_REQUIRE(bound <= 65535, "%s: %lld tiles exceed the launch grid", what, (long long)bound);
+  return XP_OK;
+}
+
+// The two (or, for few pairs, narrow) GEMM launches of one expert call over a
+// workspace of xp_moe_workspace_bytes(T * topk, I) bytes at `work`.
+int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
+                   int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
+                   int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, uint8_t* work,
+                   uint16_t* out, void* stream) {
   const int64_t npairs = T * topk;
-  const int64_t need = xp_moe_workspace_bytes(npairs, I);
-  XP_REQUIRE(work_bytes >= need, "xp_moe_experts: workspace of %lld B, needs %lld", (long long)work_bytes,
-             (long long)need);
   const int64_t bound = xp_moe_max_tiles(npairs, slots);
-  XP_REQUIRE(bound <= 65535, "xp_moe_experts: %lld tiles exceed the launch grid", (long long)bound);
   Work w;
-  work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
+  work_layout(npairs, I, &w, work);
   const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
   const int64_t g2 = tiles8 * (H / kBN);
   XP_REQUIRE(g2 <= INT32_MAX, "xp_moe_experts: grid too large");
@@ -1081,6 +1093,27 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
     hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, as_stream(stream), H, I,
                        topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
   return check_launch("gemm2_kernel");
+}
+
+}  // namespace
+}  // namespace xp
+
+extern "C" {
+
+int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
+                   int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
+                   int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, void* work,
+                   int64_t work_bytes, uint16_t* out, void* stream) {
+  int rc = check_experts("xp_moe_experts", xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots,
+                         offsets, pairs, tiles, out);
+  if (rc || T == 0) return rc;
+  XP_REQUIRE(work && (reinterpret_cast<uintptr_t>(work) & 255) == 0,
+             "xp_moe_experts: the workspace must be non-null and 256-byte aligned");
+  const int64_t need = xp_moe_workspace_bytes(T * topk, I);
+  XP_REQUIRE(work_bytes >= need, "xp_moe_experts: workspace of %lld B, needs %lld", (long long)work_bytes,
+             (long long)need);
+  return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
+                        tiles, static_cast<uint8_t*>(work), out, stream);
 }
 
 int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk, int64_t H, const void* topk_ids,
