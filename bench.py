@@ -92,6 +92,29 @@ def decode_traffic(rows: int):
     return None
 
 
+def warm_by_time(step, min_ms: float = 200.0, batch: int = 10, tol: float = 0.02, max_s: float = 5.0) -> dict:
+    """Launch `step` in batches until at least `min_ms` of launches have run and
+    two consecutive batches agree within `tol`, so the timed launches that
+    follow run at steady clocks whatever --warmup is (at most `max_s`)."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    spent, prev, batches = 0.0, None, 0
+    t0 = time.time()
+    while True:
+        e0.record()
+        for _ in range(batch):
+            step()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / batch
+        spent += ms * batch
+        batches += 1
+        steady = prev is not None and abs(ms - prev) <= tol * prev
+        if (spent >= min_ms and steady) or time.time() - t0 > max_s:
+            return {"launches": batches * batch, "ms": round(spent, 1), "steady": steady,
+                    "last_ms_per_launch": round(ms, 4)}
+        prev = ms
+
+
 def bench_decode(args, dev, cores):
     from oracle import codec_ref
     from vllm_expert_pager import codec
@@ -116,6 +139,9 @@ def bench_decode(args, dev, cores):
 
     for _ in range(args.warmup):
         step()
+    torch.cuda.synchronize()
+    warm = warm_by_time(step)
+    log(f"decode warm-up: {warm}")
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -168,6 +194,7 @@ def bench_decode(args, dev, cores):
     log(f"cpu decode: {cpu_gbps:.2f} GB/s on {cores} threads ({sample} experts x {reps} reps)")
     return {
         "ms": ms,
+        "warm": warm,
         "gbps": gbps,
         "raw_gbps": raw_gbps,
         "alg_bytes": alg,
@@ -902,6 +929,7 @@ def main() -> None:
             "traffic": decode_traffic(args.rows),
         },
         "cpu_baseline": dec["cpu"],
+        "decode_warmup": dec["warm"],
         "decode_raw_output_gbps": round(dec["raw_gbps"], 2),
         "decode_gbps_by_rows": dec["sweep"],
         "decode_us_by_rows": dec["sweep_us"],
