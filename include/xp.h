@@ -347,6 +347,29 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T,
                    const int32_t* tiles, void* work, int64_t work_bytes,
                    uint16_t* out, void* stream);
 
+/* Workspace bytes xp_moe_experts_noalloc holds per device (32 MiB: a
+ * 2048-token top-8 prefill at I = 512 needs 27.5 MB). */
+#define XP_MOE_SCRATCH_BYTES (32LL << 20)
+
+/* xp_moe_experts without a workspace argument, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * workspace is a device array inside the library, XP_MOE_SCRATCH_BYTES on
+ * every device it runs on, kept until the process ends; the call allocates
+ * nothing. A call whose xp_moe_workspace_bytes(T * topk, I) exceeds
+ * XP_MOE_SCRATCH_BYTES fails with XP_E_LIMIT before launching anything. All
+ * calls on one device share that array, and nothing in it needs to start
+ * zeroed: calls that overlap on one device (several streams, or several
+ * threads without ordering) race; calls ordered on one stream do not.
+ * Same arguments, results and bits as xp_moe_experts otherwise. */
+int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T,
+                           int64_t topk, const float* topk_weight, int64_t H,
+                           int64_t I, const uint8_t* w13,
+                           const float* w13_scale, const uint8_t* w2,
+                           const float* w2_scale, int64_t slots,
+                           const int32_t* offsets, const int32_t* pairs,
+                           const int32_t* tiles, uint16_t* out, void* stream);
+
 /* The single top-k combine (moe_sum after collect, experts.py:546-552):
  * out[t][H] = bf16(sum over k ascending of fp32(contrib[t*topk + k])),
  * skipping pairs whose id is outside [0, num_experts). */

@@ -1,0 +1,83 @@
+"""xp_moe_experts_noalloc: the expert FFN with the library's own workspace.
+
+Called through the C ABI and compared bit for bit with xp_moe_experts (the
+caller-provided workspace) on the same routing, twice in a row on one device
+with the second call smaller than the first: a prefill-sized call (the wide
+GEMM kernels) then a decode-sized one (the narrow kernels), which leaves the
+first call's contents in the shared array. A call whose workspace would not
+fit is refused with XP_E_LIMIT before anything is launched.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as M
+
+pytestmark = pytest.mark.gpu
+
+
+def _nat():
+    from vllm_expert_pager import _native, moe
+
+    return _native, moe
+
+
+def _inputs(rng, E, H, I, T, topk):
+    w13, w13s, w2, w2s = (torch.from_numpy(a).cuda() for a in M.random_experts(rng, E, H, I))
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).cuda()
+    ids = torch.from_numpy(np.stack([rng.permutation(E)[:topk] for _ in range(T)]).astype(np.int64)).cuda()
+    tw = torch.softmax(torch.from_numpy(rng.standard_normal((T, topk)).astype(np.float32)), 1).cuda()
+    return x, tw, ids, w13, w13s, w2, w2s
+
+
+def _run(entry, x, tw, ids, w13, w13s, w2, w2s):
+    """One expert call through the C ABI; returns the (T*topk, H) bf16 contributions."""
+    nat, moe = _nat()
+    E, T, topk, H, I = w13.shape[0], ids.shape[0], ids.shape[1], x.shape[1], w2.shape[2]
+    xq, xs = moe.quant_tokens(x)
+    r = moe.route(ids, torch.arange(E, dtype=torch.int32, device="cuda"), E)
+    out = torch.full((T * topk, H), -1, dtype=torch.int16, device="cuda")
+    head = (xq.data_ptr(), xs.data_ptr(), T, topk, tw.data_ptr(), H, I, w13.data_ptr(), w13s.data_ptr(),
+            w2.data_ptr(), w2s.data_ptr(), E, r.offsets.data_ptr(), r.pairs.data_ptr(), r.tiles.data_ptr())
+    if entry == "xp_moe_experts":
+        nbytes = int(nat.lib().xp_moe_workspace_bytes(T * topk, I))
+        work = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
+        rc = nat.lib().xp_moe_experts(*head, work.data_ptr(), nbytes, out.data_ptr(), nat.stream())
+    else:
+        rc = nat.lib().xp_moe_experts_noalloc(*head, out.data_ptr(), nat.stream())
+    assert rc == 0, nat.lib().xp_last_error()
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("seed", [0])
+def test_noalloc_matches_the_workspace_entry_point_twice(seed):
+    nat, _ = _nat()
+    rng = np.random.default_rng(seed)
+    E, H, I = 32, 2048, 512
+    # 600 tokens x top-8 = 4800 pairs (wide kernels, 8.1 MB of workspace),
+    # then 3 tokens (narrow kernels) over the array the first call filled.
+    for T in (600, 3):
+        case = _inputs(rng, E, H, I, T, 8)
+        need = int(nat.lib().xp_moe_workspace_bytes(T * 8, I))
+        assert need <= 32 << 20
+        want = _run("xp_moe_experts", *case)
+        got = _run("xp_moe_experts_noalloc", *case)
+        assert torch.equal(got, want), f"T={T}"
+        assert int((want == -1).sum()) == 0  # every pair was written
+
+
+def test_noalloc_refuses_a_workspace_above_its_limit():
+    nat, moe = _nat()
+    lib = nat.lib()
+    T, topk, H, I, E = 8192, 8, 2048, 512, 16
+    assert int(lib.xp_moe_workspace_bytes(T * topk, I)) > 32 << 20
+    dummy = torch.zeros((16,), dtype=torch.uint8, device="cuda")
+    p = dummy.data_ptr()
+    rc = lib.xp_moe_experts_noalloc(p, p, T, topk, p, H, I, p, p, p, p, E, p, p, p, p, nat.stream())
+    assert rc == nat.XP_E_LIMIT
+    assert b"above the library's" in lib.xp_last_error()
+    torch.cuda.synchronize()

@@ -28,6 +28,8 @@
 // once.
 #include <hip/hip_bf16.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace xp {
@@ -1031,7 +1033,8 @@ int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I) {
 namespace xp {
 namespace {
 
-// Argument checks of xp_moe_experts (all but the workspace's).
+// Argument checks shared by xp_moe_experts and xp_moe_experts_noalloc (all
+// but the workspace's).
 int check_experts(const char* what, const uint8_t* xq, const float* xs, int64_t T, int64_t topk,
                   const float* topk_weight, int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale,
                   const uint8_t* w2, const float* w2_scale, int64_t slots, const int32_t* offsets,
@@ -1098,6 +1101,42 @@ int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
 }  // namespace
 }  // namespace xp
 
+// Workspace of xp_moe_experts_noalloc, one copy on every device the library
+// runs on (held until the process ends). Host code never passes this name to
+// a kernel: it stands for the host-side shadow, and each device's own
+// address comes from hipGetSymbolAddress (scratch_address).
+static __device__ __align__(256) uint8_t scratch[XP_MOE_SCRATCH_BYTES];
+
+namespace xp {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kMaxDevices];  // device address of `scratch`, per device
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device (with it current) and kept.
+int scratch_address(uint8_t** out) {
+  int dev = -1;
+  XP_HIP(hipGetDevice(&dev));
+  XP_REQUIRE(dev >= 0 && dev < kMaxDevices, "xp_moe_experts_noalloc: device %d (at most %d devices)", dev,
+             kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(XP_E_HIP, "xp_moe_experts_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return XP_OK;
+}
+
+}  // namespace
+}  // namespace xp
+
 extern "C" {
 
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
@@ -1114,6 +1153,26 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
              (long long)need);
   return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
                         tiles, static_cast<uint8_t*>(work), out, stream);
+}
+
+int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight,
+                           int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
+                           const float* w2_scale, int64_t slots, const int32_t* offsets, const int32_t* pairs,
+                           const int32_t* tiles, uint16_t* out, void* stream) {
+  int rc = check_experts("xp_moe_experts_noalloc", xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2,
+                         w2_scale, slots, offsets, pairs, tiles, out);
+  if (rc || T == 0) return rc;
+  const int64_t need = xp_moe_workspace_bytes(T * topk, I);
+  if (need > XP_MOE_SCRATCH_BYTES)
+    return fail(XP_E_LIMIT,
+                "xp_moe_experts_noalloc: %lld pairs x I=%lld need a workspace of %lld B, above the library's "
+                "%lld B; call xp_moe_experts with a workspace instead",
+                (long long)(T * topk), (long long)I, (long long)need, (long long)XP_MOE_SCRATCH_BYTES);
+  uint8_t* work = nullptr;
+  rc = scratch_address(&work);
+  if (rc) return rc;
+  return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
+                        tiles, work, out, stream);
 }
 
 int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk, int64_t H, const void* topk_ids,
