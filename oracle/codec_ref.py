@@ -32,7 +32,8 @@ LANES = 32
 GROUP = CHUNK * LANES
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB = os.path.join(_HERE, "liboracle.so")
+# XP_ORACLE_LIBRARY names another build of codec_ref.c (a sanitizer build).
+_LIB = os.environ.get("XP_ORACLE_LIBRARY") or os.path.join(_HERE, "liboracle.so")
 
 
 def huffman_lengths(counts):
@@ -188,17 +189,19 @@ def decode_ref(rec: bytes, lut: bytes, n: int, chunk: int) -> list[int]:
 _lib = None
 
 
-def build_lib() -> str:
+def build_lib(out: str | None = None, sanitize: bool = False) -> str:
+    """Compile codec_ref.c into `out` (default: the library _load() uses);
+    with `sanitize`, under AddressSanitizer and UndefinedBehaviorSanitizer."""
     import subprocess
 
+    out = out or _LIB
     src = os.path.join(_HERE, "codec_ref.c")
-    tmp = _LIB + f".tmp{os.getpid()}"
-    subprocess.run(
-        ["gcc", "-O3", "-std=c11", "-fPIC", "-shared", "-pthread", src, "-o", tmp],
-        check=True,
-    )
-    os.replace(tmp, _LIB)
-    return _LIB
+    tmp = out + f".tmp{os.getpid()}"
+    opt = (["-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+            "-fno-sanitize-recover=undefined"] if sanitize else ["-O3"])
+    subprocess.run(["gcc", *opt, "-std=c11", "-fPIC", "-shared", "-pthread", src, "-o", tmp], check=True)
+    os.replace(tmp, out)
+    return out
 
 
 def _load():

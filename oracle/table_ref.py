@@ -196,3 +196,43 @@ class LruRef:
 
     def cached(self) -> set[int]:
         return set(self.slot_of)
+
+
+# ---- timing helper for the CPU baseline (bench.py) ----
+
+def acquire_trace_rate(ids: np.ndarray, E: int, S: int, R: int, seconds: float,
+                       start_at: float | None = None) -> tuple[int, float]:
+    """Replay a routing trace ids (steps, layers, topk) through TableRef.acquire
+    of both tables of each layer (a VRAM table of S slots, a RAM table of R
+    warm slots), step after step, for about `seconds` from `start_at` (a
+    time.time() value, so that several processes overlap). Returns (layer
+    acquires done, seconds taken)."""
+    import time
+
+    steps, layers = ids.shape[:2]
+    refs = []
+    for _ in range(layers):
+        v, r = TableRef(E, S), TableRef(E, R)
+        r.warm(R)
+        refs.append((v, r))
+    if start_at is not None:
+        time.sleep(max(0.0, start_at - time.time()))
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        row = ids[n % steps]
+        for layer in range(layers):
+            refs[layer][0].acquire(row[layer], pair_slots=True)
+            refs[layer][1].acquire(row[layer], pair_slots=True)
+        n += 1
+    return n * layers, time.perf_counter() - t0
+
+
+if __name__ == "__main__":
+    # python -m oracle.table_ref IDS.npy E S R SECONDS START_AT: one process of
+    # the all-cores acquire baseline; prints "<layer acquires> <seconds>".
+    import sys
+
+    _ids = np.load(sys.argv[1])
+    _E, _S, _R = (int(x) for x in sys.argv[2:5])
+    _n, _dt = acquire_trace_rate(_ids, _E, _S, _R, float(sys.argv[5]), float(sys.argv[6]))
+    print(_n, _dt)

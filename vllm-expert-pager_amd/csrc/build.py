@@ -41,7 +41,7 @@ HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "encode.hip", "moe.hip"]
 HIP_HOST_SOURCES = ["host.cpp", "codec_host.cpp"]  # HIP runtime API or headers
-HOST_SOURCES = ["ssd.cpp"]
+HOST_SOURCES = ["error.cpp", "ssd.cpp"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -93,11 +93,34 @@ def build(jobs: int = 8, verbose: bool = False) -> str:
     return OUT
 
 
+def build_host_sanitized(kind: str, out_dir: str, verbose: bool = False) -> str:
+    """The host-only part of libxp (host encoder, code construction, SSD
+    server: no HIP) built with a sanitizer (``address`` -- with
+    UndefinedBehaviorSanitizer -- or ``thread``) into out_dir/libxp.so, for
+    the CPU tests to load through VLLM_EXPERT_PAGER_LIBRARY with the
+    sanitizer's runtime preloaded. GPU entry points are absent from it."""
+    flags = {"address": ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"],
+             "thread": ["-fsanitize=thread"]}[kind]
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "libxp.so")
+    srcs = [os.path.join(HERE, s) for s in ("error.cpp", "codec_host.cpp", "ssd.cpp")]
+    # code_build.h marks its functions __host__ __device__: the HIP headers
+    # define those away for a host compiler.
+    _run(["g++", "-O1", "-g", "-fno-omit-frame-pointer", "-std=c++17", "-fPIC", "-shared", "-pthread", *flags,
+          f"-I{ROCM}/include", "-D__HIP_PLATFORM_AMD__", *srcs, "-o", out], verbose)
+    return out
+
+
 def main() -> None:
     p = argparse.ArgumentParser()
     p.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     p.add_argument("--verbose", action="store_true")
+    p.add_argument("--sanitize", choices=["address", "thread"],
+                   help="build only the host part, with this sanitizer, into csrc/_build/san-<kind>/")
     a = p.parse_args()
+    if a.sanitize:
+        print(build_host_sanitized(a.sanitize, os.path.join(BUILD, f"san-{a.sanitize}"), a.verbose))
+        return
     print(build(a.jobs, a.verbose))
 
 

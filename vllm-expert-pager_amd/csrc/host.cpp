@@ -1,7 +1,6 @@
-// Error reporting, version and pinned host memory of libxp.
+// Launch checks, version and pinned host memory of libxp.
 #include <hip/hip_runtime.h>
 
-#include <cstdarg>
 #include <cstdio>
 #include <mutex>
 #include <unordered_map>
@@ -9,18 +8,6 @@
 #include "common.h"
 
 namespace xp {
-
-static thread_local char g_err[1024] = "";
-
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof g_err, fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-void clear_error() { g_err[0] = '\0'; }
 
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
@@ -47,8 +34,6 @@ int64_t wallclock_ticks_per_us() {
 }  // namespace xp
 
 extern "C" {
-
-const char* xp_last_error(void) { return xp::g_err; }
 
 const char* xp_version(void) { return "libxp 0.1 gfx950"; }
 

@@ -13,7 +13,10 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libxp.so")
+# The library next to this file; VLLM_EXPERT_PAGER_LIBRARY names another
+# build (the sanitizer builds of the host code that the CPU tests load).
+LIB_PATH = os.environ.get("VLLM_EXPERT_PAGER_LIBRARY") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "libxp.so")
 
 XP_OK, XP_E_ARG, XP_E_PITCH, XP_E_SHAPE, XP_E_HIP, XP_E_LIMIT = range(6)
 
