@@ -303,15 +303,18 @@ void ssd_test_delay(ssd_t* s, double seconds);
 int xp_quant_tokens(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq,
                     float* xs, void* stream);
 
-/* Upper bound on the tiles route can produce for `npairs` pairs over
- * `slots` slots; size `tiles` as 1 + 2 * bound ints. */
+/* Size of route's tile lists for `npairs` pairs over `slots` slots: size
+ * `tiles` as 1 + 2 * xp_moe_max_tiles(npairs, slots) ints. */
 int64_t xp_moe_max_tiles(int64_t npairs, int64_t slots);
 
 /* List the pairs whose expert e (0 <= e < num_experts) has
  * 0 <= expert_map[e] < slots under that slot, in CSR form:
  * offsets[slots + 1], pairs[offsets[s] .. offsets[s+1]) (any order within a
- * slot; pairs holds up to T*topk entries), and tiles[0] = tile count followed
- * by (slot, first position) per tile of at most 64 pairs. slots <= 1024. */
+ * slot; pairs holds up to T*topk entries). tiles[0] = tile count, then
+ * (slot, first position) per tile of at most 64 pairs; from
+ * tiles[1 + 2 * tb], tb = ceil(npairs / 64) + min(slots, npairs), the wide
+ * tiles the prefill kernels run over: count, then (slot, first position,
+ * pair count) per wide tile of at most 128 pairs. slots <= 1024. */
 int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T,
                  int64_t topk, const int32_t* expert_map, int64_t num_experts,
                  int64_t slots, int32_t* offsets, int32_t* pairs,
@@ -335,10 +338,12 @@ int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I);
  *   out[pair][H] = bf16(topk_weight[pair] * (w2 . a)) (bf16 bits)
  * topk_weight is fp32 [T*topk]; work is a 256-byte aligned device buffer of
  * xp_moe_workspace_bytes(T*topk, I) bytes (no initial contents needed).
- * Pairs that were not routed are not written. Three launches: gate/up
- * (32 activation columns per workgroup, K split over its waves), activation
- * quantisation, down projection. H and I are multiples of 128, at most 8192;
- * fp8 buffers and out 16-byte aligned. */
+ * Pairs that were not routed are not written. Two launches, gate/up (with
+ * the activation quantisation) and down projection: at prefill sizes
+ * (64 or more tiles can exist) persistent workgroups over the wide tiles,
+ * otherwise 16-row subtiles. H and I are multiples of 128, at most 8192;
+ * at prefill sizes T*H and T*topk*I are below 2^32; fp8 buffers and out
+ * 16-byte aligned. */
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T,
                    int64_t topk, const float* topk_weight, int64_t H,
                    int64_t I, const uint8_t* w13, const float* w13_scale,

@@ -88,13 +88,18 @@ def test_exact_inputs_bit_exact(E, T, topk, seed):
     cases, so each step is pinned here."""
     moe = _moe()
     x, tw, ids, w13, w13s, w2, w2s = M.exact_inputs(np.random.default_rng(seed), E, 512, 256, T, topk)
-    bound = int(__import__("vllm_expert_pager._native", fromlist=["lib"]).lib().xp_moe_max_tiles(T * topk, E))
+    bound = _tile_bound(T * topk, E)
     assert (bound >= 64) == (E == 64)  # which kernels run
     xb = _bf16(x)
     assert torch.equal(xb.float().cpu(), torch.from_numpy(x))  # x holds bf16 values
     out = moe.fused_moe(xb, *_dev(tw, ids, w13, w13s, w2, w2s)).float().cpu().numpy()
     ref = M.fused_moe_ref(x, tw, ids, w13, w13s, w2, w2s)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"{int((out != ref).sum())} elements differ"
+
+
+def _tile_bound(npairs, slots):
+    """Tiles of 64 pairs route can produce (the prefill kernels run from 64)."""
+    return (npairs + 63) // 64 + min(slots, npairs)
 
 
 def test_quant_tokens_bit_exact():
@@ -146,6 +151,21 @@ def test_route_lists_mapped_pairs(T, topk, E, slots):
         seen.setdefault(s, []).append(first)
     for s, firsts in seen.items():
         assert sorted(firsts) == list(range(offsets[s], offsets[s + 1], 64))
+    # the wide tiles of the prefill kernels follow the tile list: up to 128
+    # pairs of one slot each, with their pair count
+    wide = tiles[1 + 2 * _tile_bound(T * topk, slots):]
+    nw = int(wide[0])
+    assert nw == int(sum((c + 127) // 128 for c in counts))
+    assert 1 + 3 * nw <= wide.size
+    seen = {}
+    for i in range(nw):
+        s, first, cnt = (int(v) for v in wide[1 + 3 * i : 4 + 3 * i])
+        assert offsets[s] <= first < offsets[s + 1]
+        assert cnt == min(128, offsets[s + 1] - first)
+        seen.setdefault(s, []).append(first)
+    assert sorted(seen) == [s for s in range(slots) if counts[s] > 0]
+    for s, firsts in seen.items():
+        assert sorted(firsts) == list(range(offsets[s], offsets[s + 1], 128))
 
 
 def _case(seed, E, H, I, T, topk, softmax=True):
@@ -161,7 +181,10 @@ def _case(seed, E, H, I, T, topk, softmax=True):
 
 @pytest.mark.parametrize(
     "E, H, I, T, topk",
-    [(8, 256, 128, 37, 4), (16, 2048, 512, 96, 8), (256, 2048, 512, 1, 8), (64, 2048, 768, 40, 8)],
+    [(8, 256, 128, 37, 4), (16, 2048, 512, 96, 8), (256, 2048, 512, 1, 8), (64, 2048, 768, 40, 8),
+     # prefill kernels over slots of ~250 pairs (four tiles, two wide tiles
+     # each), K block counts below and off the weight-row prefetch depth
+     (16, 256, 128, 1000, 4), (16, 640, 384, 1000, 4)],
 )
 @pytest.mark.parametrize("seed", [0, 1])
 def test_fused_moe_matches_oracle(E, H, I, T, topk, seed):
@@ -268,6 +291,9 @@ def test_quant_route_matches_separate_calls(T, topk, E, slots):
     assert torch.equal(r.offsets, r2.offsets)
     n = int(r.tiles[0])
     assert n == int(r2.tiles[0]) and torch.equal(r.tiles[: 1 + 2 * n], r2.tiles[: 1 + 2 * n])
+    wo = 1 + 2 * _tile_bound(T * topk, slots)
+    nw = int(r.tiles[wo])
+    assert nw == int(r2.tiles[wo]) and torch.equal(r.tiles[wo : wo + 1 + 3 * nw], r2.tiles[wo : wo + 1 + 3 * nw])
     o = r.offsets.cpu().numpy()
     for s in range(slots):
         a = np.sort(r.pairs[o[s] : o[s + 1]].cpu().numpy())

@@ -18,17 +18,20 @@
 // contribution = bf16(y * routed weight).
 //
 // Work decomposition: route lists the pairs of each slab slot in CSR form
-// and cuts them into tiles of 64 pairs of one slot. gemm1 takes one tile
-// and 128 activation columns per workgroup at prefill sizes; for few pairs
-// it takes 16 rows and 16 columns, with the K blocks split over its waves
-// (so a decode step of 8 pairs spreads over 256 workgroups). gemm2 takes
-// one tile (or 16 rows) and 128 output columns. Launch grids
-// are sized from the shapes alone (a bound on the tile count), so the
-// sequence is graph-capturable; workgroups past the live tile count exit at
-// once.
+// and cuts them into tiles of 64 pairs and wide tiles of 128 pairs of one
+// slot. At prefill sizes gemm1 and gemm2 run one persistent workgroup per
+// CU over (wide tile, 128-column block) items, so each column block of an
+// expert's weights is read once; for few pairs gemm1 takes 16 rows and 16
+// columns of a tile, with the K blocks split over its waves (so a decode
+// step of 8 pairs spreads over 256 workgroups), and gemm2 16 rows and 128
+// output columns. Launch grids are sized from the shapes alone (bounds on
+// the tile counts), so the sequence is graph-capturable; workgroups without
+// live work exit at once.
 #include <hip/hip_bf16.h>
 
+#include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -40,6 +43,7 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 64;          // pairs per tile
+constexpr int kWM = 2 * kBM;     // pairs per wide tile (the prefill GEMMs' work unit)
 constexpr int kBN = 128;         // output columns per workgroup (one quant group for GEMM1)
 constexpr int kKB = 128;         // K block = scale block = one MFMA K
 constexpr int kThreads = 256;    // 4 waves, split along N (32 columns each)
@@ -121,40 +125,45 @@ __global__ void __launch_bounds__(256) quant_tokens_kernel(const uint16_t* __res
   quant_token(x, H, xq, xs, blockIdx.x, threadIdx.x);
 }
 
-// Exclusive scan of two counters over a 1024-thread workgroup.
-__device__ __forceinline__ int2 block_scan2(int a, int b, int2* s_tot, int2* total) {
+// Exclusive scan of three counters over a 1024-thread workgroup.
+__device__ __forceinline__ int3 block_scan3(int3 v, int3* s_tot, int3* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int ia = a, ib = b;
+  int3 in = v;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int ya = __shfl_up(ia, off, 64), yb = __shfl_up(ib, off, 64);
+    const int ya = __shfl_up(in.x, off, 64), yb = __shfl_up(in.y, off, 64), yc = __shfl_up(in.z, off, 64);
     if (lane >= off) {
-      ia += ya;
-      ib += yb;
+      in.x += ya;
+      in.y += yb;
+      in.z += yc;
     }
   }
-  if (lane == 63) s_tot[wave] = make_int2(ia, ib);
+  if (lane == 63) s_tot[wave] = in;
   __syncthreads();
-  int2 base = make_int2(0, 0), all = make_int2(0, 0);
+  int3 base = make_int3(0, 0, 0), all = make_int3(0, 0, 0);
   for (int w = 0; w < kRouteThreads / 64; ++w) {
-    const int2 v = s_tot[w];
+    const int3 t = s_tot[w];
     if (w < wave) {
-      base.x += v.x;
-      base.y += v.y;
+      base.x += t.x;
+      base.y += t.y;
+      base.z += t.z;
     }
-    all.x += v.x;
-    all.y += v.y;
+    all.x += t.x;
+    all.y += t.y;
+    all.z += t.z;
   }
   *total = all;
-  return make_int2(base.x + ia - a, base.y + ib - b);
+  return make_int3(base.x + in.x - v.x, base.y + in.y - v.y, base.z + in.z - v.z);
 }
 
 // ---- routing: CSR lists of the pairs of each slab slot, and the tiles ----
 // offsets[slots + 1]; pairs[offsets[s] .. offsets[s+1]) = pair ids t*topk + k
 // of slot s; tiles[0] = live tile count, then (slot, first pair position)
-// per tile. Each wave counts a contiguous range of pairs into its own LDS
-// histogram (no contention between waves), so a slot's list is ordered by
-// wave range; dynamic LDS = 16 * slots ints.
+// per tile of kBM pairs; wide[0] = live wide-tile count, then (slot, first
+// pair position, pair count) per wide tile of kWM pairs (wide may be null).
+// Each wave counts a contiguous range of pairs into its own LDS histogram (no
+// contention between waves), so a slot's list is ordered by wave range;
+// dynamic LDS = 16 * slots ints.
 // Slots of the pairs p0, p0 + 64, ... (kRouteBatch of them; -1 for pairs
 // at or past hi, unknown experts and experts without a slot). All id loads
 // are issued before the first expert_map load, and all of those before any
@@ -178,7 +187,8 @@ __device__ __forceinline__ void route_slots(const void* ids, int eb, int64_t p0,
 __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npairs,
                                             const int32_t* __restrict__ expert_map, int E, int slots,
                                             int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
-                                            int32_t* __restrict__ tiles, int* s_hist, int2* s_tot) {
+                                            int32_t* __restrict__ tiles, int32_t* __restrict__ wide, int* s_hist,
+                                            int3* s_tot) {
   constexpr int kW = kRouteThreads / 64;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < kW * slots; i += kRouteThreads) s_hist[i] = 0;
@@ -202,9 +212,9 @@ __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npa
       c += v;
     }
   }
-  const int nt = (c + kBM - 1) / kBM;
-  int2 total;
-  const int2 off = block_scan2(c, nt, s_tot, &total);
+  const int nt = (c + kBM - 1) / kBM, nw = (c + kWM - 1) / kWM;
+  int3 total;
+  const int3 off = block_scan3(make_int3(c, nt, nw), s_tot, &total);
   if (tid < slots) {
     offsets[tid] = off.x;
     for (int w = 0; w < kW; ++w) s_hist[w * slots + tid] += off.x;  // scatter cursors
@@ -212,10 +222,17 @@ __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npa
       tiles[1 + 2 * (off.y + i)] = tid;
       tiles[2 + 2 * (off.y + i)] = off.x + i * kBM;
     }
+    if (wide)
+      for (int i = 0; i < nw; ++i) {
+        wide[1 + 3 * (off.z + i)] = tid;
+        wide[2 + 3 * (off.z + i)] = off.x + i * kWM;
+        wide[3 + 3 * (off.z + i)] = c - i * kWM < kWM ? c - i * kWM : kWM;
+      }
   }
   if (tid == 0) {
     offsets[slots] = total.x;
     tiles[0] = total.y;
+    if (wide) wide[0] = total.z;
   }
   __syncthreads();
   for (int64_t b = lo; b < hi; b += 64 * kRouteBatch) {
@@ -231,10 +248,11 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const void* ids, i
                                                               const int32_t* __restrict__ expert_map, int E,
                                                               int slots, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ pairs,
-                                                              int32_t* __restrict__ tiles) {
+                                                              int32_t* __restrict__ tiles,
+                                                              int32_t* __restrict__ wide) {
   extern __shared__ int s_hist[];  // [16 waves][slots]
-  __shared__ int2 s_tot[kRouteThreads / 64];
-  route_block(ids, eb, npairs, expert_map, E, slots, offsets, pairs, tiles, s_hist, s_tot);
+  __shared__ int3 s_tot[kRouteThreads / 64];
+  route_block(ids, eb, npairs, expert_map, E, slots, offsets, pairs, tiles, wide, s_hist, s_tot);
 }
 
 // Quantisation and routing of one MoE call in one launch: workgroup 0
@@ -246,11 +264,12 @@ __global__ void __launch_bounds__(kRouteThreads) quant_route_kernel(const uint16
                                                                     const int32_t* __restrict__ expert_map, int E,
                                                                     int slots, int32_t* __restrict__ offsets,
                                                                     int32_t* __restrict__ pairs,
-                                                                    int32_t* __restrict__ tiles) {
+                                                                    int32_t* __restrict__ tiles,
+                                                                    int32_t* __restrict__ wide) {
   extern __shared__ int s_hist[];
-  __shared__ int2 s_tot[kRouteThreads / 64];
+  __shared__ int3 s_tot[kRouteThreads / 64];
   if (blockIdx.x == 0) {
-    route_block(ids, eb, npairs, expert_map, E, slots, offsets, pairs, tiles, s_hist, s_tot);
+    route_block(ids, eb, npairs, expert_map, E, slots, offsets, pairs, tiles, wide, s_hist, s_tot);
     return;
   }
   const int64_t t = (static_cast<int64_t>(blockIdx.x) - 1) * 4 + (threadIdx.x >> 8);
@@ -280,16 +299,26 @@ __device__ __forceinline__ bool load_tile_at(int i, const int32_t* tiles, const 
   return true;
 }
 
-// Tile rows: the pair of each row (-1 for padding) and the A row it reads
-// (padding rows repeat the tile's first pair, so every load stays inside
-// the operand).
-__device__ __forceinline__ void tile_rows(const Tile& tile, const int32_t* pairs, int div, int* s_pair, int* s_row) {
-  const int tid = threadIdx.x;
-  if (tid < kBM) {
-    const int p = pairs[tile.first + (tid < tile.count ? tid : 0)];
-    s_pair[tid] = tid < tile.count ? p : -1;
-    s_row[tid] = p / div;
-  }
+// Prefill-sized calls multiply wide tiles (up to kWM pairs of one slot), so
+// that each column block of an expert's weights is read by one workgroup.
+// route writes their list after the tile list (wide_list_offset).
+
+// Bounds on the tile and wide-tile counts of npairs pairs over `slots`
+// slots (each slot's last tile may be partial).
+__host__ __device__ inline int64_t tile_bound(int64_t npairs, int64_t slots) {
+  if (npairs <= 0 || slots <= 0) return 0;
+  return (npairs + kBM - 1) / kBM + (slots < npairs ? slots : npairs);
+}
+__host__ __device__ inline int64_t wide_bound(int64_t npairs, int64_t slots) {
+  if (npairs <= 0 || slots <= 0) return 0;
+  return (npairs + kWM - 1) / kWM + (slots < npairs ? slots : npairs);
+}
+
+// The wide-tile list inside the tiles buffer, after the tile list's
+// 1 + 2 * tile_bound ints: [0] = count, then (slot, first pair position,
+// pair count) per wide tile.
+__host__ __device__ inline int64_t wide_list_offset(int64_t npairs, int64_t slots) {
+  return 1 + 2 * tile_bound(npairs, slots);
 }
 
 // Workspace of xp_moe_experts: bf16 activations, their per-16-column
@@ -322,30 +351,44 @@ constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I
 
 constexpr int kAPitch = 144;  // LDS bytes per staged A row (128 + 16 against bank conflicts)
 
-// The A rows of a tile for one K block, staged through registers into LDS
-// by all NT threads of the workgroup (16 bytes per thread per piece), so
-// the global loads of the next block are in flight while this one is used.
-template <int NT>
-struct AStage {
-  static constexpr int kPer = kBM * 8 / NT;  // 16-byte pieces per thread
-  const uint8_t* src[kPer];
+// The A rows of a wide tile, D K blocks in flight: each of the NT threads
+// loads 16-byte pieces into registers, stored to LDS one block before use.
+// Row offsets (32-bit, from one base) are kept for two items, the current
+// and the next, so the last blocks' loads can run ahead into the next item.
+template <int NT, int D>
+struct ARing {
+  static constexpr int kPer = kWM * 8 / NT;  // 16-byte pieces per thread
+  uint32_t off[2][kPer];
   int dst[kPer];
-  u32x4 v[kPer];
-  __device__ __forceinline__ void init(const uint8_t* A, int64_t lda, const int* s_row) {
+  u32x4 v[D][kPer];
+  __device__ __forceinline__ ARing() {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = static_cast<int>(threadIdx.x) + NT * i, row = c >> 3, off = (c & 7) * 16;
-      src[i] = A + static_cast<int64_t>(s_row[row]) * lda + off;
-      dst[i] = row * kAPitch + off;
+      const int c = static_cast<int>(threadIdx.x) + NT * i;
+      dst[i] = (c >> 3) * kAPitch + (c & 7) * 16;
+      off[0][i] = off[1][i] = 0;
     }
   }
-  __device__ __forceinline__ void load(int kb) {
+  // Offsets of row set `set` from the rows s_row[kWM] (A rows of lda bytes).
+  // The set is selected, not indexed: a run-time index would put the
+  // offsets in scratch memory.
+  __device__ __forceinline__ void init(int set, int64_t lda, const int* s_row) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) v[i] = *reinterpret_cast<const u32x4*>(src[i] + kb * kKB);
+    for (int i = 0; i < kPer; ++i) {
+      const int c = static_cast<int>(threadIdx.x) + NT * i;
+      const uint32_t o = static_cast<uint32_t>(s_row[c >> 3] * lda + (c & 7) * 16);
+      off[0][i] = set ? off[0][i] : o;
+      off[1][i] = set ? o : off[1][i];
+    }
   }
-  __device__ __forceinline__ void store(uint8_t* s_a) const {
+  __device__ __forceinline__ void load(int stage, const uint8_t* A, int set, int kb) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) *reinterpret_cast<u32x4*>(s_a + dst[i]) = v[i];
+    for (int i = 0; i < kPer; ++i)
+      v[stage][i] = *reinterpret_cast<const u32x4*>(A + (set ? off[1][i] : off[0][i]) + kb * kKB);
+  }
+  __device__ __forceinline__ void store(int stage, uint8_t* s_a) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) *reinterpret_cast<u32x4*>(s_a + dst[i]) = v[stage][i];
   }
 };
 
@@ -355,169 +398,349 @@ __device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4
   a[1] = p[1];
 }
 
-// GEMM1: gate and up for NW*16 = 128 activation columns of one tile (1-D
-// grid in XCD order, see xcd_item); each wave owns 16 columns and runs the K
-// blocks in order, so a column's value does not depend on the workgroup
-// width. The tile's A rows are staged in LDS, double-buffered, one block
-// ahead. Then a = bf16(silu(bf16 gate) * bf16 up) is quantised to fp8 per
-// row over the workgroup's 128 columns, one scale group. Only the 16-row
-// subtiles that hold pairs are multiplied.
+// ---- prefill GEMMs: persistent workgroups over wide tiles ----
+//
+// A work item is (wide tile, column block). The items of XCD x belong to the
+// wide tiles x, x + 8, x + 16, ..., a tile's column blocks consecutive;
+// workgroup b runs on XCD b % 8 and takes that XCD's items l, l + nl,
+// l + 2 nl, ... (l = b / 8, nl = gridDim.x / 8), so a tile's column blocks
+// run side by side on one XCD and its token rows are read into one L2.
+//
+// A workgroup streams its items' operands without a break: the next item's
+// rows and scales are looked up during the current item's first K blocks,
+// and its first kPD blocks of weights and A rows are requested during the
+// current item's last blocks, so the epilogue and the next item's set-up
+// overlap the operand stream. Each wave keeps kPD K blocks in flight.
+constexpr int kPD = 2;
+
+template <int N>
+using Int = std::integral_constant<int, N>;
+
+// Calls f(Int<n>{}) for the tile's subtile count n in 1..kWM/16: the K loop
+// is compiled once per count, without branches and with no more
+// accumulators than it needs.
+template <int N, typename F>
+__device__ __forceinline__ void with_subtiles_from(int nmi, F&& f) {
+  if constexpr (N >= kWM / 16) {
+    f(Int<kWM / 16>{});
+  } else {
+    if (nmi <= N)
+      f(Int<N>{});
+    else
+      with_subtiles_from<N + 1>(nmi, f);
+  }
+}
+
+template <typename F>
+__device__ __forceinline__ void with_subtiles(int nmi, F&& f) {
+  with_subtiles_from<1>(nmi, f);
+}
+
+struct Item {
+  int slot, first, count, col;  // count 0: no item
+};
+
+// Candidate n of this workgroup: item j = l + n * nl of its XCD, i.e. wide
+// tile (j / ncols) * 8 + xcd and column block j % ncols.
+__device__ __forceinline__ void item_index(int n, int ncols, int& w, int& col) {
+  const int jj = (static_cast<int>(blockIdx.x) >> 3) + n * (static_cast<int>(gridDim.x) >> 3);
+  w = (jj / ncols) * 8 + (static_cast<int>(blockIdx.x) & 7);
+  col = jj - (jj / ncols) * ncols;
+}
+
+// Lanes 0..3 of each wave load the list's live count and candidate n's
+// (slot, first, count): vector loads, which complete in order with the
+// operand loads; item_get reads them once landed.
+__device__ __forceinline__ int item_request(int n, int ncols, const int32_t* __restrict__ wide, int64_t wmax) {
+  int w, col;
+  item_index(n, ncols, w, col);
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  if (lane == 0) return wide[0];
+  if (lane < 4 && w < wmax) return wide[1 + 3 * static_cast<int64_t>(w) + (lane - 1)];
+  return 0;
+}
+
+__device__ __forceinline__ Item item_get(int m, int n, int ncols) {
+  int w, col;
+  item_index(n, ncols, w, col);
+  Item it;
+  const int live = __builtin_amdgcn_readlane(m, 0);
+  it.slot = __builtin_amdgcn_readlane(m, 1);
+  it.first = __builtin_amdgcn_readlane(m, 2);
+  it.count = w < live ? __builtin_amdgcn_readlane(m, 3) : 0;
+  it.col = col;
+  return it;
+}
+
+// The pair of row tid of an item (padding rows repeat its first pair), and
+// its LDS copy with the operand row it reads (pair / div).
+__device__ __forceinline__ int item_pair(const Item& it, const int32_t* __restrict__ pairs) {
+  const int tid = threadIdx.x;
+  return tid < kWM ? pairs[it.first + (tid < it.count ? tid : 0)] : 0;
+}
+
+__device__ __forceinline__ void put_rows(const Item& it, int p, int div, int* s_pair, int* s_row) {
+  const int tid = threadIdx.x;
+  if (tid < kWM) {
+    s_pair[tid] = tid < it.count ? p : -1;
+    s_row[tid] = p / div;
+  }
+}
+
+// K blocks an item's loop runs: KB rounded up to kPD, and at least 2 kPD,
+// so that the next item is looked up before its first blocks are requested.
+__host__ __device__ inline int padded_blocks(int KB) {
+  const int r = (KB + kPD - 1) / kPD * kPD;
+  return r > 2 * kPD ? r : 2 * kPD;
+}
+
+// Per-row scales of an item, [K block][row], are loaded 4 floats per
+// thread per K loop step (kScaleStep of them per chunk).
+template <int NT>
+struct ScaleChunk {
+  static constexpr int kFloats = 4 * NT;
+  float v[4];
+  // Chunk c of the scales src[row * KB + kb] of rows s_row.
+  __device__ __forceinline__ void load(const float* __restrict__ src, int KB, const int* s_row, int c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = c * kFloats + i * NT + static_cast<int>(threadIdx.x);
+      const int kb = e / kWM, r = e - kb * kWM;
+      v[i] = kb < KB ? src[static_cast<int64_t>(s_row[r]) * KB + kb] : 0.f;
+    }
+  }
+  __device__ __forceinline__ void store(float* dst, int KB, int c) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = c * kFloats + i * NT + static_cast<int>(threadIdx.x);
+      if (e < KB * kWM) dst[e] = v[i];
+    }
+  }
+};
+
+// GEMM1 at prefill sizes: gate and up for NW*16 = 128 activation columns of
+// a wide tile per item; each wave owns 16 columns and runs the K blocks in
+// order, so a column's value does not depend on the workgroup width or the
+// tile height. The tile's A rows are staged in LDS one block ahead (double
+// buffered). Then a = bf16(silu(bf16 gate) * bf16 up) is quantised to fp8
+// per row over the workgroup's 128 columns, one scale group. Only the 16-row
+// subtiles that hold pairs are multiplied. Dynamic LDS: the token scales of
+// two items, 2 x (H / 128) x kWM floats.
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
                                                         int64_t H, int64_t I, int topk,
                                                         const uint8_t* __restrict__ w13,
                                                         const float* __restrict__ w13_scale,
-                                                        const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ pairs,
-                                                        const int32_t* __restrict__ tiles, Work work) {
+                                                        const int32_t* __restrict__ wide, int64_t wmax, Work work) {
   constexpr int NT = NW * 64, NC = NW * 16;
-  __shared__ int s_row[kBM];
-  __shared__ int s_pair[kBM];
-  __shared__ float s_xs[kBM * kMaxKB];  // token scales per row and K block
-  __shared__ float s_sw[2][kMaxKB];     // gate and up weight scales per K block
-  __shared__ float s_m[NW][kBM];        // row maxima per wave (16 columns)
-  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kBM * kAPitch];  // A stages; then the bf16 staging
+  static_assert(NC == kKB, "a workgroup covers one 128-column scale group of the activations");
+  extern __shared__ __attribute__((aligned(16))) float s_xs[];  // [2 items][K block][row] token scales
+  __shared__ int s_row[2][kWM];
+  __shared__ int s_pair[2][kWM];
+  __shared__ float s_sw[2][2][kMaxKB];  // gate and up weight scales per K block, two items
+  __shared__ float s_m[NW][kWM];        // row maxima per wave (16 columns)
+  __shared__ float s_q[kWM];            // row scales of the activations
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kWM * kAPitch];  // A stages
+  __shared__ __attribute__((aligned(16))) uint16_t s_a16[kWM * kKB];      // bf16 activations of an item
 
-  Tile tile;
-  int ti, cb;
-  xcd_item(static_cast<int>(I / NC), ti, cb);
-  if (!load_tile_at(ti, tiles, offsets, tile)) return;
-  const int c0 = cb * NC;
+  const int ncols = static_cast<int>(I / NC);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
-  const int KB = static_cast<int>(H / kKB);
-  const int nmi = (tile.count + 15) >> 4;
+  const int KB = static_cast<int>(H / kKB), KBP = padded_blocks(KB);
+  const int nchunks = (KB * kWM + ScaleChunk<NT>::kFloats - 1) / ScaleChunk<NT>::kFloats;
+  const int64_t ksz = static_cast<int64_t>(KB) * kWM;
 
-  tile_rows(tile, pairs, topk, s_pair, s_row);
-  __syncthreads();
-  for (int i = tid; i < 16 * nmi * KB; i += NT) {
-    const int r = i / KB, kb = i - r * KB;
-    s_xs[i] = xs[static_cast<int64_t>(s_row[r]) * KB + kb];
-  }
-  {
-    // The workgroup's gate and up rows each lie in one 128-row scale block.
-    const float* sg = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + c0 / kKB) * KB;
-    const float* su = w13_scale + (static_cast<int64_t>(tile.slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
-    for (int i = tid; i < 2 * KB; i += NT) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
-  }
-  AStage<NT> st0, st1;  // token rows of two K blocks in flight
-  st0.init(xq, H, s_row);
-  st1.init(xq, H, s_row);
+  Item cur = item_get(item_request(0, ncols, wide, wmax), 0, ncols);
+  if (cur.count == 0) return;
+  Item nxt = item_get(item_request(1, ncols, wide, wmax), 1, ncols);
+  int n = 2;
 
-  const uint8_t* wslot = w13 + static_cast<int64_t>(tile.slot) * 2 * I * H;
-  const int64_t n = c0 + 16 * wave + j;
-  const uint8_t* brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
-
-  f32x4 acc[4][2];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 b0[2][2], b1[2][2];
-  auto load_b = [&](u32x4 (&b)[2][2], int kb) {
-#pragma unroll
-    for (int si = 0; si < 2; ++si) load32(brow[si] + kb * kKB, b[si]);
+  // Weight rows: the item's gate rows start at wbase, its up rows I rows
+  // later; this lane reads row 16 * wave + j of each at byte 32q.
+  const int64_t boff = static_cast<int64_t>(16 * wave + j) * H + 32 * q;
+  auto wbase = [&](const Item& it) {
+    return w13 + (static_cast<int64_t>(it.slot) * 2 * I + static_cast<int64_t>(it.col) * NC) * H + boff;
   };
-  auto compute = [&](const uint8_t* sa_buf, const u32x4 (&b)[2][2], int kb) {
-    const float g = s_sw[0][kb], u = s_sw[1][kb];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      if (mi >= nmi) continue;
-      u32x4 a[2];
-      read_a(sa_buf, 16 * mi + j, q, a);
-      // One combined scale per output row and K block (token scale x weight
-      // scale), so each MFMA output needs a single FMA.
-      float sc[2][4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float sa = s_xs[(16 * mi + 4 * q + r) * KB + kb];
-        sc[0][r] = sa * g;
-        sc[1][r] = sa * u;
-      }
-#pragma unroll
-      for (int si = 0; si < 2; ++si) {
-        const f32x4 part = mfma_k128(a, b[si]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][si][r] = fmaf(part[r], sc[si][r], acc[mi][si][r]);
-      }
-    }
+  auto load_b = [&](u32x4 (&bb)[2][2], const uint8_t* base, int kb) {
+    load32(base + kb * kKB, bb[0]);
+    load32(base + I * H + kb * kKB, bb[1]);
+  };
+  // The workgroup's gate and up rows each lie in one 128-row scale block.
+  auto weight_scale = [&](const Item& it, int i) {
+    const int64_t blk = static_cast<int64_t>(it.slot) * (2 * I / kKB) + (i < KB ? 0 : I / kKB) + it.col;
+    return w13_scale[blk * KB + (i < KB ? i : i - KB)];
   };
 
-  // Token rows are loaded two K blocks ahead of their multiply and stored to
-  // LDS one block ahead; weight rows one block ahead. Block indices are
-  // clamped at the last block, so the loads are unconditional.
-  auto clampk = [&](int k) { return k < KB ? k : KB - 1; };
-  __syncthreads();  // s_row, s_xs, s_sw
-  st0.load(0);
-  st1.load(clampk(1));
-  load_b(b0, 0);
-  st0.store(s_a[0]);
-  __syncthreads();
-  for (int kb = 0; kb < KB; kb += 2) {
-    st0.load(clampk(kb + 2));
-    load_b(b1, clampk(kb + 1));
-    compute(s_a[0], b0, kb);
-    st1.store(s_a[1]);
+  u32x4 b[kPD][2][2];
+  ARing<NT, kPD> ar;
+  {
+    // First item: weights first (they depend on the slot alone), then its
+    // rows, scales and A rows.
+    const uint8_t* wb = wbase(cur);
+#pragma unroll
+    for (int d = 0; d < kPD; ++d) load_b(b[d], wb, d < KB ? d : KB - 1);
+    put_rows(cur, item_pair(cur, pairs), topk, s_pair[0], s_row[0]);
     __syncthreads();
-    st1.load(clampk(kb + 3));
-    load_b(b0, clampk(kb + 2));
-    if (kb + 1 < KB) compute(s_a[1], b1, kb + 1);
-    st0.store(s_a[0]);
+    for (int c = 0; c < nchunks; ++c) {
+      ScaleChunk<NT> sc;
+      sc.load(xs, KB, s_row[0], c);
+      sc.store(s_xs, KB, c);
+    }
+    if (tid < 2 * KB) s_sw[0][tid / KB][tid % KB] = weight_scale(cur, tid);
+    ar.init(0, H, s_row[0]);
+#pragma unroll
+    for (int d = 0; d < kPD; ++d) ar.load(d, xq, 0, d < KB ? d : KB - 1);
+    __syncthreads();
+    ar.store(0, s_a[0]);
     __syncthreads();
   }
 
-  static_assert(NC == kKB, "a workgroup covers one 128-column scale group of the activations");
-  {
-    // 128 columns: one whole scale group of the activations, so they are
-    // quantised here (s = max(max |a|, 1e-10) / 448, q = rne(clamp(a / s)),
-    // the rule gemm2_narrow_kernel applies, on the same bf16 values).
-    float av[4][4];
+  int cb = 0;  // LDS buffer and A row set of the current item
+  for (;;) {
+    const int nb = cb ^ 1;
+    const bool more = nxt.count > 0;
+    const uint8_t* wb_cur = wbase(cur);
+    const uint8_t* wb_nxt = more ? wbase(nxt) : wb_cur;
+    const int nmi = (cur.count + 15) >> 4;
+    const int c0 = cur.col * NC;
+    const float* xs_cur = s_xs + cb * ksz;
+    int pn = 0, m2 = 0;
+    float swn = 0.f;
+    ScaleChunk<NT> scn;
+
+    with_subtiles(nmi, [&](auto nmi_c) {
+      constexpr int MI = decltype(nmi_c)::value;
+      f32x4 acc[MI][2];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      if (mi >= nmi) continue;
+      for (int mi = 0; mi < MI; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      auto compute = [&](const uint8_t* sa_buf, const u32x4 (&bb)[2][2], int kb) {
+        const float g = s_sw[cb][0][kb], u = s_sw[cb][1][kb];
+        // Subtile mi + 1's A rows and token scales are read from LDS while
+        // subtile mi multiplies; the scheduling barrier keeps the compiler
+        // from hoisting more subtiles' operands (registers are the limit).
+        u32x4 a[2][2];
+        f32x4 sa[2];
+        auto fetch = [&](int mi, int slot) {
+          read_a(sa_buf, 16 * mi + j, q, a[slot]);
+          sa[slot] = *reinterpret_cast<const f32x4*>(xs_cur + kb * kWM + 16 * mi + 4 * q);
+        };
+        fetch(0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float g = bf16_round(acc[mi][0][r]), u = bf16_round(acc[mi][1][r]);
-        const float a = bf16_round(g / (1.0f + expf(-g)) * u);
-        av[mi][r] = a;
-        float m = fabsf(a);
+        for (int mi = 0; mi < MI; ++mi) {
+          const int c = mi & 1;
+          if (mi + 1 < MI) fetch(mi + 1, c ^ 1);
+          const f32x4 part0 = mfma_k128(a[c], bb[0]), part1 = mfma_k128(a[c], bb[1]);
+          // One combined scale per output row and K block (token scale x
+          // weight scale), so each MFMA output needs a single FMA.
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
-        if (j == 0) s_m[wave][16 * mi + 4 * q + r] = m;
+          for (int r = 0; r < 4; ++r) {
+            acc[mi][0][r] = fmaf(part0[r], sa[c][r] * g, acc[mi][0][r]);
+            acc[mi][1][r] = fmaf(part1[r], sa[c][r] * u, acc[mi][1][r]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+
+      for (int kb = 0; kb < KBP; kb += kPD) {
+#pragma unroll
+        for (int d = 0; d < kPD; ++d) {
+          const int k = kb + d;
+          // The next item: its pairs and metadata of the one after (step 0),
+          // its rows (1), its A row offsets and weight scales (2, 3) and its
+          // token scales (2 ..).
+          if (more) {
+            if (k == 0) {
+              pn = item_pair(nxt, pairs);
+              m2 = item_request(n, ncols, wide, wmax);
+            } else if (k == 1) {
+              put_rows(nxt, pn, topk, s_pair[nb], s_row[nb]);
+            } else {
+              if (k == 2) {
+                ar.init(nb, H, s_row[nb]);
+                swn = tid < 2 * KB ? weight_scale(nxt, tid) : 0.f;
+              } else if (k == 3 && tid < 2 * KB) {
+                s_sw[nb][tid / KB][tid % KB] = swn;
+              }
+              if (k - 3 >= 0 && k - 3 < nchunks) scn.store(s_xs + nb * ksz, KB, k - 3);
+              if (k - 2 < nchunks) scn.load(xs, KB, s_row[nb], k - 2);
+            }
+          }
+          // Block k + kPD of this item, or block k + kPD - KBP of the next,
+          // goes to stage d of both rings.
+          const int blk = k + kPD;
+          const bool own = blk < KBP || !more;
+          const int kr = own ? (blk < KB ? blk : KB - 1) : blk - KBP;
+          ar.load(d, xq, own ? cb : nb, kr);
+          if (k < KB) compute(s_a[k & 1], b[d], k);
+          load_b(b[d], own ? wb_cur : wb_nxt, kr);
+          ar.store((d + 1) % kPD, s_a[(k + 1) & 1]);
+          __syncthreads();
+        }
       }
-    }
-    __syncthreads();
-    float* s_q = s_m[0];  // row scales, written over wave 0's maxima after all are read
-    float qs = 0.f;
-    if (tid < kBM) {
-      float m = s_m[0][tid];
+
+      // 128 columns: one whole scale group of the activations, so they are
+      // quantised here (s = max(max |a|, 1e-10) / 448, q = rne(clamp(a / s)),
+      // the rule gemm2_narrow_kernel applies, on the same bf16 values). The
+      // bf16 values go through LDS one subtile at a time, so the
+      // accumulators die as they are converted (the operand rings still hold
+      // the next item's first blocks).
 #pragma unroll
-      for (int w = 1; w < NW; ++w) m = fmaxf(m, s_m[w][tid]);
-      qs = quant_scale(m);
-    }
-    __syncthreads();
-    if (tid < kBM) {
-      s_q[tid] = qs;
-      const int p = s_pair[tid];
-      if (p >= 0) work.acts[static_cast<int64_t>(p) * (I / kKB) + c0 / kKB] = qs;
-    }
-    __syncthreads();
-    uint8_t* s_act = s_a[0];  // [kBM][128] fp8
+      for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      if (mi >= nmi) continue;
+        for (int r = 0; r < 4; ++r) {
+          const float g = bf16_round(acc[mi][0][r]), u = bf16_round(acc[mi][1][r]);
+          const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+          const int row = 16 * mi + 4 * q + r;
+          s_a16[row * kKB + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(a));
+          float m = fabsf(a);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * mi + 4 * q + r;
-        s_act[row * kKB + 16 * wave + j] = static_cast<uint8_t>(to_fp8(clamp_fp8(av[mi][r] / s_q[row])));
+          for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+          if (j == 0) s_m[wave][row] = m;
+        }
       }
-    }
-    __syncthreads();
-    for (int i = tid; i < kBM * (kKB / 16); i += NT) {  // 16-byte pieces
-      const int row = i / (kKB / 16), piece = i - row * (kKB / 16);
-      const int p = s_pair[row];
-      if (p >= 0)
-        *reinterpret_cast<u32x4*>(work.act + static_cast<int64_t>(p) * I + c0 + piece * 16) =
-            *reinterpret_cast<const u32x4*>(s_act + row * kKB + piece * 16);
-    }
+      __syncthreads();
+      if (tid < 16 * MI) {
+        float m = s_m[0][tid];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) m = fmaxf(m, s_m[w][tid]);
+        const float qs = quant_scale(m);
+        s_q[tid] = qs;
+        const int p = s_pair[cb][tid];
+        if (p >= 0) work.acts[static_cast<int64_t>(p) * (I / kKB) + c0 / kKB] = qs;
+      }
+      __syncthreads();
+      // 16 values (one 16-byte fp8 piece) per thread: 8 threads per row.
+      for (int i = tid; i < 16 * MI * (kKB / 16); i += NT) {
+        const int row = i / (kKB / 16), piece = i - row * (kKB / 16);
+        const int p = s_pair[cb][row];
+        if (p < 0) continue;
+        const float sq = s_q[row];
+        const u32x4* src = reinterpret_cast<const u32x4*>(s_a16 + row * kKB + piece * 16);
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const u32x4 v = src[h];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const uint32_t pk = v[2 * e + t];
+              word |= to_fp8(clamp_fp8(bf16_value(pk & 0xffffu) / sq)) << (16 * t);
+              word |= to_fp8(clamp_fp8(bf16_value(pk >> 16) / sq)) << (16 * t + 8);
+            }
+            o[2 * h + e] = word;
+          }
+        }
+        *reinterpret_cast<u32x4*>(work.act + static_cast<int64_t>(p) * I + c0 + piece * 16) = o;
+      }
+    });
+    if (!more) break;
+    cur = nxt;
+    nxt = item_get(m2, n, ncols);
+    ++n;
+    cb = nb;
   }
 }
 
@@ -806,119 +1029,168 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   }
 }
 
-// GEMM2: down projection of 128 output columns times the routed weight,
-// bf16 rows per pair; each wave owns 32 columns and runs the K blocks in
-// order over the tile's fp8 activations, staged in LDS one block ahead.
-// 1-D grid in XCD order (see xcd_item).
-__global__ void __launch_bounds__(kThreads) gemm2_kernel(int64_t H, int64_t I, const float* __restrict__ topk_weight,
-                                                         const uint8_t* __restrict__ w2,
-                                                         const float* __restrict__ w2_scale,
-                                                         const int32_t* __restrict__ offsets,
-                                                         const int32_t* __restrict__ pairs,
-                                                         const int32_t* __restrict__ tiles, Work work,
-                                                         uint16_t* __restrict__ out) {
-  __shared__ int s_row[kBM];
-  __shared__ int s_pair[kBM];
-  __shared__ float s_as[kBM * kMaxKB];
-  __shared__ float s_w[kBM];
-  __shared__ float s_sw[kMaxKB];  // weight scales per K block of this 128-column block
-  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kBM * kAPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t s_o[kBM * kBN];
+// GEMM2 at prefill sizes: down projection of 128 output columns of a wide
+// tile per item, times the routed weight, bf16 rows per pair. Each of the 8
+// waves owns 16 columns and runs the K blocks in order over the tile's fp8
+// activations, staged in LDS one block ahead; persistent over items as
+// gemm1_kernel. Dynamic LDS: the activation scales of two items,
+// 2 x (I / 128) x kWM floats.
+constexpr int kWideNW2 = 8;
 
-  Tile tile;
-  int ti, cb;
-  xcd_item(static_cast<int>(H / kBN), ti, cb);
-  if (!load_tile_at(ti, tiles, offsets, tile)) return;
-  const int n0 = cb * kBN;
+__global__ void __launch_bounds__(kWideNW2 * 64) gemm2_kernel(int64_t H, int64_t I,
+                                                              const float* __restrict__ topk_weight,
+                                                              const uint8_t* __restrict__ w2,
+                                                              const float* __restrict__ w2_scale,
+                                                              const int32_t* __restrict__ pairs,
+                                                              const int32_t* __restrict__ wide, int64_t wmax,
+                                                              Work work, uint16_t* __restrict__ out) {
+  constexpr int NT = kWideNW2 * 64;
+  static_assert(kWideNW2 * 16 == kBN, "the waves cover one 128-column block");
+  extern __shared__ __attribute__((aligned(16))) float s_as[];  // [2 items][K block][row] activation scales
+  __shared__ int s_row[2][kWM];
+  __shared__ int s_pair[2][kWM];
+  __shared__ float s_w[2][kWM];
+  __shared__ float s_sw[2][kMaxKB];  // weight scales per K block of the item's 128-column block
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kWM * kAPitch];  // A stages
+  __shared__ __attribute__((aligned(16))) uint16_t s_o[kWM * kBN];        // output rows of an item
+
+  const int ncols = static_cast<int>(H / kBN);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
-  const int KB = static_cast<int>(I / kKB);
-  const int nmi = (tile.count + 15) >> 4;
+  const int KB = static_cast<int>(I / kKB), KBP = padded_blocks(KB);
+  const int nchunks = (KB * kWM + ScaleChunk<NT>::kFloats - 1) / ScaleChunk<NT>::kFloats;
+  const int64_t ksz = static_cast<int64_t>(KB) * kWM;
 
-  tile_rows(tile, pairs, 1, s_pair, s_row);
-  __syncthreads();
-  for (int i = tid; i < 16 * nmi * KB; i += kThreads) {
-    const int r = i / KB, kb = i - r * KB;
-    s_as[i] = work.acts[static_cast<int64_t>(s_row[r]) * KB + kb];
-  }
-  if (tid < kBM) s_w[tid] = s_pair[tid] >= 0 ? topk_weight[s_pair[tid]] : 0.f;
-  if (tid < KB) s_sw[tid] = w2_scale[(static_cast<int64_t>(tile.slot) * (H / kKB) + n0 / kKB) * KB + tid];
-  AStage<kThreads> st0, st1;  // activation rows of two K blocks in flight
-  st0.init(work.act, I, s_row);
-  st1.init(work.act, I, s_row);
+  Item cur = item_get(item_request(0, ncols, wide, wmax), 0, ncols);
+  if (cur.count == 0) return;
+  Item nxt = item_get(item_request(1, ncols, wide, wmax), 1, ncols);
+  int n = 2;
 
-  const uint8_t* wslot = w2 + static_cast<int64_t>(tile.slot) * H * I;
-  const uint8_t* brow[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) brow[t] = wslot + static_cast<int64_t>(n0 + 32 * wave + 16 * t + j) * I + 32 * q;
-
-  f32x4 acc[4][2];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 b0[2][2], b1[2][2];
-  auto load_b = [&](u32x4 (&b)[2][2], int kb) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) load32(brow[t] + kb * kKB, b[t]);
+  const int64_t boff = static_cast<int64_t>(16 * wave + j) * I + 32 * q;
+  auto wbase = [&](const Item& it) {
+    return w2 + (static_cast<int64_t>(it.slot) * H + static_cast<int64_t>(it.col) * kBN) * I + boff;
   };
-  auto compute = [&](const uint8_t* sa_buf, const u32x4 (&b)[2][2], int kb) {
-    const float w = s_sw[kb];
+  auto weight_scale = [&](const Item& it, int kb) {
+    return w2_scale[(static_cast<int64_t>(it.slot) * (H / kKB) + it.col) * KB + kb];
+  };
+
+  u32x4 b[kPD][2];
+  ARing<NT, kPD> ar;
+  {
+    const uint8_t* wb = wbase(cur);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      if (mi >= nmi) continue;
-      u32x4 a[2];
-      read_a(sa_buf, 16 * mi + j, q, a);
-      float sc[4];
+    for (int d = 0; d < kPD; ++d) load32(wb + (d < KB ? d : KB - 1) * kKB, b[d]);
+    put_rows(cur, item_pair(cur, pairs), 1, s_pair[0], s_row[0]);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+      ScaleChunk<NT> sc;
+      sc.load(work.acts, KB, s_row[0], c);
+      sc.store(s_as, KB, c);
+    }
+    if (tid < kWM) s_w[0][tid] = s_pair[0][tid] >= 0 ? topk_weight[s_pair[0][tid]] : 0.f;
+    if (tid < KB) s_sw[0][tid] = weight_scale(cur, tid);
+    ar.init(0, I, s_row[0]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = s_as[(16 * mi + 4 * q + r) * KB + kb] * w;
+    for (int d = 0; d < kPD; ++d) ar.load(d, work.act, 0, d < KB ? d : KB - 1);
+    __syncthreads();
+    ar.store(0, s_a[0]);
+    __syncthreads();
+  }
+
+  int cb = 0;
+  for (;;) {
+    const int nb = cb ^ 1;
+    const bool more = nxt.count > 0;
+    const uint8_t* wb_cur = wbase(cur);
+    const uint8_t* wb_nxt = more ? wbase(nxt) : wb_cur;
+    const int nmi = (cur.count + 15) >> 4;
+    const int n0 = cur.col * kBN;
+    const float* as_cur = s_as + cb * ksz;
+    int pn = 0, m2 = 0;
+    float swn = 0.f, wn = 0.f;
+    ScaleChunk<NT> scn;
+
+    with_subtiles(nmi, [&](auto nmi_c) {
+      constexpr int MI = decltype(nmi_c)::value;
+      f32x4 acc[MI];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const f32x4 part = mfma_k128(a, b[t]);
+      for (int mi = 0; mi < MI; ++mi) acc[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+      auto compute = [&](const uint8_t* sa_buf, const u32x4 (&bb)[2], int kb) {
+        const float w = s_sw[cb][kb];
+        u32x4 a[2][2];  // operands of subtiles mi and mi + 1, as in gemm1_kernel
+        f32x4 sa[2];
+        auto fetch = [&](int mi, int slot) {
+          read_a(sa_buf, 16 * mi + j, q, a[slot]);
+          sa[slot] = *reinterpret_cast<const f32x4*>(as_cur + kb * kWM + 16 * mi + 4 * q);
+        };
+        fetch(0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mi][t][r] = fmaf(part[r], sc[r], acc[mi][t][r]);
+        for (int mi = 0; mi < MI; ++mi) {
+          const int c = mi & 1;
+          if (mi + 1 < MI) fetch(mi + 1, c ^ 1);
+          const f32x4 part = mfma_k128(a[c], bb);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(part[r], sa[c][r] * w, acc[mi][r]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+
+      for (int kb = 0; kb < KBP; kb += kPD) {
+#pragma unroll
+        for (int d = 0; d < kPD; ++d) {
+          const int k = kb + d;
+          if (more) {
+            if (k == 0) {
+              pn = item_pair(nxt, pairs);
+              m2 = item_request(n, ncols, wide, wmax);
+            } else if (k == 1) {
+              put_rows(nxt, pn, 1, s_pair[nb], s_row[nb]);
+            } else {
+              if (k == 2) {
+                ar.init(nb, I, s_row[nb]);
+                swn = tid < KB ? weight_scale(nxt, tid) : 0.f;
+                wn = tid < kWM && s_pair[nb][tid] >= 0 ? topk_weight[s_pair[nb][tid]] : 0.f;
+              } else if (k == 3) {
+                if (tid < KB) s_sw[nb][tid] = swn;
+                if (tid < kWM) s_w[nb][tid] = wn;
+              }
+              if (k - 3 >= 0 && k - 3 < nchunks) scn.store(s_as + nb * ksz, KB, k - 3);
+              if (k - 2 < nchunks) scn.load(work.acts, KB, s_row[nb], k - 2);
+            }
+          }
+          const int blk = k + kPD;
+          const bool own = blk < KBP || !more;
+          const int kr = own ? (blk < KB ? blk : KB - 1) : blk - KBP;
+          ar.load(d, work.act, own ? cb : nb, kr);
+          if (k < KB) compute(s_a[k & 1], b[d], k);
+          load32((own ? wb_cur : wb_nxt) + kr * kKB, b[d]);
+          ar.store((d + 1) % kPD, s_a[(k + 1) & 1]);
+          __syncthreads();
+        }
       }
-    }
-  };
-
-  // As in gemm1_kernel: activation rows two K blocks ahead, weights one.
-  auto clampk = [&](int k) { return k < KB ? k : KB - 1; };
-  __syncthreads();  // s_row, s_as, s_w, s_sw
-  st0.load(0);
-  st1.load(clampk(1));
-  load_b(b0, 0);
-  st0.store(s_a[0]);
-  __syncthreads();
-  for (int kb = 0; kb < KB; kb += 2) {
-    st0.load(clampk(kb + 2));
-    load_b(b1, clampk(kb + 1));
-    compute(s_a[0], b0, kb);
-    st1.store(s_a[1]);
-    __syncthreads();
-    st1.load(clampk(kb + 3));
-    load_b(b0, clampk(kb + 2));
-    if (kb + 1 < KB) compute(s_a[1], b1, kb + 1);
-    st0.store(s_a[0]);
-    __syncthreads();
-  }
 
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    if (mi >= nmi) continue;
+      for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mi + 4 * q + r;
-      const float wgt = s_w[row];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        s_o[row * kBN + 32 * wave + 16 * t + j] = static_cast<uint16_t>(bf16_bits(acc[mi][t][r] * wgt));
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mi + 4 * q + r;
+          s_o[row * kBN + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(acc[mi][r] * s_w[cb][row]));
+        }
+      }
+    });
+    __syncthreads();
+    // 256 bytes per row: 16 threads x 16 bytes, 32 rows per pass.
+    for (int row = tid >> 4; row < cur.count; row += NT / 16) {
+      const int p = s_pair[cb][row];
+      const int col = (tid & 15) * 8;
+      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
+          *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
     }
-  }
-  __syncthreads();
-  // 256 bytes per row: 16 threads x 16 bytes, 16 rows per pass.
-  for (int row = tid >> 4; row < tile.count; row += kThreads / 16) {
-    const int p = s_pair[row];
-    const int col = (tid & 15) * 8;
-    *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
-        *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
+    if (!more) break;
+    cur = nxt;
+    nxt = item_get(m2, n, ncols);
+    ++n;
+    cb = nb;
   }
 }
 
@@ -970,7 +1242,9 @@ extern "C" {
 
 int64_t xp_moe_max_tiles(int64_t npairs, int64_t slots) {
   if (npairs <= 0 || slots <= 0) return 0;
-  return (npairs + kBM - 1) / kBM + (slots < npairs ? slots : npairs);
+  // The tile list, then the wide-tile list (1 + 3 * wide_bound ints), in
+  // two-int entries past tiles[0].
+  return tile_bound(npairs, slots) + (2 + 3 * wide_bound(npairs, slots)) / 2;
 }
 
 int xp_quant_tokens(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq, float* xs, void* stream) {
@@ -994,9 +1268,10 @@ int xp_moe_route(const void* topk_ids, int topk_elem_bytes, int64_t T, int64_t t
   XP_REQUIRE(num_experts >= 1 && num_experts <= INT32_MAX, "xp_moe_route: %lld experts", (long long)num_experts);
   XP_REQUIRE(expert_map && offsets && pairs && tiles && (T == 0 || topk_ids), "xp_moe_route: null argument");
   const size_t lds = static_cast<size_t>(kRouteThreads / 64) * static_cast<size_t>(slots) * sizeof(int);
+  int32_t* wide = T * topk > 0 ? tiles + wide_list_offset(T * topk, slots) : nullptr;
   hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), lds, as_stream(stream), topk_ids, topk_elem_bytes,
                      T * topk, expert_map, static_cast<int>(num_experts), static_cast<int>(slots), offsets, pairs,
-                     tiles);
+                     tiles, wide);
   return check_launch("route_kernel");
 }
 
@@ -1017,9 +1292,10 @@ int xp_moe_quant_route(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq, flo
              "xp_moe_quant_route: null or misaligned buffer");
   const size_t lds = static_cast<size_t>(kRouteThreads / 64) * static_cast<size_t>(slots) * sizeof(int);
   const unsigned grid = static_cast<unsigned>(1 + (T + 3) / 4);
+  int32_t* wide = T * topk > 0 ? tiles + wide_list_offset(T * topk, slots) : nullptr;
   hipLaunchKernelGGL(quant_route_kernel, dim3(grid), dim3(kRouteThreads), lds, as_stream(stream), x, T, H, xq, xs,
                      topk_ids, topk_elem_bytes, T * topk, expert_map, static_cast<int>(num_experts),
-                     static_cast<int>(slots), offsets, pairs, tiles);
+                     static_cast<int>(slots), offsets, pairs, tiles, wide);
   return check_launch("quant_route_kernel");
 }
 
@@ -1049,8 +1325,26 @@ int check_experts(const char* what, const uint8_t* xq, const float* xs, int64_t 
              "%s: null argument", what);
   XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(out),
              "%s: fp8 and output buffers must be 16-byte aligned", what);
-  const int64_t bound = xp_moe_max_tiles(T * topk, slots);
+  const int64_t bound = tile_bound(T * topk, slots);
   XP_REQUIRE(bound <= 65535, "%s: %lld tiles exceed the launch grid", what, (long long)bound);
+  return XP_OK;
+}
+
+// Compute units per XCD of the current device (8 XCDs), looked up once per
+// device.
+int cus_per_xcd(int* out) {
+  static std::mutex mu;
+  static int cache[64];
+  int dev = -1;
+  XP_HIP(hipGetDevice(&dev));
+  XP_REQUIRE(dev >= 0 && dev < 64, "device %d (at most 64 devices)", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] == 0) {
+    int n = 0;
+    XP_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    cache[dev] = n / 8 > 0 ? n / 8 : 1;
+  }
+  *out = cache[dev];
   return XP_OK;
 }
 
@@ -1061,41 +1355,53 @@ int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
                    int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, uint8_t* work,
                    uint16_t* out, void* stream) {
   const int64_t npairs = T * topk;
-  const int64_t bound = xp_moe_max_tiles(npairs, slots);
+  const int64_t bound = tile_bound(npairs, slots);
   Work w;
   work_layout(npairs, I, &w, work);
+  // Prefill-sized calls run persistent workgroups over wide tiles, 128
+  // activation (gemm1) or output (gemm2) columns per item, and quantise the
+  // activations in gemm1; small calls take 16-row subtiles (more workgroups
+  // for few pairs) and the small-batch gemm2 quantises. Every column is
+  // computed the same way in both.
+  const bool narrow = bound < kWideTiles;
+  int rc = XP_OK;
+  if (!narrow) {
+    XP_REQUIRE(T * H <= UINT32_MAX && npairs * I <= UINT32_MAX,
+               "xp_moe_experts: T*H=%lld and T*topk*I=%lld must stay below 2^32 (call over fewer tokens)",
+               (long long)(T * H), (long long)(npairs * I));
+    int per_xcd = 0;
+    rc = cus_per_xcd(&per_xcd);
+    if (rc) return rc;
+    const int64_t wmax = wide_bound(npairs, slots);
+    const int32_t* wide = tiles + wide_list_offset(npairs, slots);
+    const int64_t per_xcd_tiles = (wmax + 7) / 8;  // wide tiles of one XCD, at most
+    // One workgroup per CU: their registers allow no more.
+    const int64_t n1 = std::min<int64_t>(per_xcd, per_xcd_tiles * (I / (16 * kWideNW)));
+    const int64_t n2 = std::min<int64_t>(per_xcd, per_xcd_tiles * (H / kBN));
+    hipLaunchKernelGGL(gemm1_kernel<kWideNW>, dim3(static_cast<unsigned>(8 * n1)), dim3(64 * kWideNW),
+                       static_cast<size_t>(2 * kWM * (H / kKB)) * sizeof(float), as_stream(stream), xq, xs, H, I,
+                       static_cast<int>(topk), w13, w13_scale, pairs, wide, wmax, w);
+    rc = check_launch("gemm1_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(8 * n2)), dim3(64 * kWideNW2),
+                       static_cast<size_t>(2 * kWM * (I / kKB)) * sizeof(float), as_stream(stream), H, I, topk_weight,
+                       w2, w2_scale, pairs, wide, wmax, w, out);
+    return check_launch("gemm2_kernel");
+  }
   const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
   const int64_t g2 = tiles8 * (H / kBN);
-  XP_REQUIRE(g2 <= INT32_MAX, "xp_moe_experts: grid too large");
-  // Prefill-sized calls take 16*kWideNW = 128 activation columns of a tile
-  // per workgroup (token rows shared by more waves) and quantise them there;
-  // small calls take 16 rows x 16 columns (more workgroups for few pairs)
-  // and the small-batch gemm2 quantises. Every column is computed the same
-  // way in both.
-  const bool narrow = bound < kWideTiles;
   // 16-row subtiles a tile can have: a tile holds at most min(64, npairs) pairs.
   const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
-  if (!narrow) {
-    const int64_t g1w = tiles8 * (I / (16 * kWideNW));
-    hipLaunchKernelGGL(gemm1_kernel<kWideNW>, dim3(static_cast<unsigned>(g1w)), dim3(64 * kWideNW), 0,
-                       as_stream(stream), xq, xs,
-                       H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, w);
-  } else {
-    // Few pairs: 16-row subtiles x 16 columns, the K blocks split over 4 waves.
-    const int64_t g1n = tiles8 * nsub * (I / 16);
-    XP_REQUIRE(g1n <= INT32_MAX, "xp_moe_experts: grid too large");
-    hipLaunchKernelGGL(gemm1_narrow_kernel, dim3(static_cast<unsigned>(g1n)), dim3(kThreads), 0, as_stream(stream), xq,
-                       xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, nsub, w);
-  }
-  int rc = check_launch("gemm1_kernel");
+  // Few pairs: 16-row subtiles x 16 columns, the K blocks split over 4 waves.
+  const int64_t g1n = tiles8 * nsub * (I / 16);
+  XP_REQUIRE(g1n <= INT32_MAX && nsub * g2 <= INT32_MAX, "xp_moe_experts: grid too large");
+  hipLaunchKernelGGL(gemm1_narrow_kernel, dim3(static_cast<unsigned>(g1n)), dim3(kThreads), 0, as_stream(stream), xq,
+                     xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, nsub, w);
+  rc = check_launch("gemm1_narrow_kernel");
   if (rc) return rc;
-  if (narrow)
-    hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(nsub * g2)), dim3(kThreads), 0,
-                       as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, nsub, w, out);
-  else
-    hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(g2)), dim3(kThreads), 0, as_stream(stream), H, I,
-                       topk_weight, w2, w2_scale, offsets, pairs, tiles, w, out);
-  return check_launch("gemm2_kernel");
+  hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(nsub * g2)), dim3(kThreads), 0,
+                     as_stream(stream), H, I, topk_weight, w2, w2_scale, offsets, pairs, tiles, nsub, w, out);
+  return check_launch("gemm2_narrow_kernel");
 }
 
 }  // namespace
