@@ -15,8 +15,10 @@ decoder on a bounded sample as the CPU baseline.
 
 import argparse
 import concurrent.futures as cf
+import ctypes
 import json
 import os
+import shutil
 import sys
 import time
 
@@ -683,12 +685,12 @@ def build_paged_model(dev, settings, keep_weights: bool = False):
     return pager, layers, weights
 
 
-def decode_trace(args, dev, pager, layers, label: str) -> dict:
+def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None) -> dict:
     """Run the Zipf(1.1)/0.7-reuse decode trace through a captured 40-layer step; tok/s, hit rates,
     and the paging path alone per layer."""
     c = QWEN
     L, E, H, k = c["layers"], c["experts"], c["hidden"], c["topk"]
-    steps, warm = args.decode_steps, args.decode_warmup
+    steps, warm = steps or args.decode_steps, args.decode_warmup
     store = pager.store
     rng = np.random.default_rng(2025)
     trace = torch.from_numpy(zipf_trace(rng, warm + steps, L, E, k, 1.1, 0.7)).to(dev)
@@ -784,25 +786,72 @@ def bench_model_decode(args, dev):
         pager.close()
 
 
-def bench_tiered(args, dev):
+def disk_ceiling(path: str, record_bytes: int, records: int, seconds: float = 0.5) -> dict:
+    """Record-sized O_DIRECT reads of the paging file at 1, 8 and 32 in flight, from a thread pool
+    (the SSD server's way) and from io_uring: the disk's ceiling in this run."""
+    from vllm_expert_pager import _native
+
+    lib = _native.lib()
+    fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+    out = {"record_bytes": record_bytes}
+    rng = np.random.default_rng(11)
+    runs = {}
+    try:
+        # Two passes in different orders; each configuration keeps its better pass (a disk that
+        # has just been written can serve some reads from its own cache).
+        for order in ((8, 32, 1), (1, 32, 8)):
+            for mode, name in ((0, "threads"), (1, "io_uring")):
+                for depth in order:
+                    # about `seconds` of reads at 3 GB/s, at least 4 per reader
+                    count = max(4 * depth, int(3e9 * seconds / record_bytes))
+                    idx = rng.choice(records, size=count, replace=count > records)
+                    offs = (ctypes.c_int64 * count)(*(int(i) * record_bytes for i in idx))
+                    sec = ctypes.c_double()
+                    rc = lib.xp_ssd_read_probe(fd, record_bytes, offs, count, depth, mode, ctypes.byref(sec))
+                    key = (name, str(depth))
+                    if rc:
+                        runs.setdefault(key, []).append(f"failed: {lib.xp_last_error().decode(errors='replace')}")
+                    else:
+                        runs.setdefault(key, []).append(round(count * record_bytes / sec.value / 1e9, 3))
+    finally:
+        os.close(fd)
+    for (name, depth), vals in runs.items():
+        nums = [v for v in vals if isinstance(v, float)]
+        out.setdefault(f"{name}_gbps", {})[depth] = max(nums) if nums else vals[-1]
+        out.setdefault(f"{name}_passes", {})[depth] = vals
+    log(f"disk ceiling: {out}")
+    return out
+
+
+def bench_tiered(args, dev, decode_steps: int | None = None):
     """The compressed tier: 40 layers x 256 experts, 32 cache slots, 128 RAM slots holding rows
     compressed at pitch 0.89, the rest in a paging file read with O_DIRECT by the host server.
 
-    Prefill: one 2048-token prompt (hidden states bf16 N(0,1), top-8 of random logits, softmax
-    weights), every layer through the 64-row working slab in chunks; each layer's output is
-    checked bit for bit against a one-shot run over all its experts. Then the decode trace."""
+    The disk's ceiling for record reads is measured first on the same file. Prefill: one
+    2048-token prompt (hidden states bf16 N(0,1), top-8 of random logits, softmax weights), every
+    layer through the 64-row working slab in chunks; each layer's output is checked bit for bit
+    against a one-shot run over all its experts. Then the decode trace."""
     from vllm_expert_pager import moe
     from vllm_expert_pager import pager as pg
 
     c = QWEN
     L, E, H, k = c["layers"], c["experts"], c["hidden"], c["topk"]
     T = args.prefill_tokens
+    need = L * E * (1_867_776 + 933_888)  # records at pitch 0.89
+    try:
+        free = shutil.disk_usage(args.paging_dir).free
+    except OSError as e:
+        return {"skipped": f"paging directory {args.paging_dir}: {e}"}
+    if free < need + (4 << 30):
+        return {"skipped": f"the paging file needs {need / 2**30:.1f} GiB and {args.paging_dir} has "
+                           f"{free / 2**30:.1f} GiB free (4 GiB kept spare)"}
     path = os.path.join(args.paging_dir, f"xp_paging_{os.getpid()}.bin")
     settings = pg.Settings(cache_slots=32, ram_slots=128, ssd_path=path, compress="on", pitch_ratio=0.89,
                            working_rows=64, log_interval=0)
     pager, layers, weights = build_paged_model(dev, settings, keep_weights=True)
     store = pager.store
     try:
+        ceiling = disk_ceiling(path, store.record_bytes, L * E)
         g = torch.Generator(device=dev).manual_seed(77)
         xs, ws, ids = [], [], []
         for l in range(L):
@@ -841,12 +890,24 @@ def bench_tiered(args, dev):
         if exact != L:
             raise SystemExit("chunked prefill differs from the one-shot run")
         del xs, ws, ids, outs, weights
+        steps = decode_steps or args.decode_steps
         decode = decode_trace(args, dev, pager, layers,
                               "40-layer decode trace, 256 experts x 3 MiB, 32 cache slots, 128 RAM slots of "
                               "rows compressed at pitch 0.89, the rest read from the paging file (O_DIRECT), "
-                              f"batch 1, top-8, Zipf(1.1) with 0.7 reuse, {args.decode_steps} steps in one "
-                              "captured hipGraph per step")
-        return {"prefill": prefill, "decode": decode}
+                              f"batch 1, top-8, Zipf(1.1) with 0.7 reuse, {steps} steps in one "
+                              "captured hipGraph per step", steps=steps)
+        # The server's read rate while it has requests (reads x record / time serving them),
+        # against the ceiling at its own depth (the server thread and 7 workers: 8 in flight).
+        rb = store.record_bytes
+        top = ceiling.get("threads_gbps", {}).get("8")
+        for leg, reads, io in (("prefill", prefill["ssd_reads"], prefill["ssd_io_seconds"]),
+                               ("decode", (decode.get("ssd") or {}).get("reads", 0),
+                                (decode.get("ssd") or {}).get("io_seconds", 0.0))):
+            rate = reads * rb / io / 1e9 if io > 0 else None
+            tgt = prefill if leg == "prefill" else decode
+            tgt["ssd_gbps_while_reading"] = round(rate, 3) if rate else None
+            tgt["ssd_frac_of_disk_ceiling_8"] = round(rate / top, 3) if rate and isinstance(top, float) else None
+        return {"disk_ceiling": ceiling, "prefill": prefill, "decode": decode}
     finally:
         pager.close()
         if os.path.exists(path):
@@ -868,8 +929,12 @@ def main() -> None:
     ap.add_argument("--only-model", action="store_true")
     ap.add_argument("--only-encode", action="store_true")
     ap.add_argument("--tiered", action="store_true",
-                    help="run only the compressed-tier legs (2048-token prefill, decode trace; needs ~30 GB "
-                         "of disk for the paging file)")
+                    help="run only the compressed-tier legs (disk ceiling, 2048-token prefill, decode trace; "
+                         "needs ~30 GB of disk for the paging file)")
+    ap.add_argument("--no-tiered", action="store_true",
+                    help="leave the compressed-tier legs out of the default run")
+    ap.add_argument("--tiered-decode-steps", type=int, default=300,
+                    help="decode steps of the compressed tier in the default run")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--paging-dir", default=os.environ.get("TMPDIR", "/tmp"))
     ap.add_argument("--decode-steps", type=int, default=2000)
@@ -921,6 +986,8 @@ def main() -> None:
         extras["acquire"] = bench_acquire(args, dev)
         extras["moe"] = bench_moe(args, dev)
         extras["model_decode"] = bench_model_decode(args, dev)
+        if not args.no_tiered:
+            extras["tiered"] = bench_tiered(args, dev, args.tiered_decode_steps)
     line = {
         "metric": "Huffman decode GB/s (% HBM peak); gather GB/s; acquire us/layer; decode tok/s",
         "value": round(dec["gbps"], 2),

@@ -382,6 +382,20 @@ int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk,
                     int64_t H, const void* topk_ids, int topk_elem_bytes,
                     int64_t num_experts, uint16_t* out, void* stream);
 
+/* ---- measurement ---- */
+
+/* Reads `count` records of record_bytes (a multiple of 4096) at the given
+ * 4096-aligned offsets of fd (opened with O_DIRECT) into host buffers of the
+ * library's own, `depth` (1..256) reads in flight: from `depth` threads
+ * issuing pread, the way the SSD server's reader pool does (use_uring 0),
+ * or from one io_uring queue of `depth` entries (use_uring 1). Writes the
+ * elapsed seconds. Host only; no counterpart in the reference: it measures
+ * the disk's ceiling for the paging file's record reads beside the server's
+ * own rate. */
+int xp_ssd_read_probe(int fd, int64_t record_bytes, const int64_t* offsets,
+                      int64_t count, int depth, int use_uring,
+                      double* seconds);
+
 #ifdef __cplusplus
 }
 #endif

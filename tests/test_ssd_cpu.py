@@ -192,3 +192,30 @@ def test_start_rejects_bad_arguments(tmp_path):
     ptrs = (ctypes.c_void_p * 5)()
     pitch = (ctypes.c_long * 5)()
     assert not lib.ssd_start(0, req.ctypes.data, done.ctypes.data, RING, BLOCK, 1, 1, 1, 4096, 5, ptrs, pitch, 1)
+
+
+@pytest.mark.parametrize("use_uring", [0, 1], ids=["threads", "io_uring"])
+@pytest.mark.parametrize("depth", [1, 3, 8])
+def test_read_probe_reads_every_record(tmp_path, use_uring, depth):
+    """The disk probe reads whole records with O_DIRECT at any depth, through
+    the thread pool and through io_uring, and refuses misaligned offsets."""
+    lib = _lib()
+    rec = 3 * 4096
+    path = tmp_path / "records.bin"
+    path.write_bytes(bytes(range(256)) * (rec * 12 // 256))
+    fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+    try:
+        offs = (ctypes.c_int64 * 10)(*[rec * i for i in (3, 0, 11, 5, 5, 7, 1, 9, 2, 10)])
+        sec = ctypes.c_double(-1.0)
+        rc = lib.xp_ssd_read_probe(fd, rec, offs, 10, depth, use_uring, ctypes.byref(sec))
+        if rc and use_uring and b"io_uring" in (lib.xp_last_error() or b""):
+            pytest.skip(f"io_uring unavailable here: {lib.xp_last_error().decode()}")
+        assert rc == 0, lib.xp_last_error()
+        assert sec.value >= 0.0
+        bad = (ctypes.c_int64 * 1)(100)
+        assert lib.xp_ssd_read_probe(fd, rec, bad, 1, depth, use_uring, ctypes.byref(sec)) != 0
+        assert b"aligned" in lib.xp_last_error()
+        past = (ctypes.c_int64 * 1)(rec * 40)  # beyond the end: a short read is an error
+        assert lib.xp_ssd_read_probe(fd, rec, past, 1, depth, use_uring, ctypes.byref(sec)) != 0
+    finally:
+        os.close(fd)

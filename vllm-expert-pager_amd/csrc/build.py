@@ -41,7 +41,7 @@ HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "encode.hip", "moe.hip"]
 HIP_HOST_SOURCES = ["host.cpp", "codec_host.cpp"]  # HIP runtime API or headers
-HOST_SOURCES = ["error.cpp", "ssd.cpp"]
+HOST_SOURCES = ["error.cpp", "ssd.cpp", "ssd_probe.cpp"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:
@@ -103,7 +103,7 @@ def build_host_sanitized(kind: str, out_dir: str, verbose: bool = False) -> str:
              "thread": ["-fsanitize=thread"]}[kind]
     os.makedirs(out_dir, exist_ok=True)
     out = os.path.join(out_dir, "libxp.so")
-    srcs = [os.path.join(HERE, s) for s in ("error.cpp", "codec_host.cpp", "ssd.cpp")]
+    srcs = [os.path.join(HERE, s) for s in ("error.cpp", "codec_host.cpp", "ssd.cpp", "ssd_probe.cpp")]
     # code_build.h marks its functions __host__ __device__: the HIP headers
     # define those away for a host compiler.
     _run(["g++", "-O1", "-g", "-fno-omit-frame-pointer", "-std=c++17", "-fPIC", "-shared", "-pthread", *flags,
