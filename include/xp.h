@@ -375,6 +375,25 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T,
                            const int32_t* offsets, const int32_t* pairs,
                            const int32_t* tiles, uint16_t* out, void* stream);
 
+/* A decode step's expert FFN in two launches, for at most 64 pairs
+ * (T * topk), H <= 4096 and topk * I <= 32768: out[T][H] gets the bits of
+ * xp_moe_quant_route + xp_moe_experts + xp_moe_topk_sum, but the routing and
+ * quantisation run inside the gate/up launch and each token's top-k sum
+ * inside the down-projection launch (one workgroup per token and 16
+ * columns). Replaces, like those calls, fused_experts + moe_sum of a step
+ * whose experts are all in the slab (experts.py:579-604): every pair with a
+ * valid id should have a slot (one without adds nothing here). work is
+ * xp_moe_workspace_bytes(T * topk, I) bytes, 256-byte aligned. Fails with
+ * XP_E_LIMIT (launching nothing) above those sizes. */
+int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H,
+                          const void* topk_ids, int topk_elem_bytes,
+                          int64_t topk, const float* topk_weight,
+                          const int32_t* expert_map, int64_t num_experts,
+                          int64_t I, const uint8_t* w13,
+                          const float* w13_scale, const uint8_t* w2,
+                          const float* w2_scale, int64_t slots, void* work,
+                          int64_t work_bytes, uint16_t* out, void* stream);
+
 /* The single top-k combine (moe_sum after collect, experts.py:546-552):
  * out[t][H] = bf16(sum over k ascending of fp32(contrib[t*topk + k])),
  * skipping pairs whose id is outside [0, num_experts). */

@@ -299,3 +299,95 @@ def test_quant_route_matches_separate_calls(T, topk, E, slots):
         a = np.sort(r.pairs[o[s] : o[s + 1]].cpu().numpy())
         b = np.sort(r2.pairs[o[s] : o[s + 1]].cpu().numpy())
         assert np.array_equal(a, b)
+
+
+def _separate(moe, xb, tw_t, ids_t, emap, E, slots, w):
+    xq, xs, r = moe.quant_route(xb, ids_t, emap, slots)
+    contrib = torch.zeros((ids_t.numel(), xb.shape[1]), dtype=torch.bfloat16, device="cuda")
+    moe.run_experts(xq, xs, tw_t, *w, r, contrib)
+    return moe.topk_sum(contrib, ids_t, E)
+
+
+@pytest.mark.parametrize(
+    "T, topk, E, slots, H, I, idbits",
+    [(1, 8, 256, 32, 2048, 512, 64), (5, 8, 64, 64, 2048, 512, 32), (8, 8, 256, 200, 2048, 512, 64),
+     (3, 4, 12, 12, 256, 128, 32), (16, 4, 32, 32, 640, 1024, 64),
+     # more than 16 tokens: each workgroup quantises its own subtile's rows
+     (32, 2, 40, 40, 384, 256, 64)],
+)
+def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits):
+    """The two-launch decode FFN (routing and quantisation inside gate/up, each
+    token's top-k sum inside the down projection) gives the bits of
+    quant_route + run_experts + topk_sum, with invalid ids skipped as topk_sum
+    skips them; I = 1024 takes activation scales past the first four K blocks."""
+    moe = _moe()
+    rng = np.random.default_rng(T * 100 + E)
+    x, tw, ids, w13, w13s, w2, w2s = _case(T * 31 + E, E, H, I, T, topk)
+    if T > 2:
+        ids[1, 0] = -1
+        ids[2, topk - 1] = E + 3
+    ids = ids.astype(np.int64 if idbits == 64 else np.int32)
+    xb = _bf16(x)
+    tw_t, ids_t = _dev(tw, ids)
+    # a slab of `slots` rows holding the step's experts (every valid id mapped)
+    used = np.unique(ids[(ids >= 0) & (ids < E)])
+    assert used.size <= slots
+    order = np.concatenate([used, np.setdiff1d(np.arange(E), used)])[:slots]
+    emap = np.full(E, -1, np.int32)
+    emap[order] = rng.permutation(slots)
+    slab = [np.empty((slots, *a.shape[1:]), a.dtype) for a in (w13, w13s, w2, w2s)]
+    for dst, src in zip(slab, (w13, w13s, w2, w2s)):
+        dst[emap[order]] = src[order]
+    w = _dev(*slab)
+    emap_t = _dev(emap)[0]
+    want = _separate(moe, xb, tw_t, ids_t, emap_t, E, slots, w)
+    assert moe.decode_fits(xb, ids_t, I)
+    for _ in range(2):
+        got = moe.decode_experts(xb, tw_t, ids_t, emap_t, E, *w, slots)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_decode_experts_in_a_graph():
+    """Captured once, replayed with new inputs: every replay equals the separate calls."""
+    moe = _moe()
+    T, topk, E, slots, H, I = 1, 8, 64, 16, 2048, 512
+    x, tw, ids, w13, w13s, w2, w2s = _case(5, E, H, I, T, topk)
+    emap = np.full(E, -1, np.int32)
+    emap[:slots] = np.arange(slots)
+    w = _dev(w13[:slots], w13s[:slots], w2[:slots], w2s[:slots])
+    emap_t = _dev(emap)[0]
+    xs_t = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    tw_t = torch.empty((T, topk), dtype=torch.float32, device="cuda")
+    ids_t = torch.empty((T, topk), dtype=torch.int64, device="cuda")
+    rng = np.random.default_rng(9)
+
+    def fill():
+        xs_t.copy_(_bf16(rng.standard_normal((T, H)).astype(np.float32)))
+        tw_t.copy_(torch.from_numpy(rng.random((T, topk)).astype(np.float32)))
+        ids_t.copy_(torch.from_numpy(np.stack([rng.permutation(slots)[:topk] for _ in range(T)])))
+
+    fill()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        moe.decode_experts(xs_t, tw_t, ids_t, emap_t, E, *w, slots)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = moe.decode_experts(xs_t, tw_t, ids_t, emap_t, E, *w, slots)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(4):
+        fill()
+        g.replay()
+        torch.cuda.synchronize()
+        want = _separate(moe, xs_t, tw_t, ids_t, emap_t, E, slots, w)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+def test_decode_experts_limits():
+    moe = _moe()
+    x = torch.zeros((9, 2048), dtype=torch.bfloat16, device="cuda")
+    ids = torch.zeros((9, 8), dtype=torch.int64, device="cuda")
+    assert not moe.decode_fits(x, ids, 512)  # 72 pairs
+    assert moe.decode_fits(x[:8], ids[:8], 512)
+    assert not moe.decode_fits(x[:1], ids[:1], 8192)  # topk * I above 32 KiB
+    assert not moe.decode_fits(torch.zeros((1, 8192), dtype=torch.bfloat16, device="cuda"), ids[:1], 512)

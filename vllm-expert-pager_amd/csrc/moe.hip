@@ -909,6 +909,357 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
   }
 }
 
+// ---- decode steps: two launches for the expert FFN ----
+//
+// For at most kDecodePairs pairs, every gemm1 workgroup routes the pairs
+// itself (wave 0, one pair per lane) and quantises the token rows of its
+// subtile into LDS, so no routing or quantisation launch precedes it. gemm2
+// then takes one token and 16 output columns per workgroup, computes each of
+// the token's pairs and sums them there, so no top-k sum launch follows. The
+// bits are those of xp_moe_quant_route, xp_moe_experts and xp_moe_topk_sum.
+constexpr int kDecodePairs = 64;
+constexpr int kDecodeMaxH = 4096;       // 16 quantised token rows of H bytes fit in LDS
+constexpr int kDecodeActBytes = 32768;  // a token's quantised activations (topk x I) in LDS
+
+// Pair p's routing, the lists route_kernel writes (pairs by slot, then by
+// pair index; one tile per occupied slot, since a slot holds at most 64 of
+// these pairs): its slot (-1: not routed), its position in the pair list,
+// its slot's tile index, and whether it is its slot's first pair.
+struct DecodeRoute {
+  int slot, pos, tile;
+  bool first;
+};
+
+__device__ __forceinline__ DecodeRoute decode_route(int p, int n, const void* ids, int eb,
+                                                    const int32_t* __restrict__ expert_map, int E, int slots) {
+  int slot = -1;
+  if (p < n) {
+    const int64_t e = load_id(ids, eb, p);
+    if (e >= 0 && e < E) {
+      const int sl = expert_map[e];
+      slot = sl >= 0 && sl < slots ? sl : -1;
+    }
+  }
+  int before = 0;
+  bool first = slot >= 0;
+  for (int q = 0; q < n; ++q) {
+    const int sq = __shfl(slot, q, 64);
+    if (slot < 0 || sq < 0) continue;
+    if (sq < slot || (sq == slot && q < p)) ++before;
+    if (sq == slot && q < p) first = false;
+  }
+  int tile = 0;
+  for (int q = 0; q < n; ++q) {
+    const int sq = __shfl(slot, q, 64);
+    const bool fq = __shfl(static_cast<int>(first), q, 64) != 0;
+    if (fq && sq < slot) ++tile;
+  }
+  return DecodeRoute{slot, before, tile, first};
+}
+
+// gemm1_narrow_kernel over a decode step's pairs, with their routing and the
+// quantisation of their token rows done here. Dynamic LDS: 16 x H fp8 rows.
+__global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
+    const uint16_t* __restrict__ x, int64_t H, int64_t I, const void* ids, int eb, int npairs, int topk,
+    const int32_t* __restrict__ expert_map, int E, int slots, const uint8_t* __restrict__ w13,
+    const float* __restrict__ w13_scale, int nsub, Work work) {
+  constexpr int kPerWave = kSplitRound / (kThreads / 64);
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_aq[];  // [16][H] fp8 token rows
+  __shared__ int s_slot[kDecodePairs], s_pos[kDecodePairs], s_tile[kDecodePairs], s_first[kDecodePairs];
+  __shared__ int s_pairat[kDecodePairs];  // pair at each list position
+  __shared__ int s_ntiles;
+  __shared__ int s_pair[16];
+  __shared__ int s_arow[16];            // LDS row of each subtile row's activations
+  __shared__ float s_xs[16 * kMaxKB];   // their scales [LDS row][K block]
+  __shared__ float s_sw[2][kMaxKB];
+  __shared__ float s_m[16];
+  __shared__ f32x4 s_part[kSplitRound][2][64];
+  __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * 16];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const int KB = static_cast<int>(H / kKB);
+
+  // Token rows quantised as quant_tokens_kernel does (16 lanes per
+  // 128-column group, 8 values per lane) into LDS row r, by `nthreads`
+  // threads from thread `t0` (whole waves).
+  auto quant_row = [&](int r, int64_t t, int t0, int nthreads) {
+    const uint16_t* row = x + t * H;
+    for (int64_t c8 = (tid - t0) * 8; c8 < H; c8 += nthreads * 8) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(row + c8);
+      float v[8];
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = bf16_value(raw[i] & 0xffffu);
+        v[2 * i + 1] = bf16_value(raw[i] >> 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+      const float sc = quant_scale(amax);
+      uint32_t q0 = 0, q1 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q0 |= to_fp8(clamp_fp8(v[i] / sc)) << (8 * i);
+        q1 |= to_fp8(clamp_fp8(v[4 + i] / sc)) << (8 * i);
+      }
+      *reinterpret_cast<uint2*>(s_aq + r * H + c8) = make_uint2(q0, q1);
+      if ((tid & 15) == 0) s_xs[r * KB + c8 / kKB] = sc;
+    }
+  };
+  // With at most 16 tokens, all their rows are quantised (by waves 1-3)
+  // while wave 0 routes; otherwise each workgroup quantises its subtile's.
+  const int ntok = npairs / topk;
+  const bool by_token = ntok <= 16;
+  if (wave == 0) {
+    const DecodeRoute r = decode_route(lane, npairs, ids, eb, expert_map, E, slots);
+    s_slot[lane] = r.slot;
+    s_pos[lane] = r.pos;
+    s_tile[lane] = r.tile;
+    s_first[lane] = r.first;
+    if (r.slot >= 0) s_pairat[r.pos] = lane;
+    const int nt = __popcll(__ballot(r.first));
+    if (lane == 0) s_ntiles = nt;
+  } else if (by_token) {
+    for (int t = 0; t < ntok; ++t) quant_row(t, t, 64, kThreads - 64);
+  }
+  __syncthreads();
+
+  const int ncb = static_cast<int>(I / 16);
+  int ti, item;
+  xcd_item(nsub * ncb, ti, item);
+  if (ti >= s_ntiles) return;
+  int slot = -1, first = 0, count = 0;
+  for (int p = 0; p < npairs; ++p) {
+    if (s_first[p] && s_tile[p] == ti) {
+      slot = s_slot[p];
+      first = s_pos[p];
+    }
+  }
+  for (int p = 0; p < npairs; ++p) count += s_slot[p] == slot;
+  const int sub = item / ncb, r0 = 16 * sub;
+  if (r0 >= count) return;
+  const int c0 = (item - sub * ncb) * 16;
+  const int nrow = count - r0 < 16 ? count - r0 : 16;
+
+  // The first round's weight rows depend on the slot alone.
+  const uint8_t* wslot = w13 + static_cast<int64_t>(slot) * 2 * I * H;
+  const int64_t n = c0 + j;
+  const uint8_t* const brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
+  const int kw0 = wave * kPerWave;
+  KBlock c[kPerWave];
+  load_chunk_b<kPerWave>(c, brow, kw0, KB);
+
+  if (tid < 16) s_pair[tid] = tid < nrow ? s_pairat[first + r0 + tid] : -1;
+  {
+    const float* sg = w13_scale + (static_cast<int64_t>(slot) * (2 * I / kKB) + c0 / kKB) * KB;
+    const float* su = w13_scale + (static_cast<int64_t>(slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
+    for (int i = tid; i < 2 * KB; i += kThreads) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
+  }
+  __syncthreads();  // s_pair
+  if (!by_token)
+    for (int r = 0; r < nrow; ++r) quant_row(r, s_pair[r] / topk, 0, kThreads);
+  // The LDS row each subtile row reads (rows past nrow, whose outputs are
+  // not stored, read the first row's).
+  if (tid < 16) {
+    const int rr = tid < nrow ? tid : 0;
+    s_arow[tid] = by_token ? s_pair[rr] / topk : rr;
+  }
+  __syncthreads();  // s_aq, s_xs, s_arow, s_pair, s_sw
+
+  const uint8_t* arow = s_aq + s_arow[j] * H + 32 * q;
+  auto load_a = [&](int kb0) {
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int kb = kb0 + i < KB ? kb0 + i : KB - 1;
+      c[i].a[0] = *reinterpret_cast<const u32x4*>(arow + kb * kKB);
+      c[i].a[1] = *reinterpret_cast<const u32x4*>(arow + kb * kKB + 16);
+    }
+  };
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // wave 0's sums
+  for (int k0 = 0; k0 < KB; k0 += kSplitRound) {
+    const int kw = k0 + kw0;
+    if (k0 > 0) load_chunk_b<kPerWave>(c, brow, kw, KB);
+    load_a(kw);
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      if (kw + i >= KB) continue;
+      s_part[wave * kPerWave + i][0][lane] = mfma_k128(c[i].a, c[i].b[0]);
+      s_part[wave * kPerWave + i][1][lane] = mfma_k128(c[i].a, c[i].b[1]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int nk = KB - k0 < kSplitRound ? KB - k0 : kSplitRound;
+      for (int t = 0; t < nk; ++t) {
+        const int kb = k0 + t;
+        const float g = s_sw[0][kb], u = s_sw[1][kb];
+        const f32x4 pg = s_part[t][0][lane], pu = s_part[t][1][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sa = s_xs[s_arow[4 * q + r] * KB + kb];
+          acc[0][r] = fmaf(pg[r], sa * g, acc[0][r]);
+          acc[1][r] = fmaf(pu[r], sa * u, acc[1][r]);
+        }
+      }
+    }
+    __syncthreads();  // s_part is rewritten by the next round
+  }
+
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
+      const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+      float m = fabsf(a);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      const int row = 4 * q + r;
+      if (j == 0) s_m[row] = m;
+      s_o[row * 16 + j] = static_cast<uint16_t>(bf16_bits(a));
+    }
+  }
+  __syncthreads();
+  if (tid < 16) {
+    const int p = s_pair[tid];
+    if (p >= 0) work.amax16[static_cast<int64_t>(p) * (I / 16) + c0 / 16] = s_m[tid];
+  } else if (tid < 48) {  // 16 rows x 2 pieces of 16 bytes
+    const int row = (tid - 16) >> 1, piece = tid & 1;
+    const int p = s_pair[row];
+    if (p >= 0)
+      *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
+          *reinterpret_cast<const u32x4*>(s_o + row * 16 + piece * 8);
+  }
+}
+
+// gemm2 of a decode step with the top-k sum: one workgroup per (token, 16
+// output columns). Its waves take the token's pairs two at a time (wave w:
+// pairs w and w + 4, then w + 8 and w + 12, ...); each pair's 16 contributions are computed as
+// gemm2_narrow_kernel computes them (the token's quantised activation row as
+// every row of the MFMA operand, kNarrowChunk K blocks of weight rows per
+// load) and rounded to bf16; then the contributions are summed in k order
+// in fp32 and rounded once, as topk_sum_kernel does. A token's experts are
+// distinct slots, so its pairs share no weights. Pairs whose id is outside
+// [0, E) add nothing; so do pairs without a slot (the separate calls would
+// read a contribution never written).
+__global__ void __launch_bounds__(kThreads) gemm2_decode_kernel(
+    int64_t H, int64_t I, int topk, const void* ids, int eb, const int32_t* __restrict__ expert_map, int E,
+    int slots, const float* __restrict__ topk_weight, const uint8_t* __restrict__ w2,
+    const float* __restrict__ w2_scale, Work work, uint16_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];  // [topk][I] fp8 activations
+  __shared__ int s_slot[kDecodePairs];
+  __shared__ float s_as[kDecodePairs * 4];  // activation scales [pair][K block], K blocks of a round
+  __shared__ uint16_t s_c[kDecodePairs][16];
+  __shared__ int s_ok[kDecodePairs];
+
+  const int ncol = static_cast<int>(H / 16);
+  const int t = static_cast<int>(blockIdx.x) / ncol, n0 = (static_cast<int>(blockIdx.x) - t * ncol) * 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const int KB = static_cast<int>(I / kKB);
+  const int64_t p0 = static_cast<int64_t>(t) * topk;
+
+  if (tid < topk) {
+    const int64_t e = load_id(ids, eb, p0 + tid);
+    const bool valid = e >= 0 && e < E;
+    const int sl = valid ? expert_map[e] : -1;
+    s_slot[tid] = sl >= 0 && sl < slots ? sl : -1;
+    s_ok[tid] = valid;
+  }
+  // The pairs' activations quantised into LDS, 8 columns per item, as
+  // gemm2_narrow_kernel quantises them (a 128-column group's scale from its
+  // eight 16-column maxima).
+  for (int i = tid; i < topk * static_cast<int>(I / 8); i += kThreads) {
+    const int k = i / static_cast<int>(I / 8), c8 = (i - k * static_cast<int>(I / 8)) * 8, g = c8 / kKB;
+    const int64_t p = p0 + k;
+    const float* m = work.amax16 + p * (I / 16) + 8 * g;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c8);
+    float mx = m[0];
+#pragma unroll
+    for (int u = 1; u < 8; ++u) mx = fmaxf(mx, m[u]);
+    const float sc = quant_scale(mx);
+    if (c8 % kKB == 0 && g < 4) s_as[k * 4 + g] = sc;
+    uint32_t q0 = 0, q1 = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      q0 |= to_fp8(clamp_fp8(bf16_value(v[u] & 0xffffu) / sc)) << (16 * u);
+      q0 |= to_fp8(clamp_fp8(bf16_value(v[u] >> 16) / sc)) << (16 * u + 8);
+      q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + u] & 0xffffu) / sc)) << (16 * u);
+      q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + u] >> 16) / sc)) << (16 * u + 8);
+    }
+    *reinterpret_cast<uint2*>(s_act + k * I + c8) = make_uint2(q0, q1);
+  }
+  __syncthreads();
+
+  // Two pairs per wave at a time (k and k + 4), their weight rows requested
+  // together.
+  constexpr int NWAVE = kThreads / 64;
+  for (int k = wave; k < topk; k += 2 * NWAVE) {
+    const int kk[2] = {k, k + NWAVE};
+    int slot[2];
+    const uint8_t* brow[2];
+    const float* sw[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      slot[h] = kk[h] < topk ? s_slot[kk[h]] : -1;
+      const int sl = slot[h] < 0 ? 0 : slot[h];
+      brow[h] = w2 + static_cast<int64_t>(sl) * H * I + static_cast<int64_t>(n0 + j) * I + 32 * q;
+      sw[h] = w2_scale + (static_cast<int64_t>(sl) * (H / kKB) + n0 / kKB) * KB;
+    }
+    float acc[2] = {0.f, 0.f};  // row 0 (lanes q = 0, r = 0) is the pair's value
+    for (int k0 = 0; k0 < KB; k0 += kNarrowChunk) {
+      u32x4 b[2][kNarrowChunk][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (slot[h] < 0) continue;
+#pragma unroll
+        for (int i = 0; i < kNarrowChunk; ++i) load32(brow[h] + (k0 + i < KB ? k0 + i : KB - 1) * kKB, b[h][i]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (slot[h] < 0) continue;
+        const int64_t p = p0 + kk[h];
+        const uint8_t* arow = s_act + kk[h] * I + 32 * q;
+#pragma unroll
+        for (int i = 0; i < kNarrowChunk; ++i) {
+          const int kb = k0 + i;
+          if (kb >= KB) continue;
+          u32x4 a[2];
+          a[0] = *reinterpret_cast<const u32x4*>(arow + kb * kKB);
+          a[1] = *reinterpret_cast<const u32x4*>(arow + kb * kKB + 16);
+          // the pair's activation scale for this K block: from LDS for the
+          // first four blocks, else recomputed from the maxima
+          float sa;
+          if (kb < 4) {
+            sa = s_as[kk[h] * 4 + kb];
+          } else {
+            const float* m = work.amax16 + p * (I / 16) + 8 * kb;
+            float mx = m[0];
+#pragma unroll
+            for (int u = 1; u < 8; ++u) mx = fmaxf(mx, m[u]);
+            sa = quant_scale(mx);
+          }
+          const f32x4 part = mfma_k128(a, b[h][i]);
+          acc[h] = fmaf(part[0], sa * sw[h][kb], acc[h]);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (kk[h] >= topk || q != 0) continue;
+      s_c[kk[h]][j] = slot[h] < 0 ? 0 : static_cast<uint16_t>(bf16_bits(acc[h] * topk_weight[p0 + kk[h]]));
+    }
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float sum = 0.f;
+    for (int k = 0; k < topk; ++k)
+      if (s_ok[k] && s_slot[k] >= 0) sum += bf16_value(s_c[k][tid]);
+    out[static_cast<int64_t>(t) * H + n0 + tid] = static_cast<uint16_t>(bf16_bits(sum));
+  }
+}
+
 // GEMM2 for small batches: one 16-row subtile x 128 output columns (4 waves
 // x 32). The subtile's activations arrive as bf16 rows with their
 // 16-column maxima (gemm1_narrow_kernel's output): the workgroup quantises
@@ -941,10 +1292,11 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   Tile tile;
   int ti, item;
   xcd_item(nsub * ncb, ti, item);
+  const int sub = item / ncb, cb = item - sub * ncb;
   if (!load_tile_at(ti, tiles, offsets, tile)) return;
-  const int sub = item / ncb, r0 = 16 * sub;
+  const int r0 = 16 * sub;
   if (r0 >= tile.count) return;
-  const int n0 = (item - sub * ncb) * kBN;
+  const int n0 = cb * kBN;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(I / kKB);
@@ -1309,24 +1661,34 @@ int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I) {
 namespace xp {
 namespace {
 
-// Argument checks shared by xp_moe_experts and xp_moe_experts_noalloc (all
-// but the workspace's).
-int check_experts(const char* what, const uint8_t* xq, const float* xs, int64_t T, int64_t topk,
-                  const float* topk_weight, int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale,
-                  const uint8_t* w2, const float* w2_scale, int64_t slots, const int32_t* offsets,
-                  const int32_t* pairs, const int32_t* tiles, const uint16_t* out) {
+// Argument checks shared by the expert entry points (all but the
+// workspace's and the token operands').
+int check_ffn(const char* what, int64_t T, int64_t topk, const float* topk_weight, int64_t H, int64_t I,
+              const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale, int64_t slots,
+              const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, const uint16_t* out) {
   XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0 && H <= kKB * kMaxKB && I <= kKB * kMaxKB,
              "%s: H=%lld and I=%lld must be multiples of %d, at most %d", what, (long long)H, (long long)I, kBN,
              kKB * kMaxKB);
   XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX && slots >= 1 && slots <= kMaxRouteSlots,
              "%s: T=%lld, topk=%lld, slots=%lld", what, (long long)T, (long long)topk, (long long)slots);
   if (T == 0) return XP_OK;
-  XP_REQUIRE(xq && xs && topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && out,
+  XP_REQUIRE(topk_weight && w13 && w13_scale && w2 && w2_scale && offsets && pairs && tiles && out,
              "%s: null argument", what);
-  XP_REQUIRE(aligned16(xq) && aligned16(w13) && aligned16(w2) && aligned16(out),
-             "%s: fp8 and output buffers must be 16-byte aligned", what);
+  XP_REQUIRE(aligned16(w13) && aligned16(w2) && aligned16(out), "%s: fp8 and output buffers must be 16-byte aligned",
+             what);
   const int64_t bound = tile_bound(T * topk, slots);
   XP_REQUIRE(bound <= 65535, "%s: %lld tiles exceed the launch grid", what, (long long)bound);
+  return XP_OK;
+}
+
+int check_experts(const char* what, const uint8_t* xq, const float* xs, int64_t T, int64_t topk,
+                  const float* topk_weight, int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale,
+                  const uint8_t* w2, const float* w2_scale, int64_t slots, const int32_t* offsets,
+                  const int32_t* pairs, const int32_t* tiles, const uint16_t* out) {
+  const int rc = check_ffn(what, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
+                           tiles, out);
+  if (rc || T == 0) return rc;
+  XP_REQUIRE(xq && xs && aligned16(xq), "%s: xq and xs must be non-null, xq 16-byte aligned", what);
   return XP_OK;
 }
 
@@ -1479,6 +1841,51 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T, int64_
   if (rc) return rc;
   return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
                         tiles, work, out, stream);
+}
+
+int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* topk_ids, int topk_elem_bytes,
+                          int64_t topk, const float* topk_weight, const int32_t* expert_map, int64_t num_experts,
+                          int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
+                          const float* w2_scale, int64_t slots, void* work, int64_t work_bytes, uint16_t* out,
+                          void* stream) {
+  const char* what = "xp_moe_decode_experts";
+  XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX, "%s: T=%lld, topk=%lld", what, (long long)T,
+             (long long)topk);
+  if (T == 0) return XP_OK;
+  const int64_t npairs = T * topk;
+  if (npairs > kDecodePairs || H > kDecodeMaxH || topk * I > kDecodeActBytes)
+    return fail(XP_E_LIMIT,
+                "%s: %lld pairs (at most %d), H=%lld (at most %d), topk*I=%lld (at most %d): use the separate calls",
+                what, (long long)npairs, kDecodePairs, (long long)H, kDecodeMaxH, (long long)(topk * I),
+                kDecodeActBytes);
+  XP_REQUIRE(topk_elem_bytes == 4 || topk_elem_bytes == 8, "%s: id size %d", what, topk_elem_bytes);
+  XP_REQUIRE(num_experts >= 1 && num_experts <= INT32_MAX, "%s: %lld experts", what, (long long)num_experts);
+  XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0, "%s: H=%lld and I=%lld must be multiples of %d", what,
+             (long long)H, (long long)I, kBN);
+  XP_REQUIRE(slots >= 1 && slots <= kMaxRouteSlots, "%s: %lld slots (at most %d)", what, (long long)slots,
+             kMaxRouteSlots);
+  XP_REQUIRE(x && topk_ids && expert_map && topk_weight && w13 && w13_scale && w2 && w2_scale && out,
+             "%s: null argument", what);
+  XP_REQUIRE(aligned16(x) && aligned16(w13) && aligned16(w2) && aligned16(out), "%s: misaligned buffer", what);
+  XP_REQUIRE(work && (reinterpret_cast<uintptr_t>(work) & 255) == 0,
+             "%s: the workspace must be non-null and 256-byte aligned", what);
+  const int64_t need = xp_moe_workspace_bytes(npairs, I);
+  XP_REQUIRE(work_bytes >= need, "%s: workspace of %lld B, needs %lld", what, (long long)work_bytes, (long long)need);
+  Work w;
+  work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
+  const int64_t tiles8 = (tile_bound(npairs, slots) + 7) / 8 * 8;
+  const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(static_cast<unsigned>(tiles8 * nsub * (I / 16))), dim3(kThreads),
+                     static_cast<size_t>(16 * H), as_stream(stream), x, H, I, topk_ids, topk_elem_bytes,
+                     static_cast<int>(npairs), static_cast<int>(topk), expert_map, static_cast<int>(num_experts),
+                     static_cast<int>(slots), w13, w13_scale, nsub, w);
+  int rc = check_launch("gemm1_decode_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(static_cast<unsigned>(T * (H / 16))), dim3(kThreads),
+                     static_cast<size_t>(topk * I), as_stream(stream), H, I, static_cast<int>(topk), topk_ids,
+                     topk_elem_bytes, expert_map, static_cast<int>(num_experts), static_cast<int>(slots), topk_weight,
+                     w2, w2_scale, w, out);
+  return check_launch("gemm2_decode_kernel");
 }
 
 int xp_moe_topk_sum(const uint16_t* contrib, int64_t T, int64_t topk, int64_t H, const void* topk_ids,

@@ -207,6 +207,64 @@ def topk_sum(contrib: torch.Tensor, topk_ids: torch.Tensor, num_experts: int,
     return out
 
 
+DECODE_PAIRS = 64  # a fused decode call's limits: pairs (T * topk), H, topk * I
+DECODE_MAX_H = 4096
+DECODE_ACT_BYTES = 32768
+
+
+def decode_fits(x: torch.Tensor, topk_ids: torch.Tensor, intermediate: int) -> bool:
+    """Whether ``decode_experts`` takes this step (else the separate calls)."""
+    T, topk = _shape(topk_ids)
+    return (0 < T * topk <= DECODE_PAIRS and x.dim() == 2 and x.shape[1] <= DECODE_MAX_H
+            and topk * intermediate <= DECODE_ACT_BYTES)
+
+
+def decode_experts(
+    x: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    expert_map: torch.Tensor,
+    num_experts: int,
+    w13: torch.Tensor,
+    w13_scale: torch.Tensor,
+    w2: torch.Tensor,
+    w2_scale: torch.Tensor,
+    slots: int,
+) -> torch.Tensor:
+    """``quant_route`` + ``run_experts`` + ``topk_sum`` of a decode step in two launches, same bits.
+
+    Every pair with a valid expert id should have a slot below ``slots``
+    (one without adds nothing, where the separate calls would read a
+    contribution never written).
+    """
+    nat.require_device(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise ValueError(f"x must be a 2-D bfloat16 tensor, got {x.dtype} {tuple(x.shape)}")
+    x = x.contiguous()
+    T, H = x.shape
+    Tk, topk = _shape(topk_ids)
+    if Tk != T or tuple(topk_weights.shape) != (T, topk):
+        raise ValueError(f"topk_ids {tuple(topk_ids.shape)} and topk_weights {tuple(topk_weights.shape)} "
+                         f"must both be ({T}, topk)")
+    nat.require_device(expert_map, "expert_map")
+    if expert_map.dtype != torch.int32 or not expert_map.is_contiguous():
+        raise ValueError("expert_map must be a contiguous int32 tensor")
+    ids, eb = nat.ids_arg(topk_ids)
+    tw = topk_weights if topk_weights.dtype == torch.float32 else topk_weights.float()
+    tw = _f32(tw.contiguous(), "topk_weights")
+    S = w13.shape[0]
+    I = w13.shape[1] // 2
+    nbytes = int(nat.lib().xp_moe_workspace_bytes(T * topk, I))
+    work = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=x.device)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
+    nat.call(
+        "xp_moe_decode_experts", x.data_ptr(), T, H, nat.ptr(ids), eb, topk, tw.data_ptr(), expert_map.data_ptr(),
+        num_experts, I, _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(), _fp8_ptr(w2, "w2"),
+        _f32(w2_scale, "w2_scale").data_ptr(), min(slots, S), work.data_ptr(), nbytes, out.data_ptr(), nat.stream(),
+    )
+    return out
+
+
 def fused_moe(
     x: torch.Tensor,
     topk_weights: torch.Tensor,

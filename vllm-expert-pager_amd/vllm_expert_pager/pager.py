@@ -270,6 +270,12 @@ class PagedExperts:
                     decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
 
         with trace.range(f"expert_pager L{layer} experts"):
+            if moe.decode_fits(x, topk_ids, self.pager.intermediate):
+                slab = self.cache_slab
+                out = moe.decode_experts(x, topk_weights, topk_ids, self.expert_map, E, slab[PARAMS[0]],
+                                         slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]], self.table.num_slots)
+                self._log()
+                return out
             xq, xs, routing = moe.quant_route(x, topk_ids, self.expert_map, self.table.num_slots)
             contrib = self._contrib(topk_weights, x)
             self._run(self.cache_slab, xq, xs, topk_weights, topk_ids, contrib, routing)
