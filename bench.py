@@ -450,8 +450,9 @@ def bench_moe(args, dev):
     scales, tokens bf16 ~N(0,1), softmax gate weights over the top 8 of
     random logits (near-uniform coverage). Times the two GEMM launches over
     a 256-slot slab (one-shot), the whole layer (quantise, route, GEMMs,
-    top-k sum), and the overflow path's compute over four 64-row chunks,
-    which must give the one-shot bits.
+    top-k sum), the overflow path's compute over four 64-row chunks,
+    which must give the one-shot bits, and the batch-1 decode step of the
+    same layer (two launches per step).
     """
     from vllm_expert_pager import moe
 
@@ -516,6 +517,27 @@ def bench_moe(args, dev):
     exact = bool(torch.equal(one.view(torch.int16), two.view(torch.int16)))
     if not exact:
         raise SystemExit("chunked expert FFN differs from the one-shot run")
+    # Batch-1 decode step of the same layer: one token, its top-8 experts
+    # resident in the slab, the two-launch decode FFN. 64 steps with
+    # different experts are captured in one graph so that launch overhead
+    # and cache reuse of one expert set stay out of the figure.
+    nd = 64
+    x1 = torch.randn((nd, 1, H), generator=g, device=dev).to(torch.bfloat16)
+    ids1 = torch.stack([torch.randperm(E, generator=g, device=dev)[:topk] for _ in range(nd)]).view(nd, 1, topk)
+    tw1 = torch.softmax(torch.randn((nd, 1, topk), generator=g, device=dev), dim=2).contiguous()
+    ids1 = ids1.to(torch.int64).contiguous()
+
+    def decode_steps():
+        for i in range(nd):
+            moe.decode_experts(x1[i], tw1[i], ids1[i], emap, E, w13, w13s, w2, w2s, E)
+
+    decode_steps()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        decode_steps()
+    us_decode = timed(graph.replay, reps) * 1e3 / nd
+    decode_bytes = topk * (2 * I * H + H * I)
     pairs = T * topk
     flops = 2.0 * pairs * (2 * I * H + H * I)
     weight_bytes = E * (2 * I * H + H * I) + 4 * (w13s.numel() + w2s.numel())
@@ -533,6 +555,8 @@ def bench_moe(args, dev):
         "ms_layer_one_shot": round(ms_layer, 4),
         "ms_layer_chunked_4x64": round(ms_chunked, 4),
         "chunked_bit_exact": exact,
+        "decode_ffn_batch1_us": round(us_decode, 2),
+        "decode_ffn_batch1_weight_gbps": round(decode_bytes / (us_decode * 1e-6) / 1e9, 1),
     }
     log(f"moe: {out}")
     return out
@@ -940,7 +964,7 @@ def main() -> None:
     ap.add_argument("--decode-steps", type=int, default=2000)
     ap.add_argument("--decode-warmup", type=int, default=20)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
-                    help="after the decode leg, copy this many MiB device to device three times "
+                    help="before the legs, copy this many MiB device to device three times "
                          "(the plain copy that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -956,6 +980,17 @@ def main() -> None:
     torch.cuda.set_device(dev)
     cores = len(os.sched_getaffinity(0))
 
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib << 20
+        a = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        for _ in range(3):
+            torch.bitwise_not(a, out=b)
+        torch.cuda.synchronize()
+        del a, b
+        log(f"copy probe: 3 device copies and 3 elementwise passes of {args.copy_probe_mib} MiB")
     if args.only_moe:
         print(json.dumps({"moe": bench_moe(args, dev)}), flush=True)
         return
@@ -969,16 +1004,6 @@ def main() -> None:
         print(json.dumps({"tiered": bench_tiered(args, dev)}), flush=True)
         return
     dec = bench_decode(args, dev, cores)
-    if args.copy_probe_mib:
-        n = args.copy_probe_mib << 20
-        a = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
-        b = torch.empty_like(a)
-        for _ in range(3):
-            b.copy_(a)
-        for _ in range(3):
-            torch.bitwise_not(a, out=b)
-        torch.cuda.synchronize()
-        log(f"copy probe: 3 device copies and 3 elementwise passes of {args.copy_probe_mib} MiB")
     extras = {}
     if not args.only_decode:
         extras["encode"] = bench_encode(args, dev, cores)

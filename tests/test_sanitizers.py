@@ -70,6 +70,7 @@ def test_ssd_server_under_thread_sanitizer(tmp_path):
         "VLLM_EXPERT_PAGER_LIBRARY": lib,
         "LD_PRELOAD": tsan,
         "TSAN_OPTIONS": "halt_on_error=1 ignore_noninstrumented_modules=1",
+        "XP_SSD_TEST_OWN_ONLY": "1",
     }
     assert _loaded(env, tsan)
     out = _run(env, ["tests/test_ssd_cpu.py"])
@@ -87,6 +88,7 @@ def test_host_codec_server_and_oracle_under_address_sanitizer(tmp_path):
         # The interpreter's own allocations outlive the run by design.
         "ASAN_OPTIONS": "detect_leaks=0",
         "UBSAN_OPTIONS": "halt_on_error=1 print_stacktrace=1",
+        "XP_SSD_TEST_OWN_ONLY": "1",
     }
     assert _loaded(env, asan)
     out = _run(env, ["tests/test_oracle_codec.py", "tests/test_ssd_cpu.py"])

@@ -5,6 +5,11 @@ writes a request slot, publishes its seq, and polls `done`. Covers in-order
 serving, the worker pool, read failures that still release the waiter, the
 re-publish and idle resend of `done`, gaps in seq counted as missed, and the
 test delay (the behaviours of store.py:83-308 and tests/test_store.py).
+
+The protocol tests run against both servers: this build's (``xp``) and the
+reference's own C server compiled from its source text by
+``oracle/build_ref.py`` (``ref``, skipped where no reference tree is
+present), which pins ``ssd.cpp`` to the reference's behaviour.
 """
 
 import ctypes
@@ -22,10 +27,45 @@ PITCH = (4096, 8192)
 RECORD = sum(PITCH)
 
 
-def _lib():
+_SSD_SIGS = {
+    "ssd_start": (ctypes.c_void_p, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_long] * 6
+                  + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
+    "ssd_stop": (None, [ctypes.c_void_p]),
+    "ssd_stats": (None, [ctypes.c_void_p] * 5),
+    "ssd_error": (ctypes.c_char_p, [ctypes.c_void_p]),
+    "ssd_test_delay": (None, [ctypes.c_void_p, ctypes.c_double]),
+}
+_REF = {}
+
+
+def _ref_lib():
+    """The reference's C server (built once per session), or a skip without a reference tree."""
+    if "lib" not in _REF:
+        from oracle import build_ref
+
+        path = build_ref.build_ssd_ref()
+        lib = None
+        if path:
+            lib = ctypes.CDLL(path)
+            for name, (res, args) in _SSD_SIGS.items():
+                fn = getattr(lib, name)
+                fn.restype, fn.argtypes = res, args
+        _REF["lib"] = lib
+    if _REF["lib"] is None:
+        pytest.skip("no reference tree to build its C server from")
+    return _REF["lib"]
+
+
+def _lib(which="xp"):
+    if which == "ref":
+        return _ref_lib()
     from vllm_expert_pager import _native
 
     return _native.lib()
+
+
+# The sanitizer runs instrument this build's server only.
+SERVERS = ["xp"] if os.environ.get("XP_SSD_TEST_OWN_ONLY") else ["xp", "ref"]
 
 
 def aligned(nbytes, dtype=np.uint8):
@@ -39,8 +79,8 @@ def pattern(layer, e, name):
 
 
 class Server:
-    def __init__(self, path, nworkers=7):
-        self.lib = _lib()
+    def __init__(self, path, nworkers=7, which="xp"):
+        self.lib = _lib(which)
         with open(path, "wb") as f:
             for layer in range(L):
                 for e in range(E):
@@ -92,9 +132,14 @@ class Server:
             os.close(self.fd)
 
 
+@pytest.fixture(params=SERVERS)
+def which(request):
+    return request.param
+
+
 @pytest.fixture
-def server(tmp_path):
-    s = Server(str(tmp_path / "paging.bin"))
+def server(tmp_path, which):
+    s = Server(str(tmp_path / "paging.bin"), which=which)
     yield s
     s.close()
 
@@ -134,8 +179,8 @@ def test_read_failure_still_releases(server):
     assert "outside the RAM tier" in server.error()  # the first failure is kept
 
 
-def test_expert_out_of_range(tmp_path):
-    s = Server(str(tmp_path / "p.bin"))
+def test_expert_out_of_range(tmp_path, which):
+    s = Server(str(tmp_path / "p.bin"), which=which)
     try:
         s.wait(s.publish(5, [1], [0]))
         assert "out of range" in s.error()
@@ -175,8 +220,8 @@ def test_test_delay_holds_requests(server):
     server.lib.ssd_test_delay(server.h, 0.0)
 
 
-def test_stop_while_delaying(tmp_path):
-    s = Server(str(tmp_path / "p.bin"))
+def test_stop_while_delaying(tmp_path, which):
+    s = Server(str(tmp_path / "p.bin"), which=which)
     s.lib.ssd_test_delay(s.h, 60.0)
     s.publish(0, [1], [0])
     time.sleep(0.05)
@@ -185,8 +230,8 @@ def test_stop_while_delaying(tmp_path):
     assert time.time() - t0 < 5.0
 
 
-def test_start_rejects_bad_arguments(tmp_path):
-    lib = _lib()
+def test_start_rejects_bad_arguments(tmp_path, which):
+    lib = _lib(which)
     req = aligned(8 * 64, np.int64)
     done = aligned(4096, np.int64)
     ptrs = (ctypes.c_void_p * 5)()
