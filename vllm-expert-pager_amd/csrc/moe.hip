@@ -20,8 +20,9 @@
 // Work decomposition: route lists the pairs of each slab slot in CSR form
 // and cuts them into tiles of 64 pairs and wide tiles of 128 pairs of one
 // slot. At prefill sizes gemm1 and gemm2 run one persistent workgroup per
-// CU over (wide tile, 128-column block) items, so each column block of an
-// expert's weights is read once; for few pairs gemm1 takes 16 rows and 16
+// CU over (wide tile, column block) items (128 activation columns, 256
+// output columns), so each column block of an expert's weights is read
+// once, streamed through an LDS ring; for few pairs gemm1 takes 16 rows and 16
 // columns of a tile, with the K blocks split over its waves (so a decode
 // step of 8 pairs spreads over 256 workgroups), and gemm2 16 rows and 128
 // output columns. Launch grids are sized from the shapes alone (bounds on
@@ -345,58 +346,8 @@ inline int64_t work_layout(int64_t npairs, int64_t I, Work* w, uint8_t* base) {
 }
 
 constexpr int kWideTiles = 64;  // tile bound from which gemm1 uses the wide workgroups
-constexpr int kWideNW = 8;      // waves (16 activation columns each) of a wide gemm1 workgroup
 constexpr int kNarrowChunk = 4; // K blocks per load chunk of the small-batch GEMMs
 constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I <= 8192)
-
-constexpr int kAPitch = 144;  // LDS bytes per staged A row (128 + 16 against bank conflicts)
-
-// The A rows of a wide tile, D K blocks in flight: each of the NT threads
-// loads 16-byte pieces into registers, stored to LDS one block before use.
-// Row offsets (32-bit, from one base) are kept for two items, the current
-// and the next, so the last blocks' loads can run ahead into the next item.
-template <int NT, int D>
-struct ARing {
-  static constexpr int kPer = kWM * 8 / NT;  // 16-byte pieces per thread
-  uint32_t off[2][kPer];
-  int dst[kPer];
-  u32x4 v[D][kPer];
-  __device__ __forceinline__ ARing() {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = static_cast<int>(threadIdx.x) + NT * i;
-      dst[i] = (c >> 3) * kAPitch + (c & 7) * 16;
-      off[0][i] = off[1][i] = 0;
-    }
-  }
-  // Offsets of row set `set` from the rows s_row[kWM] (A rows of lda bytes).
-  // The set is selected, not indexed: a run-time index would put the
-  // offsets in scratch memory.
-  __device__ __forceinline__ void init(int set, int64_t lda, const int* s_row) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = static_cast<int>(threadIdx.x) + NT * i;
-      const uint32_t o = static_cast<uint32_t>(s_row[c >> 3] * lda + (c & 7) * 16);
-      off[0][i] = set ? off[0][i] : o;
-      off[1][i] = set ? o : off[1][i];
-    }
-  }
-  __device__ __forceinline__ void load(int stage, const uint8_t* A, int set, int kb) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i)
-      v[stage][i] = *reinterpret_cast<const u32x4*>(A + (set ? off[1][i] : off[0][i]) + kb * kKB);
-  }
-  __device__ __forceinline__ void store(int stage, uint8_t* s_a) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) *reinterpret_cast<u32x4*>(s_a + dst[i]) = v[stage][i];
-  }
-};
-
-__device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4 (&a)[2]) {
-  const u32x4* p = reinterpret_cast<const u32x4*>(s_a + row * kAPitch + 32 * q);
-  a[0] = p[0];
-  a[1] = p[1];
-}
 
 // ---- prefill GEMMs: persistent workgroups over wide tiles ----
 //
@@ -406,12 +357,85 @@ __device__ __forceinline__ void read_a(const uint8_t* s_a, int row, int q, u32x4
 // l + 2 nl, ... (l = b / 8, nl = gridDim.x / 8), so a tile's column blocks
 // run side by side on one XCD and its token rows are read into one L2.
 //
-// A workgroup streams its items' operands without a break: the next item's
-// rows and scales are looked up during the current item's first K blocks,
-// and its first kPD blocks of weights and A rows are requested during the
-// current item's last blocks, so the epilogue and the next item's set-up
-// overlap the operand stream. Each wave keeps kPD K blocks in flight.
-constexpr int kPD = 2;
+// The operands stream through a ring of kRing LDS stages that global-to-LDS
+// loads fill without passing through registers: a stage holds one K block
+// of the item's weight rows, of the tile's A rows and of the A rows' scales.
+// Each wave keeps the loads of the next kRing - 1 blocks in flight while it
+// multiplies one, and the stream runs on across items: the next item's rows
+// are looked up during the current item's first steps and its first blocks
+// are requested during the last, so the epilogue and the next item's set-up
+// overlap the loads.
+//
+// Vector memory operations complete in issue order, so "block k has landed"
+// is "at most the last step's kOps loads are in flight" (s_waitcnt vmcnt).
+// That holds only if nothing is issued after a step's operand loads, and if
+// the compiler adds no waits of its own: every other load in the loop goes
+// to LDS or through the scalar cache, and the epilogue's global stores are
+// issued at the start of the next item's first step.
+constexpr int kRing = 3;
+constexpr int kAhead = kRing - 1;  // blocks requested ahead of the one multiplied
+constexpr int kRowB = kKB;         // bytes of one operand row's K block (fp8)
+constexpr int kGemmWaves = 8;      // waves of a prefill GEMM workgroup
+constexpr int kMinSteps = 4;       // steps per item at least (the next item's set-up takes 3)
+
+// This wave's loads but the last N have landed and its LDS writes are done;
+// then the workgroup meets. A plain s_barrier: the fence of __syncthreads
+// would also wait for the loads in flight.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
+}
+// One piece per lane from global memory into LDS: lane l's 16 (4) bytes, at
+// base + off, land at dst + 16 l (4 l); base and dst are the same for the
+// whole wave. Written in assembly so that the compiler does not track these
+// loads: it would make every LDS access wait for all of them. M0 (the LDS
+// destination) is restored afterwards.
+// The readfirstlane builtin returns int: each half is taken as uint32_t
+// before widening, or a low half with bit 31 set would sign-extend into the
+// high half.
+__device__ __forceinline__ uint64_t uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off), "s"(uniform_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds_addr(dst)))
+      : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* dst) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(off), "s"(uniform_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds_addr(dst)))
+      : "memory");
+}
+
+// Stage rows are 128 bytes; 16-byte piece p of row r sits at slot p ^ (r & 7),
+// so the 8 lanes that read one piece of 8 consecutive rows use distinct
+// banks. A load of 8 rows writes slot l & 7 of row l / 8 from lane l, which
+// therefore fetches global piece (l & 7) ^ (row & 7).
+__device__ __forceinline__ int swizzled_piece(int lane) { return (lane & 7) ^ ((lane >> 3) & 7); }
+
+// A lane's MFMA operand: bytes 32q .. 32q + 31 of stage row `row`.
+__device__ __forceinline__ void read_frag(const uint8_t* stage, int row, int q, u32x4 (&v)[2]) {
+  const uint8_t* r = stage + row * kRowB;
+  const int s = row & 7;
+  v[0] = *reinterpret_cast<const u32x4*>(r + (((2 * q) ^ s) << 4));
+  v[1] = *reinterpret_cast<const u32x4*>(r + (((2 * q + 1) ^ s) << 4));
+}
 
 template <int N>
 using Int = std::integral_constant<int, N>;
@@ -441,307 +465,277 @@ struct Item {
 };
 
 // Candidate n of this workgroup: item j = l + n * nl of its XCD, i.e. wide
-// tile (j / ncols) * 8 + xcd and column block j % ncols.
-__device__ __forceinline__ void item_index(int n, int ncols, int& w, int& col) {
+// tile (j / ncols) * 8 + xcd and column block j % ncols. Its list entry is
+// read through the scalar cache (the list does not change during the call).
+__device__ __forceinline__ Item item_fetch(int n, int ncols, const int32_t* __restrict__ wide, int64_t wmax) {
   const int jj = (static_cast<int>(blockIdx.x) >> 3) + n * (static_cast<int>(gridDim.x) >> 3);
-  w = (jj / ncols) * 8 + (static_cast<int>(blockIdx.x) & 7);
-  col = jj - (jj / ncols) * ncols;
-}
-
-// Lanes 0..3 of each wave load the list's live count and candidate n's
-// (slot, first, count): vector loads, which complete in order with the
-// operand loads; item_get reads them once landed.
-__device__ __forceinline__ int item_request(int n, int ncols, const int32_t* __restrict__ wide, int64_t wmax) {
-  int w, col;
-  item_index(n, ncols, w, col);
-  const int lane = static_cast<int>(threadIdx.x) & 63;
-  if (lane == 0) return wide[0];
-  if (lane < 4 && w < wmax) return wide[1 + 3 * static_cast<int64_t>(w) + (lane - 1)];
-  return 0;
-}
-
-__device__ __forceinline__ Item item_get(int m, int n, int ncols) {
-  int w, col;
-  item_index(n, ncols, w, col);
+  const int w = __builtin_amdgcn_readfirstlane((jj / ncols) * 8 + (static_cast<int>(blockIdx.x) & 7));
   Item it;
-  const int live = __builtin_amdgcn_readlane(m, 0);
-  it.slot = __builtin_amdgcn_readlane(m, 1);
-  it.first = __builtin_amdgcn_readlane(m, 2);
-  it.count = w < live ? __builtin_amdgcn_readlane(m, 3) : 0;
-  it.col = col;
+  it.col = __builtin_amdgcn_readfirstlane(jj - (jj / ncols) * ncols);
+  it.slot = it.first = it.count = 0;
+  const int live = wide[0];
+  if (w < live && w < wmax) {
+    it.slot = wide[1 + 3 * static_cast<int64_t>(w)];
+    it.first = wide[2 + 3 * static_cast<int64_t>(w)];
+    it.count = wide[3 + 3 * static_cast<int64_t>(w)];
+  }
   return it;
 }
 
-// The pair of row tid of an item (padding rows repeat its first pair), and
-// its LDS copy with the operand row it reads (pair / div).
-__device__ __forceinline__ int item_pair(const Item& it, const int32_t* __restrict__ pairs) {
-  const int tid = threadIdx.x;
-  return tid < kWM ? pairs[it.first + (tid < it.count ? tid : 0)] : 0;
+// The pairs of an item's rows (padding rows repeat its first pair) into
+// s_pn, by waves 0 and 1.
+__device__ __forceinline__ void request_pairs(const Item& it, const int32_t* __restrict__ pairs, int* s_pn) {
+  const int tid = threadIdx.x, wave = tid >> 6;
+  if (wave < kWM / 64) dma4(pairs + it.first, 4 * (tid < it.count ? tid : 0), s_pn + 64 * wave);
 }
 
-__device__ __forceinline__ void put_rows(const Item& it, int p, int div, int* s_pair, int* s_row) {
+// s_pair (pair or -1 past the count) and s_row (the operand row, pair / div)
+// from s_pn. Pairs are clamped to [0, npairs) before they address anything.
+__device__ __forceinline__ void put_rows(const Item& it, const int* s_pn, int div, int64_t npairs, int* s_pair,
+                                         int* s_row) {
   const int tid = threadIdx.x;
   if (tid < kWM) {
-    s_pair[tid] = tid < it.count ? p : -1;
-    s_row[tid] = p / div;
+    const int p = s_pn[tid];
+    const int c = p < 0 ? 0 : (p >= npairs ? static_cast<int>(npairs - 1) : p);
+    s_pair[tid] = tid < it.count && c == p ? p : -1;
+    s_row[tid] = c / div;
   }
 }
 
-// K blocks an item's loop runs: KB rounded up to kPD, and at least 2 kPD,
-// so that the next item is looked up before its first blocks are requested.
-__host__ __device__ inline int padded_blocks(int KB) {
-  const int r = (KB + kPD - 1) / kPD * kPD;
-  return r > 2 * kPD ? r : 2 * kPD;
-}
-
-// Per-row scales of an item, [K block][row], are loaded 4 floats per
-// thread per K loop step (kScaleStep of them per chunk).
-template <int NT>
-struct ScaleChunk {
-  static constexpr int kFloats = 4 * NT;
-  float v[4];
-  // Chunk c of the scales src[row * KB + kb] of rows s_row.
-  __device__ __forceinline__ void load(const float* __restrict__ src, int KB, const int* s_row, int c) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = c * kFloats + i * NT + static_cast<int>(threadIdx.x);
-      const int kb = e / kWM, r = e - kb * kWM;
-      v[i] = kb < KB ? src[static_cast<int64_t>(s_row[r]) * KB + kb] : 0.f;
-    }
-  }
-  __device__ __forceinline__ void store(float* dst, int KB, int c) const {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = c * kFloats + i * NT + static_cast<int>(threadIdx.x);
-      if (e < KB * kWM) dst[e] = v[i];
-    }
-  }
+// Per-lane byte offsets of a wave's A-row and A-scale loads for an item with
+// operand rows s_row (A rows of lda bytes, KB scales per row): A stage rows
+// 16 wave + 8 i + lane / 8 (i = 0, 1), scale rows 64 (wave & 1) + lane.
+struct AOffsets {
+  uint32_t a[2];
+  uint32_t s;
 };
 
-// GEMM1 at prefill sizes: gate and up for NW*16 = 128 activation columns of
-// a wide tile per item; each wave owns 16 columns and runs the K blocks in
-// order, so a column's value does not depend on the workgroup width or the
-// tile height. The tile's A rows are staged in LDS one block ahead (double
-// buffered). Then a = bf16(silu(bf16 gate) * bf16 up) is quantised to fp8
-// per row over the workgroup's 128 columns, one scale group. Only the 16-row
-// subtiles that hold pairs are multiplied. Dynamic LDS: the token scales of
-// two items, 2 x (H / 128) x kWM floats.
-template <int NW>
-__global__ void __launch_bounds__(NW * 64) gemm1_kernel(const uint8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                        int64_t H, int64_t I, int topk,
-                                                        const uint8_t* __restrict__ w13,
-                                                        const float* __restrict__ w13_scale,
-                                                        const int32_t* __restrict__ pairs,
-                                                        const int32_t* __restrict__ wide, int64_t wmax, Work work) {
-  constexpr int NT = NW * 64, NC = NW * 16;
+__device__ __forceinline__ AOffsets a_offsets(const int* s_row, int64_t lda, int KB) {
+  const int wave = static_cast<int>(threadIdx.x) >> 6, lane = static_cast<int>(threadIdx.x) & 63;
+  AOffsets o;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    o.a[i] = static_cast<uint32_t>(s_row[16 * wave + 8 * i + (lane >> 3)] * lda + 16 * swizzled_piece(lane));
+  o.s = static_cast<uint32_t>(s_row[64 * (wave & 1) + lane] * KB * 4);
+  return o;
+}
+
+// GEMM1 at prefill sizes: gate and up for 128 activation columns of a wide
+// tile per item; each wave owns 16 columns (16 gate and 16 up rows) and runs
+// the K blocks in order, so a column's value does not depend on the
+// workgroup width or the tile height. Then a = bf16(silu(bf16 gate) *
+// bf16 up) is quantised to fp8 per row over the workgroup's 128 columns, one
+// scale group. Only the 16-row subtiles that hold pairs are multiplied.
+__global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* __restrict__ xq,
+                                                               const float* __restrict__ xs, int64_t H, int64_t I,
+                                                               int topk, const uint8_t* __restrict__ w13,
+                                                               const float* __restrict__ w13_scale,
+                                                               const int32_t* __restrict__ pairs,
+                                                               const int32_t* __restrict__ wide, int64_t wmax,
+                                                               int64_t npairs, Work work) {
+  constexpr int NW = kGemmWaves, NT = NW * 64, NC = NW * 16;
+  constexpr int NB = 2 * NC;       // weight rows per item: per wave 16 gate, then 16 up
+  constexpr int kOps = 4 + 2 + 1;  // loads per wave and step: weight rows, A rows, A scales
   static_assert(NC == kKB, "a workgroup covers one 128-column scale group of the activations");
-  extern __shared__ __attribute__((aligned(16))) float s_xs[];  // [2 items][K block][row] token scales
+  __shared__ __attribute__((aligned(16))) uint8_t s_b[kRing][NB * kRowB];
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[kRing][kWM * kRowB];
+  __shared__ __attribute__((aligned(16))) float s_s[kRing][kWM];
+  __shared__ int s_pn[kWM];
   __shared__ int s_row[2][kWM];
   __shared__ int s_pair[2][kWM];
-  __shared__ float s_sw[2][2][kMaxKB];  // gate and up weight scales per K block, two items
-  __shared__ float s_m[NW][kWM];        // row maxima per wave (16 columns)
-  __shared__ float s_q[kWM];            // row scales of the activations
-  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kWM * kAPitch];  // A stages
-  __shared__ __attribute__((aligned(16))) uint16_t s_a16[kWM * kKB];      // bf16 activations of an item
+  __shared__ float s_sw[2][2 * kMaxKB];  // gate (first KB) and up weight scales per K block, two items
+  __shared__ float s_m[NW][kWM];         // row maxima per wave (16 columns)
+  __shared__ float s_q[kWM];             // row scales of the activations
 
   const int ncols = static_cast<int>(I / NC);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
-  const int KB = static_cast<int>(H / kKB), KBP = padded_blocks(KB);
-  const int nchunks = (KB * kWM + ScaleChunk<NT>::kFloats - 1) / ScaleChunk<NT>::kFloats;
-  const int64_t ksz = static_cast<int64_t>(KB) * kWM;
+  const int KB = static_cast<int>(H / kKB), KS = KB > kMinSteps ? KB : kMinSteps;
 
-  Item cur = item_get(item_request(0, ncols, wide, wmax), 0, ncols);
+  Item cur = item_fetch(0, ncols, wide, wmax);
   if (cur.count == 0) return;
-  Item nxt = item_get(item_request(1, ncols, wide, wmax), 1, ncols);
+  Item nxt = item_fetch(1, ncols, wide, wmax);
   int n = 2;
 
-  // Weight rows: the item's gate rows start at wbase, its up rows I rows
-  // later; this lane reads row 16 * wave + j of each at byte 32q.
-  const int64_t boff = static_cast<int64_t>(16 * wave + j) * H + 32 * q;
+  // Weight-row loads: load i of a wave covers its stage rows 8i .. 8i + 7,
+  // gate rows for i < 2 and up rows (I rows further) for i >= 2.
+  uint32_t boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    boff[i] = static_cast<uint32_t>(((i >= 2 ? I : 0) + 16 * wave + 8 * (i & 1) + (lane >> 3)) * H +
+                                    16 * swizzled_piece(lane));
   auto wbase = [&](const Item& it) {
-    return w13 + (static_cast<int64_t>(it.slot) * 2 * I + static_cast<int64_t>(it.col) * NC) * H + boff;
+    return w13 + (static_cast<int64_t>(it.slot) * 2 * I + static_cast<int64_t>(it.col) * NC) * H;
   };
-  auto load_b = [&](u32x4 (&bb)[2][2], const uint8_t* base, int kb) {
-    load32(base + kb * kKB, bb[0]);
-    load32(base + I * H + kb * kKB, bb[1]);
-  };
-  // The workgroup's gate and up rows each lie in one 128-row scale block.
-  auto weight_scale = [&](const Item& it, int i) {
-    const int64_t blk = static_cast<int64_t>(it.slot) * (2 * I / kKB) + (i < KB ? 0 : I / kKB) + it.col;
-    return w13_scale[blk * KB + (i < KB ? i : i - KB)];
-  };
-
-  u32x4 b[kPD][2][2];
-  ARing<NT, kPD> ar;
-  {
-    // First item: weights first (they depend on the slot alone), then its
-    // rows, scales and A rows.
-    const uint8_t* wb = wbase(cur);
-#pragma unroll
-    for (int d = 0; d < kPD; ++d) load_b(b[d], wb, d < KB ? d : KB - 1);
-    put_rows(cur, item_pair(cur, pairs), topk, s_pair[0], s_row[0]);
-    __syncthreads();
-    for (int c = 0; c < nchunks; ++c) {
-      ScaleChunk<NT> sc;
-      sc.load(xs, KB, s_row[0], c);
-      sc.store(s_xs, KB, c);
+  // Weight scales of an item into s_sw (waves 0 and 1): the workgroup's gate
+  // and up rows each lie in one 128-row scale block.
+  auto request_weight_scales = [&](const Item& it, float* dst) {
+    if (wave < 2) {
+      const int i = tid < 2 * KB ? tid : 2 * KB - 1;
+      const int64_t blk = static_cast<int64_t>(it.slot) * (2 * I / kKB) + (i < KB ? 0 : I / kKB) + it.col;
+      dma4(w13_scale, static_cast<uint32_t>(4 * (blk * KB + (i < KB ? i : i - KB))), dst + 64 * wave);
     }
-    if (tid < 2 * KB) s_sw[0][tid / KB][tid % KB] = weight_scale(cur, tid);
-    ar.init(0, H, s_row[0]);
+  };
+  auto issue = [&](int stage, const uint8_t* wb, const AOffsets& ao, int kb) {
+    const uint8_t* bsrc = wb + kb * kRowB;
 #pragma unroll
-    for (int d = 0; d < kPD; ++d) ar.load(d, xq, 0, d < KB ? d : KB - 1);
-    __syncthreads();
-    ar.store(0, s_a[0]);
-    __syncthreads();
-  }
+    for (int i = 0; i < 4; ++i) dma16(bsrc, boff[i], s_b[stage] + (32 * wave + 8 * i) * kRowB);
+    const uint8_t* asrc = xq + kb * kRowB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(asrc, ao.a[i], s_a[stage] + (16 * wave + 8 * i) * kRowB);
+    dma4(xs + kb, ao.s, &s_s[stage][64 * (wave & 1)]);
+  };
+  // The fp8 rows and scales of the previous item, staged in LDS.
+  int out_cb = 0, out_c0 = 0, out_rows = 0;
+  auto copy_out = [&](const uint8_t* stg) {
+    if (tid < out_rows) {
+      const int p = s_pair[out_cb][tid];
+      if (p >= 0) work.acts[static_cast<int64_t>(p) * (I / kKB) + out_c0 / kKB] = s_q[tid];
+    }
+    // 16 bytes per thread and pass: 8 threads per row.
+    for (int i = tid; i < out_rows * (kKB / 16); i += NT) {
+      const int row = i >> 3, piece = i & 7;
+      const int p = s_pair[out_cb][row];
+      if (p >= 0)
+        *reinterpret_cast<u32x4*>(work.act + static_cast<int64_t>(p) * I + out_c0 + piece * 16) =
+            *reinterpret_cast<const u32x4*>(stg + row * kRowB + piece * 16);
+    }
+  };
 
-  int cb = 0;  // LDS buffer and A row set of the current item
+  request_pairs(cur, pairs, s_pn);
+  request_weight_scales(cur, s_sw[0]);
+  ring_barrier<0>();
+  put_rows(cur, s_pn, topk, npairs, s_pair[0], s_row[0]);
+  lds_barrier();
+  AOffsets ao_cur = a_offsets(s_row[0], H, KB), ao_nxt = ao_cur;
+  issue(0, wbase(cur), ao_cur, 0);
+  issue(1, wbase(cur), ao_cur, KB > 1 ? 1 : 0);
+
+  int st = 0;  // stage of the current step
+  int cb = 0;  // row set of the current item
   for (;;) {
     const int nb = cb ^ 1;
     const bool more = nxt.count > 0;
     const uint8_t* wb_cur = wbase(cur);
     const uint8_t* wb_nxt = more ? wbase(nxt) : wb_cur;
     const int nmi = (cur.count + 15) >> 4;
-    const int c0 = cur.col * NC;
-    const float* xs_cur = s_xs + cb * ksz;
-    int pn = 0, m2 = 0;
-    float swn = 0.f;
-    ScaleChunk<NT> scn;
+    Item after = nxt;
 
     with_subtiles(nmi, [&](auto nmi_c) {
       constexpr int MI = decltype(nmi_c)::value;
       f32x4 acc[MI][2];
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      auto compute = [&](const uint8_t* sa_buf, const u32x4 (&bb)[2][2], int kb) {
-        const float g = s_sw[cb][0][kb], u = s_sw[cb][1][kb];
-        // Subtile mi + 1's A rows and token scales are read from LDS while
-        // subtile mi multiplies; the scheduling barrier keeps the compiler
-        // from hoisting more subtiles' operands (registers are the limit).
-        u32x4 a[2][2];
-        f32x4 sa[2];
-        auto fetch = [&](int mi, int slot) {
-          read_a(sa_buf, 16 * mi + j, q, a[slot]);
-          sa[slot] = *reinterpret_cast<const f32x4*>(xs_cur + kb * kWM + 16 * mi + 4 * q);
-        };
-        fetch(0, 0);
-#pragma unroll
-        for (int mi = 0; mi < MI; ++mi) {
-          const int c = mi & 1;
-          if (mi + 1 < MI) fetch(mi + 1, c ^ 1);
-          const f32x4 part0 = mfma_k128(a[c], bb[0]), part1 = mfma_k128(a[c], bb[1]);
-          // One combined scale per output row and K block (token scale x
-          // weight scale), so each MFMA output needs a single FMA.
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            acc[mi][0][r] = fmaf(part0[r], sa[c][r] * g, acc[mi][0][r]);
-            acc[mi][1][r] = fmaf(part1[r], sa[c][r] * u, acc[mi][1][r]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      };
 
-      for (int kb = 0; kb < KBP; kb += kPD) {
+      for (int k = 0; k < KS; ++k) {
+        ring_barrier<kOps>();  // block k is in stage st
+        const int sn = st == 0 ? kRing - 1 : st - 1;  // the stage multiplied one step ago
+        if (k == 0 && out_rows > 0) {
+          copy_out(s_a[sn]);  // staged there by the previous item's epilogue
+          out_rows = 0;
+          lds_barrier();
+        }
+        // The next item: its pairs and the entry of the one after (step 0),
+        // its rows (1), its A offsets and weight scales (2).
+        if (more) {
+          if (k == 0) {
+            request_pairs(nxt, pairs, s_pn);
+            after = item_fetch(n, ncols, wide, wmax);
+          } else if (k == 1) {
+            put_rows(nxt, s_pn, topk, npairs, s_pair[nb], s_row[nb]);
+          } else if (k == 2) {
+            ao_nxt = a_offsets(s_row[nb], H, KB);
+            request_weight_scales(nxt, s_sw[nb]);
+          }
+        }
+        // Block k + kAhead of this item, or the next item's first blocks.
+        const int blk = k + kAhead;
+        if (blk < KS || !more)
+          issue(sn, wb_cur, ao_cur, blk < KB ? blk : KB - 1);
+        else
+          issue(sn, wb_nxt, ao_nxt, blk - KS < KB ? blk - KS : KB - 1);
+        if (k < KB) {
+          const float g = s_sw[cb][k], u = s_sw[cb][KB + k];
+          u32x4 bg[2], bu[2];
+          read_frag(s_b[st], 32 * wave + j, q, bg);
+          read_frag(s_b[st], 32 * wave + 16 + j, q, bu);
+          // Subtile mi + 1's A rows and scales are read while subtile mi
+          // multiplies.
+          u32x4 a[2][2];
+          f32x4 sa[2];
+          auto fetch = [&](int mi, int slot) {
+            read_frag(s_a[st], 16 * mi + j, q, a[slot]);
+            sa[slot] = *reinterpret_cast<const f32x4*>(&s_s[st][16 * mi + 4 * q]);
+          };
+          fetch(0, 0);
 #pragma unroll
-        for (int d = 0; d < kPD; ++d) {
-          const int k = kb + d;
-          // The next item: its pairs and metadata of the one after (step 0),
-          // its rows (1), its A row offsets and weight scales (2, 3) and its
-          // token scales (2 ..).
-          if (more) {
-            if (k == 0) {
-              pn = item_pair(nxt, pairs);
-              m2 = item_request(n, ncols, wide, wmax);
-            } else if (k == 1) {
-              put_rows(nxt, pn, topk, s_pair[nb], s_row[nb]);
-            } else {
-              if (k == 2) {
-                ar.init(nb, H, s_row[nb]);
-                swn = tid < 2 * KB ? weight_scale(nxt, tid) : 0.f;
-              } else if (k == 3 && tid < 2 * KB) {
-                s_sw[nb][tid / KB][tid % KB] = swn;
-              }
-              if (k - 3 >= 0 && k - 3 < nchunks) scn.store(s_xs + nb * ksz, KB, k - 3);
-              if (k - 2 < nchunks) scn.load(xs, KB, s_row[nb], k - 2);
+          for (int mi = 0; mi < MI; ++mi) {
+            const int c = mi & 1;
+            if (mi + 1 < MI) fetch(mi + 1, c ^ 1);
+            const f32x4 part0 = mfma_k128(a[c], bg), part1 = mfma_k128(a[c], bu);
+            // One combined scale per output row and K block (token scale x
+            // weight scale), so each MFMA output needs a single FMA.
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc[mi][0][r] = fmaf(part0[r], sa[c][r] * g, acc[mi][0][r]);
+              acc[mi][1][r] = fmaf(part1[r], sa[c][r] * u, acc[mi][1][r]);
             }
           }
-          // Block k + kPD of this item, or block k + kPD - KBP of the next,
-          // goes to stage d of both rings.
-          const int blk = k + kPD;
-          const bool own = blk < KBP || !more;
-          const int kr = own ? (blk < KB ? blk : KB - 1) : blk - KBP;
-          ar.load(d, xq, own ? cb : nb, kr);
-          if (k < KB) compute(s_a[k & 1], b[d], k);
-          load_b(b[d], own ? wb_cur : wb_nxt, kr);
-          ar.store((d + 1) % kPD, s_a[(k + 1) & 1]);
-          __syncthreads();
         }
+        st = st == kRing - 1 ? 0 : st + 1;
       }
 
       // 128 columns: one whole scale group of the activations, so they are
       // quantised here (s = max(max |a|, 1e-10) / 448, q = rne(clamp(a / s)),
       // the rule gemm2_narrow_kernel applies, on the same bf16 values). The
-      // bf16 values go through LDS one subtile at a time, so the
-      // accumulators die as they are converted (the operand rings still hold
-      // the next item's first blocks).
+      // fp8 rows are staged in the A stage of the last step, which no load
+      // targets before the next item's first step writes them out.
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float g = bf16_round(acc[mi][0][r]), u = bf16_round(acc[mi][1][r]);
-          const float a = bf16_round(g / (1.0f + expf(-g)) * u);
-          const int row = 16 * mi + 4 * q + r;
-          s_a16[row * kKB + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(a));
+          const float gv = bf16_round(acc[mi][0][r]), uv = bf16_round(acc[mi][1][r]);
+          const float a = bf16_round(gv / (1.0f + expf(-gv)) * uv);
+          acc[mi][0][r] = a;
           float m = fabsf(a);
 #pragma unroll
           for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
-          if (j == 0) s_m[wave][row] = m;
+          if (j == 0) s_m[wave][16 * mi + 4 * q + r] = m;
         }
       }
-      __syncthreads();
+      lds_barrier();  // s_m; and every wave is done with the last stage
       if (tid < 16 * MI) {
         float m = s_m[0][tid];
 #pragma unroll
         for (int w = 1; w < NW; ++w) m = fmaxf(m, s_m[w][tid]);
-        const float qs = quant_scale(m);
-        s_q[tid] = qs;
-        const int p = s_pair[cb][tid];
-        if (p >= 0) work.acts[static_cast<int64_t>(p) * (I / kKB) + c0 / kKB] = qs;
+        s_q[tid] = quant_scale(m);
       }
-      __syncthreads();
-      // 16 values (one 16-byte fp8 piece) per thread: 8 threads per row.
-      for (int i = tid; i < 16 * MI * (kKB / 16); i += NT) {
-        const int row = i / (kKB / 16), piece = i - row * (kKB / 16);
-        const int p = s_pair[cb][row];
-        if (p < 0) continue;
-        const float sq = s_q[row];
-        const u32x4* src = reinterpret_cast<const u32x4*>(s_a16 + row * kKB + piece * 16);
-        u32x4 o;
+      lds_barrier();
+      uint8_t* stg = s_a[st == 0 ? kRing - 1 : st - 1];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const u32x4 v = src[h];
+      for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const uint32_t pk = v[2 * e + t];
-              word |= to_fp8(clamp_fp8(bf16_value(pk & 0xffffu) / sq)) << (16 * t);
-              word |= to_fp8(clamp_fp8(bf16_value(pk >> 16) / sq)) << (16 * t + 8);
-            }
-            o[2 * h + e] = word;
-          }
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mi + 4 * q + r;
+          stg[row * kRowB + 16 * wave + j] = static_cast<uint8_t>(to_fp8(clamp_fp8(acc[mi][0][r] / s_q[row])));
         }
-        *reinterpret_cast<u32x4*>(work.act + static_cast<int64_t>(p) * I + c0 + piece * 16) = o;
       }
     });
+    out_cb = cb;
+    out_c0 = cur.col * NC;
+    out_rows = 16 * nmi;
     if (!more) break;
     cur = nxt;
-    nxt = item_get(m2, n, ncols);
+    nxt = after;
     ++n;
     cb = nb;
+    ao_cur = ao_nxt;
   }
+  lds_barrier();
+  copy_out(s_a[st == 0 ? kRing - 1 : st - 1]);
+  // The last steps requested blocks that nothing reads: let them land before
+  // the workgroup's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Operands of one K block of a 16-row subtile for one wave: the A rows (the
@@ -1381,74 +1375,93 @@ __global__ void __launch_bounds__(kThreads) gemm2_narrow_kernel(int64_t H, int64
   }
 }
 
-// GEMM2 at prefill sizes: down projection of 128 output columns of a wide
+// GEMM2 at prefill sizes: down projection of 128 TB output columns of a wide
 // tile per item, times the routed weight, bf16 rows per pair. Each of the 8
-// waves owns 16 columns and runs the K blocks in order over the tile's fp8
-// activations, staged in LDS one block ahead; persistent over items as
-// gemm1_kernel. Dynamic LDS: the activation scales of two items,
-// 2 x (I / 128) x kWM floats.
-constexpr int kWideNW2 = 8;
-
-__global__ void __launch_bounds__(kWideNW2 * 64) gemm2_kernel(int64_t H, int64_t I,
-                                                              const float* __restrict__ topk_weight,
-                                                              const uint8_t* __restrict__ w2,
-                                                              const float* __restrict__ w2_scale,
-                                                              const int32_t* __restrict__ pairs,
-                                                              const int32_t* __restrict__ wide, int64_t wmax,
-                                                              Work work, uint16_t* __restrict__ out) {
-  constexpr int NT = kWideNW2 * 64;
-  static_assert(kWideNW2 * 16 == kBN, "the waves cover one 128-column block");
-  extern __shared__ __attribute__((aligned(16))) float s_as[];  // [2 items][K block][row] activation scales
+// waves owns 16 TB columns and runs the K blocks in order over the tile's
+// fp8 activations; persistent over items through the operand ring as
+// gemm1_kernel.
+template <int TB>
+__global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64_t I,
+                                                               const float* __restrict__ topk_weight,
+                                                               const uint8_t* __restrict__ w2,
+                                                               const float* __restrict__ w2_scale,
+                                                               const int32_t* __restrict__ pairs,
+                                                               const int32_t* __restrict__ wide, int64_t wmax,
+                                                               int64_t npairs, Work work, uint16_t* __restrict__ out) {
+  constexpr int NW = kGemmWaves, NT = NW * 64, NC = NW * 16 * TB;  // output columns per item
+  constexpr int kOps = 2 * TB + 2 + 1;
+  constexpr int kStageRows = 64;  // output rows staged per epilogue round: 64 x NC bf16 = one weight stage
+  static_assert(kStageRows * NC * 2 == NC * kRowB, "an epilogue round fills one weight stage");
+  __shared__ __attribute__((aligned(16))) uint8_t s_b[kRing][NC * kRowB];
+  __shared__ __attribute__((aligned(16))) uint8_t s_a[kRing][kWM * kRowB];
+  __shared__ __attribute__((aligned(16))) float s_s[kRing][kWM];
+  __shared__ int s_pn[kWM];
   __shared__ int s_row[2][kWM];
   __shared__ int s_pair[2][kWM];
   __shared__ float s_w[2][kWM];
-  __shared__ float s_sw[2][kMaxKB];  // weight scales per K block of the item's 128-column block
-  __shared__ __attribute__((aligned(16))) uint8_t s_a[2][kWM * kAPitch];  // A stages
-  __shared__ __attribute__((aligned(16))) uint16_t s_o[kWM * kBN];        // output rows of an item
+  __shared__ float s_sw[2][2 * kMaxKB];  // weight scales per 128-row block (of TB) and K block, two items
 
-  const int ncols = static_cast<int>(H / kBN);
+  const int ncols = static_cast<int>(H / NC);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
-  const int KB = static_cast<int>(I / kKB), KBP = padded_blocks(KB);
-  const int nchunks = (KB * kWM + ScaleChunk<NT>::kFloats - 1) / ScaleChunk<NT>::kFloats;
-  const int64_t ksz = static_cast<int64_t>(KB) * kWM;
+  const int KB = static_cast<int>(I / kKB), KS = KB > kMinSteps ? KB : kMinSteps;
 
-  Item cur = item_get(item_request(0, ncols, wide, wmax), 0, ncols);
+  Item cur = item_fetch(0, ncols, wide, wmax);
   if (cur.count == 0) return;
-  Item nxt = item_get(item_request(1, ncols, wide, wmax), 1, ncols);
+  Item nxt = item_fetch(1, ncols, wide, wmax);
   int n = 2;
 
-  const int64_t boff = static_cast<int64_t>(16 * wave + j) * I + 32 * q;
+  // Weight-row loads: load i of a wave covers its stage rows 8i .. 8i + 7,
+  // output columns 16 TB wave + 8i + lane / 8 of the item.
+  uint32_t boff[2 * TB];
+#pragma unroll
+  for (int i = 0; i < 2 * TB; ++i)
+    boff[i] = static_cast<uint32_t>((16 * TB * wave + 8 * i + (lane >> 3)) * I + 16 * swizzled_piece(lane));
   auto wbase = [&](const Item& it) {
-    return w2 + (static_cast<int64_t>(it.slot) * H + static_cast<int64_t>(it.col) * kBN) * I + boff;
+    return w2 + (static_cast<int64_t>(it.slot) * H + static_cast<int64_t>(it.col) * NC) * I;
   };
-  auto weight_scale = [&](const Item& it, int kb) {
-    return w2_scale[(static_cast<int64_t>(it.slot) * (H / kKB) + it.col) * KB + kb];
-  };
-
-  u32x4 b[kPD][2];
-  ARing<NT, kPD> ar;
-  {
-    const uint8_t* wb = wbase(cur);
-#pragma unroll
-    for (int d = 0; d < kPD; ++d) load32(wb + (d < KB ? d : KB - 1) * kKB, b[d]);
-    put_rows(cur, item_pair(cur, pairs), 1, s_pair[0], s_row[0]);
-    __syncthreads();
-    for (int c = 0; c < nchunks; ++c) {
-      ScaleChunk<NT> sc;
-      sc.load(work.acts, KB, s_row[0], c);
-      sc.store(s_as, KB, c);
+  // Weight scales (TB 128-row blocks of w2 x KB) and routed weights of an
+  // item into LDS, by waves 0 and 1; the rows s_row must be in place.
+  auto request_scales = [&](const Item& it, const int* rows, float* sw, float* wt) {
+    if (wave < 2) {
+      const int i = tid < TB * KB ? tid : TB * KB - 1;
+      const int t = i / KB, kb = i - t * KB;
+      dma4(w2_scale, static_cast<uint32_t>(4 * ((static_cast<int64_t>(it.slot) * (H / kKB) + it.col * TB + t) * KB + kb)),
+           sw + 64 * wave);
+      dma4(topk_weight, static_cast<uint32_t>(4 * rows[tid]), wt + 64 * wave);
     }
-    if (tid < kWM) s_w[0][tid] = s_pair[0][tid] >= 0 ? topk_weight[s_pair[0][tid]] : 0.f;
-    if (tid < KB) s_sw[0][tid] = weight_scale(cur, tid);
-    ar.init(0, I, s_row[0]);
+  };
+  auto issue = [&](int stage, const uint8_t* wb, const AOffsets& ao, int kb) {
+    const uint8_t* bsrc = wb + kb * kRowB;
 #pragma unroll
-    for (int d = 0; d < kPD; ++d) ar.load(d, work.act, 0, d < KB ? d : KB - 1);
-    __syncthreads();
-    ar.store(0, s_a[0]);
-    __syncthreads();
-  }
+    for (int i = 0; i < 2 * TB; ++i) dma16(bsrc, boff[i], s_b[stage] + (16 * TB * wave + 8 * i) * kRowB);
+    const uint8_t* asrc = work.act + kb * kRowB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(asrc, ao.a[i], s_a[stage] + (16 * wave + 8 * i) * kRowB);
+    dma4(work.acts + kb, ao.s, &s_s[stage][64 * (wave & 1)]);
+  };
+  // Output rows [r0, r0 + rows) of an item, staged in LDS.
+  int out_cb = 0, out_n0 = 0, out_r0 = 0, out_rows = 0;
+  auto copy_out = [&](const uint16_t* stg) {
+    for (int i = tid; i < out_rows * (NC / 8); i += NT) {
+      const int rr = i / (NC / 8), piece = i - rr * (NC / 8);
+      const int p = s_pair[out_cb][out_r0 + rr];
+      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + out_n0 + piece * 8) =
+          *reinterpret_cast<const u32x4*>(stg + rr * NC + piece * 8);
+    }
+  };
 
+  request_pairs(cur, pairs, s_pn);
+  ring_barrier<0>();
+  put_rows(cur, s_pn, 1, npairs, s_pair[0], s_row[0]);
+  lds_barrier();
+  request_scales(cur, s_row[0], s_sw[0], s_w[0]);
+  AOffsets ao_cur = a_offsets(s_row[0], I, KB), ao_nxt = ao_cur;
+  ring_barrier<0>();
+  issue(0, wbase(cur), ao_cur, 0);
+  issue(1, wbase(cur), ao_cur, KB > 1 ? 1 : 0);
+
+  int st = 0;
   int cb = 0;
   for (;;) {
     const int nb = cb ^ 1;
@@ -1456,94 +1469,108 @@ __global__ void __launch_bounds__(kWideNW2 * 64) gemm2_kernel(int64_t H, int64_t
     const uint8_t* wb_cur = wbase(cur);
     const uint8_t* wb_nxt = more ? wbase(nxt) : wb_cur;
     const int nmi = (cur.count + 15) >> 4;
-    const int n0 = cur.col * kBN;
-    const float* as_cur = s_as + cb * ksz;
-    int pn = 0, m2 = 0;
-    float swn = 0.f, wn = 0.f;
-    ScaleChunk<NT> scn;
+    const int n0 = cur.col * NC;
+    Item after = nxt;
 
     with_subtiles(nmi, [&](auto nmi_c) {
       constexpr int MI = decltype(nmi_c)::value;
-      f32x4 acc[MI];
+      f32x4 acc[MI][TB];
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi) acc[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
-      auto compute = [&](const uint8_t* sa_buf, const u32x4 (&bb)[2], int kb) {
-        const float w = s_sw[cb][kb];
-        u32x4 a[2][2];  // operands of subtiles mi and mi + 1, as in gemm1_kernel
-        f32x4 sa[2];
-        auto fetch = [&](int mi, int slot) {
-          read_a(sa_buf, 16 * mi + j, q, a[slot]);
-          sa[slot] = *reinterpret_cast<const f32x4*>(as_cur + kb * kWM + 16 * mi + 4 * q);
-        };
-        fetch(0, 0);
+      for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int mi = 0; mi < MI; ++mi) {
-          const int c = mi & 1;
-          if (mi + 1 < MI) fetch(mi + 1, c ^ 1);
-          const f32x4 part = mfma_k128(a[c], bb);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mi][r] = fmaf(part[r], sa[c][r] * w, acc[mi][r]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      };
+        for (int t = 0; t < TB; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-      for (int kb = 0; kb < KBP; kb += kPD) {
+      for (int k = 0; k < KS; ++k) {
+        ring_barrier<kOps>();
+        const int sn = st == 0 ? kRing - 1 : st - 1;
+        if (k == 0 && out_rows > 0) {
+          copy_out(reinterpret_cast<const uint16_t*>(s_b[sn]));
+          out_rows = 0;
+          lds_barrier();
+        }
+        if (more) {
+          if (k == 0) {
+            request_pairs(nxt, pairs, s_pn);
+            after = item_fetch(n, ncols, wide, wmax);
+          } else if (k == 1) {
+            put_rows(nxt, s_pn, 1, npairs, s_pair[nb], s_row[nb]);
+          } else if (k == 2) {
+            ao_nxt = a_offsets(s_row[nb], I, KB);
+            request_scales(nxt, s_row[nb], s_sw[nb], s_w[nb]);
+          }
+        }
+        const int blk = k + kAhead;
+        if (blk < KS || !more)
+          issue(sn, wb_cur, ao_cur, blk < KB ? blk : KB - 1);
+        else
+          issue(sn, wb_nxt, ao_nxt, blk - KS < KB ? blk - KS : KB - 1);
+        if (k < KB) {
+          const float w = s_sw[cb][(TB * wave / 8) * KB + k];
+          u32x4 b[TB][2];
 #pragma unroll
-        for (int d = 0; d < kPD; ++d) {
-          const int k = kb + d;
-          if (more) {
-            if (k == 0) {
-              pn = item_pair(nxt, pairs);
-              m2 = item_request(n, ncols, wide, wmax);
-            } else if (k == 1) {
-              put_rows(nxt, pn, 1, s_pair[nb], s_row[nb]);
-            } else {
-              if (k == 2) {
-                ar.init(nb, I, s_row[nb]);
-                swn = tid < KB ? weight_scale(nxt, tid) : 0.f;
-                wn = tid < kWM && s_pair[nb][tid] >= 0 ? topk_weight[s_pair[nb][tid]] : 0.f;
-              } else if (k == 3) {
-                if (tid < KB) s_sw[nb][tid] = swn;
-                if (tid < kWM) s_w[nb][tid] = wn;
-              }
-              if (k - 3 >= 0 && k - 3 < nchunks) scn.store(s_as + nb * ksz, KB, k - 3);
-              if (k - 2 < nchunks) scn.load(work.acts, KB, s_row[nb], k - 2);
+          for (int t = 0; t < TB; ++t) read_frag(s_b[st], 16 * TB * wave + 16 * t + j, q, b[t]);
+          u32x4 a[2][2];
+          f32x4 sa[2];
+          auto fetch = [&](int mi, int slot) {
+            read_frag(s_a[st], 16 * mi + j, q, a[slot]);
+            sa[slot] = *reinterpret_cast<const f32x4*>(&s_s[st][16 * mi + 4 * q]);
+          };
+          fetch(0, 0);
+#pragma unroll
+          for (int mi = 0; mi < MI; ++mi) {
+            const int c = mi & 1;
+            if (mi + 1 < MI) fetch(mi + 1, c ^ 1);
+#pragma unroll
+            for (int t = 0; t < TB; ++t) {
+              const f32x4 part = mfma_k128(a[c], b[t]);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[mi][t][r] = fmaf(part[r], sa[c][r] * w, acc[mi][t][r]);
             }
           }
-          const int blk = k + kPD;
-          const bool own = blk < KBP || !more;
-          const int kr = own ? (blk < KB ? blk : KB - 1) : blk - KBP;
-          ar.load(d, work.act, own ? cb : nb, kr);
-          if (k < KB) compute(s_a[k & 1], b[d], k);
-          load32((own ? wb_cur : wb_nxt) + kr * kKB, b[d]);
-          ar.store((d + 1) % kPD, s_a[(k + 1) & 1]);
-          __syncthreads();
         }
+        st = st == kRing - 1 ? 0 : st + 1;
       }
 
+      // bf16(acc x routed weight), staged 64 rows at a time in the weight
+      // stage of the last step (no load targets it before the next item's
+      // first step); the last round is written out at that step.
+      uint16_t* stg = reinterpret_cast<uint16_t*>(s_b[st == 0 ? kRing - 1 : st - 1]);
+      constexpr int kRounds = (MI + kStageRows / 16 - 1) / (kStageRows / 16);
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 16 * mi + 4 * q + r;
-          s_o[row * kBN + 16 * wave + j] = static_cast<uint16_t>(bf16_bits(acc[mi][r] * s_w[cb][row]));
+      for (int rd = 0; rd < kRounds; ++rd) {
+        const int r0 = rd * kStageRows;
+        if (rd > 0) {  // an earlier round: written out now
+          lds_barrier();
+          copy_out(stg);
         }
+        lds_barrier();  // every wave is done with the last stage, or with the previous round
+#pragma unroll
+        for (int mi = rd * (kStageRows / 16); mi < MI && mi < (rd + 1) * (kStageRows / 16); ++mi) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * mi + 4 * q + r;
+            const float wgt = s_w[cb][row];
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+              stg[(row - r0) * NC + 16 * TB * wave + 16 * t + j] = static_cast<uint16_t>(bf16_bits(acc[mi][t][r] * wgt));
+          }
+        }
+        out_cb = cb;
+        out_n0 = n0;
+        out_r0 = r0;
+        out_rows = cur.count - r0 < kStageRows ? cur.count - r0 : kStageRows;
       }
     });
-    __syncthreads();
-    // 256 bytes per row: 16 threads x 16 bytes, 32 rows per pass.
-    for (int row = tid >> 4; row < cur.count; row += NT / 16) {
-      const int p = s_pair[cb][row];
-      const int col = (tid & 15) * 8;
-      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(p) * H + n0 + col) =
-          *reinterpret_cast<const u32x4*>(s_o + row * kBN + col);
-    }
     if (!more) break;
     cur = nxt;
-    nxt = item_get(m2, n, ncols);
+    nxt = after;
     ++n;
     cb = nb;
+    ao_cur = ao_nxt;
   }
+  lds_barrier();
+  copy_out(reinterpret_cast<const uint16_t*>(s_b[st == 0 ? kRing - 1 : st - 1]));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // out[t] = bf16(sum over k of contrib[t*topk + k]) in fp32, k ascending,
@@ -1737,17 +1764,22 @@ int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
     const int64_t wmax = wide_bound(npairs, slots);
     const int32_t* wide = tiles + wide_list_offset(npairs, slots);
     const int64_t per_xcd_tiles = (wmax + 7) / 8;  // wide tiles of one XCD, at most
-    // One workgroup per CU: their registers allow no more.
-    const int64_t n1 = std::min<int64_t>(per_xcd, per_xcd_tiles * (I / (16 * kWideNW)));
-    const int64_t n2 = std::min<int64_t>(per_xcd, per_xcd_tiles * (H / kBN));
-    hipLaunchKernelGGL(gemm1_kernel<kWideNW>, dim3(static_cast<unsigned>(8 * n1)), dim3(64 * kWideNW),
-                       static_cast<size_t>(2 * kWM * (H / kKB)) * sizeof(float), as_stream(stream), xq, xs, H, I,
-                       static_cast<int>(topk), w13, w13_scale, pairs, wide, wmax, w);
+    // One workgroup per CU: the operand ring takes most of its LDS.
+    const int64_t n1 = std::min<int64_t>(per_xcd, per_xcd_tiles * (I / (16 * kGemmWaves)));
+    hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(8 * n1)), dim3(64 * kGemmWaves), 0,
+                       as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, pairs, wide, wmax, npairs, w);
     rc = check_launch("gemm1_kernel");
     if (rc) return rc;
-    hipLaunchKernelGGL(gemm2_kernel, dim3(static_cast<unsigned>(8 * n2)), dim3(64 * kWideNW2),
-                       static_cast<size_t>(2 * kWM * (I / kKB)) * sizeof(float), as_stream(stream), H, I, topk_weight,
-                       w2, w2_scale, pairs, wide, wmax, w, out);
+    // 256 output columns per item where H allows, else 128.
+    if (H % (2 * kBN) == 0) {
+      const int64_t n2 = std::min<int64_t>(per_xcd, per_xcd_tiles * (H / (2 * kBN)));
+      hipLaunchKernelGGL(gemm2_kernel<2>, dim3(static_cast<unsigned>(8 * n2)), dim3(64 * kGemmWaves), 0,
+                         as_stream(stream), H, I, topk_weight, w2, w2_scale, pairs, wide, wmax, npairs, w, out);
+    } else {
+      const int64_t n2 = std::min<int64_t>(per_xcd, per_xcd_tiles * (H / kBN));
+      hipLaunchKernelGGL(gemm2_kernel<1>, dim3(static_cast<unsigned>(8 * n2)), dim3(64 * kGemmWaves), 0,
+                         as_stream(stream), H, I, topk_weight, w2, w2_scale, pairs, wide, wmax, npairs, w, out);
+    }
     return check_launch("gemm2_kernel");
   }
   const int64_t tiles8 = (bound + 7) / 8 * 8;  // the XCD-aware grids cover whole groups of 8 tiles
