@@ -217,6 +217,49 @@ def test_full_size_expert_rows():
                                       raws[k][:2])
 
 
+def test_headline_launch_256_experts():
+    """The headline decode launch at its full size: 256 experts (w13 1024x2048
+    and w2 2048x512 fp8 rows, N(0, 0.02) weights with 128x128 block scales),
+    encoded on the GPU at pitch 0.89 and expanded in one launch of 6144
+    workgroups; every byte equals the raw rows. On a sample the GPU records
+    equal the host encoder's and the oracle decodes them to the same rows."""
+    codec = _codec()
+    dev = torch.device("cuda")
+    count = 256
+    g = torch.Generator(device=dev).manual_seed(1234)
+    raws = []
+    for r, c in ((1024, 2048), (2048, 512)):
+        rows = torch.empty((count, r * c), dtype=torch.uint8, device=dev)
+        for j in range(count):
+            w = torch.randn((r, c), generator=g, device=dev) * 0.02
+            blk = w.view(r // 128, 128, c // 128, 128)
+            scale = blk.abs().amax(dim=(1, 3), keepdim=True).clamp(min=1e-12) / 448.0
+            rows[j] = (blk / scale).to(torch.float8_e4m3fn).view(torch.uint8).reshape(-1)
+        raws.append(rows)
+    stg, luts = [], []
+    for r in raws:
+        rec, lut, _ = codec.encode_rows(r, codec.pitch_of(r.shape[1], 0.89, 4096))
+        stg.append(rec)
+        luts.append(lut)
+    lut = torch.stack(luts, dim=1).contiguous()  # (E, names, 512)
+    dst = [torch.zeros_like(r) for r in raws]
+    todo = torch.arange(count, dtype=torch.int64, device=dev)
+    cache_row = torch.full((count,), -1, dtype=torch.int64, device=dev)
+    codec.decode_rows(todo, todo.clone(), cache_row, stg, dst, lut)
+    torch.cuda.synchronize()
+    for k in range(2):
+        assert torch.equal(dst[k], raws[k]), f"name {k}"
+    for k in range(2):
+        for j in (0, 137, count - 1):
+            raw = raws[k][j].cpu().numpy()
+            rec = np.empty(stg[k].shape[1], np.uint8)
+            lut_h = np.empty(512, np.uint8)
+            codec.encode_into(raw, rec, lut_h)
+            np.testing.assert_array_equal(stg[k][j].cpu().numpy(), rec)
+            np.testing.assert_array_equal(luts[k][j].cpu().numpy(), lut_h)
+            np.testing.assert_array_equal(codec_ref.decode_fast(rec[None], lut_h[None], raw.size)[0], raw)
+
+
 def test_decode_in_graph_replays():
     codec = _codec()
     dev = torch.device("cuda")
