@@ -392,20 +392,20 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)p));
 }
-// One piece per lane from global memory into LDS: lane l's 16 (4) bytes, at
-// base + off, land at dst + 16 l (4 l); base and dst are the same for the
-// whole wave. Written in assembly so that the compiler does not track these
-// loads: it would make every LDS access wait for all of them. M0 (the LDS
-// destination) is restored afterwards.
-// The readfirstlane builtin returns int: each half is taken as uint32_t
-// before widening, or a low half with bit 31 set would sign-extend into the
-// high half.
+// A wave-uniform 64-bit address in scalar registers. The readfirstlane
+// builtin returns int: each half is taken as uint32_t before widening, or a
+// low half with bit 31 set would sign-extend into the high half.
 __device__ __forceinline__ uint64_t uniform_ptr(const void* p) {
   const uint64_t v = reinterpret_cast<uint64_t>(p);
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v)));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32)));
   return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
 }
+// One piece per lane from global memory into LDS: lane l's 16 (4) bytes, at
+// base + off (scalar base, 32-bit vector offset), land at dst + 16 l (4 l);
+// base and dst are the same for the whole wave. Written in assembly so that
+// the compiler does not track these loads: it would make every LDS access
+// wait for all of them. M0 (the LDS destination) is restored afterwards.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, void* dst) {
   uint32_t saved;
   asm volatile(
