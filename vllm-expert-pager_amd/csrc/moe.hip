@@ -1009,6 +1009,9 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
   const bool by_token = ntok <= 16;
   if (wave == 0) {
     const DecodeRoute r = decode_route(lane, npairs, ids, eb, expert_map, E, slots);
+    // gemm2_decode_kernel reads the pairs' slots from the workspace (the
+    // activation-scale region, which the decode path does not use).
+    if (blockIdx.x == 0 && lane < npairs) reinterpret_cast<int32_t*>(work.acts)[lane] = r.slot;
     s_slot[lane] = r.slot;
     s_pos[lane] = r.pos;
     s_tile[lane] = r.tile;
@@ -1134,18 +1137,18 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
 // every row of the MFMA operand, kNarrowChunk K blocks of weight rows per
 // load) and rounded to bf16; then the contributions are summed in k order
 // in fp32 and rounded once, as topk_sum_kernel does. A token's experts are
-// distinct slots, so its pairs share no weights. Pairs whose id is outside
-// [0, E) add nothing; so do pairs without a slot (the separate calls would
-// read a contribution never written).
+// distinct slots, so its pairs share no weights. The pairs' slots come from
+// gemm1_decode_kernel's routing through the workspace, one load instead of
+// the ids and expert_map lookups. Pairs whose id is outside [0, E) add
+// nothing; so do pairs without a slot (the separate calls would read a
+// contribution never written).
 __global__ void __launch_bounds__(kThreads) gemm2_decode_kernel(
-    int64_t H, int64_t I, int topk, const void* ids, int eb, const int32_t* __restrict__ expert_map, int E,
-    int slots, const float* __restrict__ topk_weight, const uint8_t* __restrict__ w2,
+    int64_t H, int64_t I, int topk, const float* __restrict__ topk_weight, const uint8_t* __restrict__ w2,
     const float* __restrict__ w2_scale, Work work, uint16_t* __restrict__ out) {
   extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];  // [topk][I] fp8 activations
   __shared__ int s_slot[kDecodePairs];
   __shared__ float s_as[kDecodePairs * 4];  // activation scales [pair][K block], K blocks of a round
   __shared__ uint16_t s_c[kDecodePairs][16];
-  __shared__ int s_ok[kDecodePairs];
 
   const int ncol = static_cast<int>(H / 16);
   const int t = static_cast<int>(blockIdx.x) / ncol, n0 = (static_cast<int>(blockIdx.x) - t * ncol) * 16;
@@ -1154,13 +1157,9 @@ __global__ void __launch_bounds__(kThreads) gemm2_decode_kernel(
   const int KB = static_cast<int>(I / kKB);
   const int64_t p0 = static_cast<int64_t>(t) * topk;
 
-  if (tid < topk) {
-    const int64_t e = load_id(ids, eb, p0 + tid);
-    const bool valid = e >= 0 && e < E;
-    const int sl = valid ? expert_map[e] : -1;
-    s_slot[tid] = sl >= 0 && sl < slots ? sl : -1;
-    s_ok[tid] = valid;
-  }
+  // The pairs' slots as gemm1_decode_kernel routed them (-1: an invalid id
+  // or an expert without a slot, which adds nothing).
+  if (tid < topk) s_slot[tid] = reinterpret_cast<const int32_t*>(work.acts)[p0 + tid];
   // The pairs' activations quantised into LDS, 8 columns per item, as
   // gemm2_narrow_kernel quantises them (a 128-column group's scale from its
   // eight 16-column maxima).
@@ -1249,7 +1248,7 @@ __global__ void __launch_bounds__(kThreads) gemm2_decode_kernel(
   if (tid < 16) {
     float sum = 0.f;
     for (int k = 0; k < topk; ++k)
-      if (s_ok[k] && s_slot[k] >= 0) sum += bf16_value(s_c[k][tid]);
+      if (s_slot[k] >= 0) sum += bf16_value(s_c[k][tid]);
     out[static_cast<int64_t>(t) * H + n0 + tid] = static_cast<uint16_t>(bf16_bits(sum));
   }
 }
@@ -1914,8 +1913,7 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
   int rc = check_launch("gemm1_decode_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(gemm2_decode_kernel, dim3(static_cast<unsigned>(T * (H / 16))), dim3(kThreads),
-                     static_cast<size_t>(topk * I), as_stream(stream), H, I, static_cast<int>(topk), topk_ids,
-                     topk_elem_bytes, expert_map, static_cast<int>(num_experts), static_cast<int>(slots), topk_weight,
+                     static_cast<size_t>(topk * I), as_stream(stream), H, I, static_cast<int>(topk), topk_weight,
                      w2, w2_scale, w, out);
   return check_launch("gemm2_decode_kernel");
 }
