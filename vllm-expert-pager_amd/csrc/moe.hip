@@ -71,6 +71,18 @@ __device__ __forceinline__ float quant_scale(float amax) { return fmaxf(amax, kE
 
 __device__ __forceinline__ float clamp_fp8(float v) { return fminf(fmaxf(v, -kFp8Max), kFp8Max); }
 
+// The maximum of v over the 16 lanes of its DPP row (lanes 16r .. 16r + 15):
+// quad swaps at lane distance 1 and 2, then the half-row and row mirrors,
+// each a DPP operand of v_max, with no LDS round trip. Max is exact and
+// order-free, so this equals a butterfly over lane distances 1, 2, 4 and 8.
+// Every lane of the row must be active.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));   // quad [1,0,3,2]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));   // quad [2,3,0,1]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));  // row_half_mirror
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)));  // row_mirror
+}
+
 // 16x16 output tile = A[16][128] . B[128][16] in fp8 e4m3. Lane l = 16q + j
 // supplies 32 bytes of A row j and of B column j at K offset 32q; the
 // instruction maps the bytes of A and B to K in the same way, so the dot
@@ -107,8 +119,7 @@ __device__ __forceinline__ void quant_token(const uint16_t* __restrict__ x, int6
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+    amax = row16_max(amax);
     const float s = quant_scale(amax);
     uint32_t q0 = 0, q1 = 0;
 #pragma unroll
@@ -698,8 +709,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
           const float a = bf16_round(gv / (1.0f + expf(-gv)) * uv);
           acc[mi][0][r] = a;
           float m = fabsf(a);
-#pragma unroll
-          for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+          m = row16_max(m);
           if (j == 0) s_m[wave][16 * mi + 4 * q + r] = m;
         }
       }
@@ -883,8 +893,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
       const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
       const float a = bf16_round(g / (1.0f + expf(-g)) * u);
       float m = fabsf(a);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      m = row16_max(m);
       const int row = 4 * q + r;
       if (j == 0) s_m[row] = m;
       s_o[row * 16 + j] = static_cast<uint16_t>(bf16_bits(a));
@@ -990,8 +999,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 16));
+      amax = row16_max(amax);
       const float sc = quant_scale(amax);
       uint32_t q0 = 0, q1 = 0;
 #pragma unroll
@@ -1110,8 +1118,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
       const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
       const float a = bf16_round(g / (1.0f + expf(-g)) * u);
       float m = fabsf(a);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 16));
+      m = row16_max(m);
       const int row = 4 * q + r;
       if (j == 0) s_m[row] = m;
       s_o[row * 16 + j] = static_cast<uint16_t>(bf16_bits(a));
