@@ -810,6 +810,25 @@ def bench_model_decode(args, dev):
         pager.close()
 
 
+def bench_model_decode_compressed(args, dev):
+    """The decode trace of bench_model_decode with every expert in a compressed RAM tier (pitch
+    0.89, no paging file): each miss's record is expanded straight from pinned RAM by the decoder,
+    with no copy to staging first. A quarter of the raw trace's steps."""
+    from vllm_expert_pager import pager as pg
+
+    settings = pg.Settings(cache_slots=32, ram_slots=None, compress="on", working_rows=64, log_interval=0)
+    pager, layers, _ = build_paged_model(dev, settings)
+    steps = max(100, args.decode_steps // 4)
+    try:
+        return decode_trace(args, dev, pager, layers,
+                            "40-layer decode trace, 256 experts x 3 MiB, 32 cache slots, all experts in a RAM "
+                            "tier of rows compressed at pitch 0.89 (expanded straight from pinned RAM), batch 1, "
+                            f"top-8, Zipf(1.1) with 0.7 reuse, {steps} steps in one captured hipGraph per step",
+                            steps=steps)
+    finally:
+        pager.close()
+
+
 def disk_ceiling(path: str, record_bytes: int, records: int, seconds: float = 0.5) -> dict:
     """Record-sized O_DIRECT reads of the paging file at 1, 8 and 32 in flight, from a thread pool
     (the SSD server's way) and from io_uring: the disk's ceiling in this run."""
@@ -1011,6 +1030,7 @@ def main() -> None:
         extras["acquire"] = bench_acquire(args, dev)
         extras["moe"] = bench_moe(args, dev)
         extras["model_decode"] = bench_model_decode(args, dev)
+        extras["model_decode_compressed"] = bench_model_decode_compressed(args, dev)
         if not args.no_tiered:
             extras["tiered"] = bench_tiered(args, dev, args.tiered_decode_steps)
     line = {

@@ -182,7 +182,7 @@ int xp_fetch_rows(const int64_t* todo, int64_t K, int64_t num_experts,
                   int64_t base, int64_t layer, const xp_ring* ring,
                   void* stream);
 
-/* Publish without waiting; the published seq goes to ticket[1] (HBM).
+/* Publish without waiting; the published seq goes to ticket[0] (HBM).
  * Replaces fetch_publish_rows (gather.py:410-431). */
 int xp_fetch_publish_rows(const int64_t* todo, int64_t K,
                           int64_t num_experts, const int64_t* row,
@@ -233,6 +233,34 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts,
                    const uint8_t* lut,
                    const xp_decode_name* names, int num_names,
                    const int64_t* skip, int64_t chunk, void* stream);
+
+/* The scale rows that go with one weight name's records. */
+typedef struct xp_decode_scale {
+  const void* scale;      /* scale rows by expert: row e at scale + e * scale_bytes (HBM) */
+  void* scale_dst;        /* destination scale rows, by dst_row */
+  int64_t scale_bytes;    /* bytes per scale row, a positive multiple of 4 */
+  int64_t scale_rows;     /* at least num_experts */
+  int64_t scale_dst_rows; /* at least the name's dst_rows */
+} xp_decode_scale;
+
+/* xp_decode_rows reading the records straight from the RAM tier: the
+ * record of expert e = todo[j] is row src_row[e] + base of names[n].stg
+ * (the tier's device address, stg_rows rows; a row outside [0, stg_rows)
+ * is skipped, never clamped), and the expert's scale row is copied from
+ * scales[n].scale[e] to scales[n].scale_dst[dst_row[e]]. The decoder's
+ * ring loads then read the host link directly, so a decode step needs no
+ * gather of its misses into staging first. Experts with cache_row[e] >= 0
+ * are skipped entirely (records and scales), as are the other skips of
+ * xp_decode_rows. No counterpart in the reference, whose decode reads a
+ * staging copy (codec.py:297-327) that gather fills (gather.py:328-393);
+ * it is for callers that decode a few misses per step from pinned RAM. */
+int xp_decode_rows_from_ram(const int64_t* todo, int64_t K, int64_t num_experts,
+                            const int64_t* dst_row, const int64_t* cache_row,
+                            const int64_t* src_row, int64_t base,
+                            const uint8_t* lut,
+                            const xp_decode_name* names, int num_names,
+                            const xp_decode_scale* scales,
+                            const int64_t* skip, int64_t chunk, void* stream);
 
 /* Host encoder: compress raw[n] (n multiple of chunk*32) into record[pitch]
  * (zero padded) and lut[512]. *needed receives the record's used bytes.

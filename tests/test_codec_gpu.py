@@ -149,6 +149,108 @@ def test_follows_todo_and_skips():
         assert np.array_equal(dst[k][0].cpu().numpy(), raws[6][k])
 
 
+def _ram_tier(records_by_row, rows, pitch):
+    """A pinned RAM tier of `rows` records of `pitch` bytes (random bytes
+    where no record is placed) and its device view."""
+    from vllm_expert_pager.gather import DeviceRows
+    from vllm_expert_pager.store import PinnedBuffer
+
+    buf = PinnedBuffer(rows * pitch, coherent=False)
+    host = buf.tensor(torch.uint8, (rows, pitch))
+    host.copy_(torch.from_numpy(np.random.default_rng(rows).integers(0, 256, (rows, pitch), dtype=np.uint8)))
+    for r, rec in records_by_row.items():
+        host[r] = torch.from_numpy(rec)
+    return buf, DeviceRows(host, buf.device_ptr)
+
+
+def test_decode_from_ram_follows_rows_and_copies_scales():
+    """xp_decode_rows_from_ram: expert e's record is RAM-tier row
+    src_row[e] + base and its scale row goes to scale_dst[dst_row[e]];
+    todo -1 entries, cached experts, listed skips and record or destination
+    rows outside their tensors are skipped (records and scales alike)."""
+    codec = _codec()
+    dev = torch.device("cuda")
+    E, rows_ram, base = 10, 16, 4
+    ns = (N, N // 2)
+    pitches = [codec_ref.pitch_of(n, 1.25, 4096) for n in ns]
+    src_row = torch.tensor([0, 3, 7, -9, 9, 12, 2, 5, 8, 1], dtype=torch.int64)  # row - base per expert
+    dst_row = torch.tensor([0, 3, 1, 0, 5, 2, 0, 4, 0, 0], dtype=torch.int64)  # dst_rows = 5: expert 4 is outside
+    used = (1, 2, 4, 5, 7, 9)
+    raws = {e: [rows(200 + 10 * e + k, n) for k, n in enumerate(ns)] for e in used}
+    lut = torch.zeros((E, 2, 512), dtype=torch.uint8, device=dev)
+    placed = [{}, {}]
+    for e in used:
+        for k in range(2):
+            rec, lt = codec_ref.encode(raws[e][k], pitches[k], CHUNK)
+            lut[e, k] = torch.from_numpy(lt).to(dev)
+            r = base + int(src_row[e])
+            if 0 <= r < rows_ram:
+                placed[k][r] = rec
+    tiers = [_ram_tier(placed[k], rows_ram, pitches[k]) for k in range(2)]
+    words = (8, 4)
+    scale = [torch.randint(1, 2**30, (E, w), dtype=torch.int32, device=dev) for w in words]
+    scale_dst = [torch.zeros((5, w), dtype=torch.int32, device=dev) for w in words]
+    dst = [torch.zeros((5, n), dtype=torch.uint8, device=dev) for n in ns]
+    # 5: base + 12 = 16 is past the tier; 4: dst row 5 is past dst; 9: cached; 1: listed as skipped.
+    todo = torch.tensor([2, 7, 4, -1, 9, 1, 5], dtype=torch.int64, device=dev)
+    cache_row = torch.full((E,), -1, dtype=torch.int64, device=dev)
+    cache_row[9] = 0
+    skip = torch.tensor([1, -1, -1, -1, -1, -1, -1], dtype=torch.int64, device=dev)
+    src, ram = [t[1] for t in tiers], (src_row.to(dev), base)
+
+    def run(sk):
+        codec.decode_rows_from_ram(todo, dst_row.to(dev), cache_row, ram[0], ram[1], src, dst, lut, scale, scale_dst,
+                                   skip=sk, chunk=CHUNK)
+        torch.cuda.synchronize()
+
+    run(skip)
+    done = {2: 1, 7: 4}
+    for k in range(2):
+        for e, d in done.items():
+            np.testing.assert_array_equal(dst[k][d].cpu().numpy(), raws[e][k])
+            assert torch.equal(scale_dst[k][d], scale[k][e])
+        for d in set(range(5)) - set(done.values()):
+            assert not dst[k][d].any() and not scale_dst[k][d].any(), (k, d)
+    run(None)  # now expert 1 too
+    for k in range(2):
+        np.testing.assert_array_equal(dst[k][3].cpu().numpy(), raws[1][k])
+        assert torch.equal(scale_dst[k][3], scale[k][1])
+        for d in (0, 2):
+            assert not dst[k][d].any() and not scale_dst[k][d].any(), (k, d)
+
+
+def test_decode_from_ram_matches_staging_full_size():
+    """Full-size expert records read from shuffled RAM-tier rows give the
+    bytes the staging decoder gives (and the raw rows)."""
+    codec = _codec()
+    dev = torch.device("cuda")
+    count, base = 6, 3
+    raws, stg_np, luts_np = _expert_batch(codec, count, 41)
+    order = [4, 0, 5, 2, 1, 3]  # expert j's record sits at RAM row base + order[j]
+    rows_ram = base + count
+    tiers = [_ram_tier({base + order[j]: stg_np[k][j] for j in range(count)}, rows_ram, stg_np[k].shape[1])
+             for k in range(2)]
+    lut = torch.from_numpy(luts_np).to(dev)
+    todo = torch.arange(count, dtype=torch.int64, device=dev)
+    dst_row = torch.tensor([5, 3, 1, 0, 2, 4], dtype=torch.int64, device=dev)
+    cache_row = torch.full((count,), -1, dtype=torch.int64, device=dev)
+    src_row = torch.tensor(order, dtype=torch.int64, device=dev)
+    scale = [torch.arange(count * w, dtype=torch.int32, device=dev).view(count, w) for w in (128, 64)]
+    scale_dst = [torch.zeros_like(c) for c in scale]
+    a = [torch.zeros((count, r.shape[1]), dtype=torch.uint8, device=dev) for r in raws]
+    b = [torch.zeros_like(t) for t in a]
+    codec.decode_rows_from_ram(todo, dst_row, cache_row, src_row, base, [t[1] for t in tiers], a, lut, scale,
+                               scale_dst)
+    stg = [torch.from_numpy(s).to(dev) for s in stg_np]
+    codec.decode_rows(todo, dst_row, cache_row, stg, b, lut)
+    torch.cuda.synchronize()
+    for k in range(2):
+        assert torch.equal(a[k], b[k])
+        for j in range(count):
+            np.testing.assert_array_equal(a[k][int(dst_row[j])].cpu().numpy(), raws[k][j])
+            assert torch.equal(scale_dst[k][int(dst_row[j])], scale[k][j])
+
+
 @pytest.mark.parametrize("chunk", [64, 512])
 def test_garbage_records_stay_in_bounds(chunk):
     """Records and LUTs of random bytes (start words out of range, code

@@ -164,7 +164,7 @@ def test_paging_file_flushed_at_the_first_forward(model):
 
 
 def test_prefill_between_decode_steps_two_layers(model):
-    """Layers share the working slab (and its head as decode staging)."""
+    """Layers share the working slab; decode steps between prefills read the RAM tier."""
     m = model(64, 4, 16, 8, True, L=2)
     rng = np.random.default_rng(7)
     for step in range(12):

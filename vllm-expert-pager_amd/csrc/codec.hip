@@ -47,6 +47,9 @@ struct NameDev {
   int64_t N;
   int G;
   int blocks;  // workgroups per row for this name
+  const uint32_t* scale;  // reading the RAM tier: scale rows by expert, copied to
+  uint32_t* scale_dst;    // scale_dst[dst_row] (scale_words 4-byte words each)
+  int scale_words;
 };
 
 struct DecodeArgs {
@@ -61,6 +64,8 @@ struct DecodeArgs {
   const int64_t* skip;
   int chunk;
   int blocks_per_row;
+  const int64_t* src_row;  // non-null: expert e's record is stg row src_row[e] + base, else row j
+  int64_t base;
 };
 
 // Sign + mantissa of 8 values (one nibble word) in their output bytes:
@@ -352,11 +357,16 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   if (active && a.skip)
     for (int k = 0; k < a.K; ++k) active = active && a.skip[k] != e;
   if (!active || a.cache_row[e] >= 0) return;
-  // A destination row outside [0, dst_rows) is skipped, never clamped.
+  // A destination or record row outside its tensor is skipped, never clamped.
   const int64_t drow = a.dst_row[e];
-  if (drow < 0 || drow >= nm.dst_rows || j >= nm.stg_rows) return;
+  const int64_t srow = a.src_row ? a.src_row[e] + a.base : j;
+  if (drow < 0 || drow >= nm.dst_rows || srow < 0 || srow >= nm.stg_rows) return;
 
   const int tid = threadIdx.x;
+  // Read from the RAM tier, the name's first workgroup of the row also
+  // copies the expert's scale row, which a staging gather would have moved.
+  if (nm.scale && r == 0)
+    for (int i = tid; i < nm.scale_words; i += kThreads) nm.scale_dst[drow * nm.scale_words + i] = nm.scale[e * nm.scale_words + i];
   const uint8_t* lut = a.lut + (e * a.num_names + name) * XP_LUT_BYTES;
   // The row's 9-bit table (entry = symbol << 4 | length) as length |
   // (exponent field << 3) << 8. Lengths are clamped to [1, LIMIT], which
@@ -374,7 +384,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   const uint32_t half_shift = upper ? 16u : 0u;
   const int G = nm.G;
   const int msteps = a.chunk / 8;
-  const uint32_t* rec = reinterpret_cast<const uint32_t*>(nm.stg + int64_t(j) * nm.pitch);
+  const uint32_t* rec = reinterpret_cast<const uint32_t*>(nm.stg + srow * nm.pitch);
   const int64_t huff_off = (G + 1) + nm.N / 8;  // in words
   const int64_t maxw = nm.pitch / 4 - huff_off;
 
@@ -469,18 +479,21 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
 
 using namespace xp;
 
-extern "C" {
+namespace {
 
-int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const int64_t* dst_row,
-                   const int64_t* cache_row, const uint8_t* lut, const xp_decode_name* names, int num_names,
-                   const int64_t* skip, int64_t chunk, void* stream) {
-  XP_REQUIRE(K >= 0 && K <= (1 << 20), "xp_decode_rows: K=%lld", (long long)K);
-  XP_REQUIRE(num_names >= 1 && num_names <= 2 && names, "xp_decode_rows: %d names (1 or 2)", num_names);
-  XP_REQUIRE(chunk >= 32 && chunk % 32 == 0 && chunk <= 4096, "xp_decode_rows: chunk=%lld (multiple of 32)",
+// Shared by both decode entry points: src_row == nullptr reads staging row j
+// (no scales), else RAM-tier row src_row[e] + base and copies the scales.
+int launch_decode(const char* what, const int64_t* todo, int64_t K, int64_t num_experts, const int64_t* dst_row,
+                  const int64_t* cache_row, const int64_t* src_row, int64_t base, const uint8_t* lut,
+                  const xp_decode_name* names, int num_names, const xp_decode_scale* scales, const int64_t* skip,
+                  int64_t chunk, void* stream) {
+  XP_REQUIRE(K >= 0 && K <= (1 << 20), "%s: K=%lld", what, (long long)K);
+  XP_REQUIRE(num_names >= 1 && num_names <= 2 && names, "%s: %d names (1 or 2)", what, num_names);
+  XP_REQUIRE(chunk >= 32 && chunk % 32 == 0 && chunk <= 4096, "%s: chunk=%lld (multiple of 32)", what,
              (long long)chunk);
-  XP_REQUIRE(num_experts >= 1, "xp_decode_rows: num_experts=%lld", (long long)num_experts);
+  XP_REQUIRE(num_experts >= 1, "%s: num_experts=%lld", what, (long long)num_experts);
   if (K == 0) return XP_OK;
-  XP_REQUIRE(todo && dst_row && cache_row && lut, "xp_decode_rows: null index tensor");
+  XP_REQUIRE(todo && dst_row && cache_row && lut, "%s: null index tensor", what);
   DecodeArgs a{};
   a.todo = todo;
   a.K = static_cast<int>(K);
@@ -491,21 +504,21 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
   a.num_names = num_names;
   a.skip = skip;
   a.chunk = static_cast<int>(chunk);
+  a.src_row = src_row;
+  a.base = base;
   int per_row = 0;
   for (int n = 0; n < num_names; ++n) {
     const xp_decode_name& s = names[n];
     const int64_t group = chunk * XP_LANES;
-    XP_REQUIRE(s.row_bytes > 0 && s.row_bytes % group == 0,
-               "xp_decode_rows: name %d row of %lld values is not a multiple of %lld", n, (long long)s.row_bytes,
-               (long long)group);
+    XP_REQUIRE(s.row_bytes > 0 && s.row_bytes % group == 0, "%s: name %d row of %lld values is not a multiple of %lld",
+               what, n, (long long)s.row_bytes, (long long)group);
     const int64_t G = s.row_bytes / group;
-    XP_REQUIRE(s.pitch < (int64_t(1) << 31), "xp_decode_rows: name %d pitch %lld is 2 GiB or more", n,
-               (long long)s.pitch);
+    XP_REQUIRE(s.pitch < (int64_t(1) << 31), "%s: name %d pitch %lld is 2 GiB or more", what, n, (long long)s.pitch);
     XP_REQUIRE(s.pitch % 4 == 0 && s.pitch >= 4 * (G + 1) + s.row_bytes / 2,
-               "xp_decode_rows: name %d pitch %lld cannot hold the record header", n, (long long)s.pitch);
-    XP_REQUIRE(s.stg && s.dst, "xp_decode_rows: name %d has a null buffer", n);
+               "%s: name %d pitch %lld cannot hold the record header", what, n, (long long)s.pitch);
+    XP_REQUIRE(s.stg && s.dst, "%s: name %d has a null buffer", what, n);
     XP_REQUIRE(aligned16(s.stg) && aligned16(s.dst) && s.pitch % 16 == 0,
-               "xp_decode_rows: name %d buffers and pitch must be 16-byte aligned", n);
+               "%s: name %d buffers and pitch must be 16-byte aligned", what, n);
     a.names[n] = NameDev{static_cast<const uint8_t*>(s.stg),
                          s.pitch,
                          s.stg_rows,
@@ -513,13 +526,32 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
                          s.dst_rows,
                          s.row_bytes,
                          static_cast<int>(G),
-                         static_cast<int>((G + kGroupsPerBlock - 1) / kGroupsPerBlock)};
+                         static_cast<int>((G + kGroupsPerBlock - 1) / kGroupsPerBlock),
+                         nullptr,
+                         nullptr,
+                         0};
+    if (scales) {
+      const xp_decode_scale& c = scales[n];
+      XP_REQUIRE(c.scale && c.scale_dst, "%s: name %d has a null scale buffer", what, n);
+      XP_REQUIRE(c.scale_bytes > 0 && c.scale_bytes % 4 == 0 && c.scale_bytes < (int64_t(1) << 20),
+                 "%s: name %d scale rows of %lld bytes (a positive multiple of 4 below 1 MiB)", what, n,
+                 (long long)c.scale_bytes);
+      XP_REQUIRE(c.scale_rows >= num_experts && c.scale_dst_rows >= s.dst_rows,
+                 "%s: name %d scale rows %lld / %lld, need %lld experts and %lld destination rows", what, n,
+                 (long long)c.scale_rows, (long long)c.scale_dst_rows, (long long)num_experts,
+                 (long long)s.dst_rows);
+      XP_REQUIRE(aligned4(c.scale) && aligned4(c.scale_dst), "%s: name %d scale buffers must be 4-byte aligned",
+                 what, n);
+      a.names[n].scale = static_cast<const uint32_t*>(c.scale);
+      a.names[n].scale_dst = static_cast<uint32_t*>(c.scale_dst);
+      a.names[n].scale_words = static_cast<int>(c.scale_bytes / 4);
+    }
     per_row += a.names[n].blocks;
   }
   if (num_names == 1) a.names[1] = a.names[0];
   a.blocks_per_row = per_row;
   const int64_t grid = K * per_row;
-  XP_REQUIRE(grid <= (int64_t(1) << 31) - 1, "xp_decode_rows: grid too large");
+  XP_REQUIRE(grid <= (int64_t(1) << 31) - 1, "%s: grid too large", what);
   // Runs of 128 bytes per store (8-lane sets) when the chunk allows it, else 64 or 32.
   if (chunk % 128 == 0)
     hipLaunchKernelGGL(decode_kernel<16>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
@@ -528,6 +560,26 @@ int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const in
   else
     hipLaunchKernelGGL(decode_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
   return check_launch("decode_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+int xp_decode_rows(const int64_t* todo, int64_t K, int64_t num_experts, const int64_t* dst_row,
+                   const int64_t* cache_row, const uint8_t* lut, const xp_decode_name* names, int num_names,
+                   const int64_t* skip, int64_t chunk, void* stream) {
+  return launch_decode("xp_decode_rows", todo, K, num_experts, dst_row, cache_row, nullptr, 0, lut, names, num_names,
+                       nullptr, skip, chunk, stream);
+}
+
+int xp_decode_rows_from_ram(const int64_t* todo, int64_t K, int64_t num_experts, const int64_t* dst_row,
+                            const int64_t* cache_row, const int64_t* src_row, int64_t base, const uint8_t* lut,
+                            const xp_decode_name* names, int num_names, const xp_decode_scale* scales,
+                            const int64_t* skip, int64_t chunk, void* stream) {
+  XP_REQUIRE(src_row && scales, "xp_decode_rows_from_ram: src_row and scales must be non-null");
+  return launch_decode("xp_decode_rows_from_ram", todo, K, num_experts, dst_row, cache_row, src_row, base, lut, names,
+                       num_names, scales, skip, chunk, stream);
 }
 
 }  // extern "C"

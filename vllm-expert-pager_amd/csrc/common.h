@@ -27,6 +27,7 @@ int check_launch(const char* what);
 int64_t wallclock_ticks_per_us();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 }  // namespace xp
 

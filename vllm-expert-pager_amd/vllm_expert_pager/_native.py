@@ -76,6 +76,16 @@ class XpDecodeName(ctypes.Structure):
     ]
 
 
+class XpDecodeScale(ctypes.Structure):
+    _fields_ = [
+        ("scale", c_ptr),
+        ("scale_dst", c_ptr),
+        ("scale_bytes", c_i64),
+        ("scale_rows", c_i64),
+        ("scale_dst_rows", c_i64),
+    ]
+
+
 _P = c_ptr
 _I = ctypes.c_int
 _L = c_i64
@@ -95,6 +105,7 @@ _SIGNATURES = {
     "xp_fetch_wait_rows": (_I, [_P, _L, _P, _P, _P]),
     "xp_fetch_set_timing": (_I, [_L, _L]),
     "xp_decode_rows": (_I, [_P, _L, _L, _P, _P, _P, _P, _I, _P, _L, _P]),
+    "xp_decode_rows_from_ram": (_I, [_P, _L, _L, _P, _P, _P, _L, _P, _P, _I, _P, _P, _L, _P]),
     "xp_encode_row": (_I, [_P, _L, _L, _P, _L, _P, _P]),
     "xp_code_build": (_I, [_P, _P, _P, _P]),
     "xp_host_alloc": (_I, [_P, _L, _I]),

@@ -165,3 +165,68 @@ def decode_rows(
         cache_row.data_ptr(), lut.data_ptr(), names, n, None if skip_t is None else skip_t.data_ptr(),
         chunk, nat.stream(),
     )
+
+
+def decode_rows_from_ram(
+    todo: torch.Tensor,
+    dst_row: torch.Tensor,
+    cache_row: torch.Tensor,
+    src_row: torch.Tensor,
+    base: int,
+    src: list,
+    dst: list[torch.Tensor],
+    lut: torch.Tensor,
+    scale: list[torch.Tensor],
+    scale_dst: list[torch.Tensor],
+    skip: torch.Tensor | None = None,
+    chunk: int = CHUNK,
+) -> None:
+    """``decode_rows`` with the records read straight from the RAM tier.
+
+    The record of expert ``e = todo[j]`` is row ``src_row[e] + base`` of
+    ``src[name]`` (a ``DeviceRows`` view or pinned tensor of the tier, pitch
+    bytes per row), and its scale row ``scale[name][e]`` is copied to
+    ``scale_dst[name][dst_row[e]]``; no staging copy is made first. Experts
+    with ``cache_row[e] >= 0`` are skipped entirely. The reference decodes a
+    staging copy (codec.py:297-327) that a gather fills (gather.py:328-393).
+    """
+    from vllm_expert_pager.gather import _rows
+
+    for t, what in ((todo, "todo"), (dst_row, "dst_row"), (cache_row, "cache_row"), (src_row, "src_row"),
+                    (lut, "lut")):
+        nat.require_device(t, what)
+    todo = todo.to(torch.int64).contiguous()
+    dst_row = dst_row.to(torch.int64).contiguous()
+    cache_row = cache_row.to(torch.int64).contiguous()
+    src_row = src_row.to(torch.int64).contiguous()
+    skip_t = None if skip is None else skip.to(torch.int64).contiguous()
+    lut = lut.contiguous()
+    n = len(dst)
+    E = dst_row.shape[0]
+    if len(src) != n or len(scale) != n or len(scale_dst) != n:
+        raise ValueError("src, dst, scale and scale_dst need one entry per name")
+    if src_row.shape[0] < E:
+        raise ValueError(f"src_row has {src_row.shape[0]} entries, fewer than the {E} experts")
+    if lut.numel() < E * n * LUT_BYTES:
+        raise ValueError(f"lut has {lut.numel()} B, needs {E} x {n} x {LUT_BYTES}")
+    if skip_t is not None and skip_t.shape[0] < todo.shape[0]:
+        raise ValueError("skip must have at least as many entries as todo")
+    names = (nat.XpDecodeName * n)()
+    scales = (nat.XpDecodeScale * n)()
+    for i in range(n):
+        sp, srows, spitch = _rows(src[i])
+        d, c, cd = dst[i], scale[i], scale_dst[i]
+        for t, what in ((c, "scale"), (cd, "scale_dst")):
+            nat.require_device(t, what)
+            if not t.is_contiguous():
+                raise ValueError(f"{what}[{i}] must be contiguous")
+        row = c[0].numel() * c.element_size() if c.shape[0] else 0
+        if cd.shape[0] and cd[0].numel() * cd.element_size() != row:
+            raise ValueError(f"scale_dst[{i}] rows are not the size of scale[{i}] rows")
+        names[i] = nat.XpDecodeName(sp, spitch, srows, d.data_ptr(), d.shape[0], d.shape[1] * d.element_size())
+        scales[i] = nat.XpDecodeScale(c.data_ptr(), cd.data_ptr(), row, c.shape[0], cd.shape[0])
+    nat.call(
+        "xp_decode_rows_from_ram", todo.data_ptr(), todo.shape[0], E, dst_row.data_ptr(), cache_row.data_ptr(),
+        src_row.data_ptr(), int(base), lut.data_ptr(), names, n, scales,
+        None if skip_t is None else skip_t.data_ptr(), chunk, nat.stream(),
+    )

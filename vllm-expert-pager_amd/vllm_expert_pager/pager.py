@@ -24,7 +24,7 @@ import torch
 
 from vllm_expert_pager import moe, trace
 from vllm_expert_pager.acquire import AcquirePair
-from vllm_expert_pager.codec import decode_rows
+from vllm_expert_pager.codec import decode_rows, decode_rows_from_ram
 from vllm_expert_pager.gather import as_rows, fetch_publish_rows, fetch_wait_rows, gather_rows
 from vllm_expert_pager.store import Store
 from vllm_expert_pager.table import ExpertTable
@@ -115,13 +115,6 @@ class Pager:
         self.store = Store(num_layers, E, R, 2 * s.working_rows, row_bytes, compress, s.pitch_ratio, s.ssd_path,
                            self.device)
         W = s.working_rows
-        if compress:
-            least = max(-(-s.cache_slots * self.store.pitch[n] // row_bytes[n]) for n in PARAMS)
-            if W < least:
-                raise ValueError(
-                    f"VLLM_EXPERT_PAGER_WORKING_ROWS={W} cannot hold the decode staging of "
-                    f"VLLM_EXPERT_PAGER_CACHE_SLOTS={s.cache_slots} compressed rows; set it to at least {least}"
-                )
         self.working_slab = {
             n: torch.empty((W, *shape), dtype=dt, device=self.device) for n, (shape, dt) in self.shapes.items()
         }
@@ -205,13 +198,6 @@ class PagedExperts:
         self.scale_rows = [as_rows(self.scales[n]) for n in SCALES]
         self.cache_bytes = [self.cache_slab[n].view(torch.uint8).reshape(S, -1) for n in PARAMS]
         self.working_bytes = [p.working_slab[n].view(torch.uint8).reshape(W, -1) for n in PARAMS]
-        # In decode the shared working slab is idle, so its head is the
-        # staging of compressed rows (S rows x pitch).
-        self.decode_staging = (
-            [p.working_slab[n].view(torch.uint8).reshape(-1)[: S * store.pitch[n]].view(S, store.pitch[n])
-             for n in PARAMS]
-            if store.compress else None
-        )
         self.ready = True
         p.layer_ready()
 
@@ -238,36 +224,47 @@ class PagedExperts:
         cached_row = self.table.no_cache  # everything comes from the RAM tier
         base = layer * store.ram_slots
         lut = store.layer_lut(layer)
-        staging = self.decode_staging
-        rows = (
-            [store.view[n] for n in PARAMS],
-            self.cache_rows[:2],
-            self.cache_rows[:2],
-            [t.view(torch.int32) for t in staging] if staging is not None else None,
-            self.scale_rows,
-            self.cache_rows[2:],
-        )
-        if store.path is None:
+        if store.compress:
+            # The decoder reads each miss's record straight from the RAM tier
+            # (its loads run over the host link while it decodes) and copies
+            # the scales, so no gather into staging comes first.
+            src = [store.view[n] for n in PARAMS]
+            dst = (self.cache_bytes, lut, self.scale_rows, self.cache_rows[2:])
+            if store.path is None:
+                with trace.range(f"expert_pager L{layer} decode"):
+                    decode_rows_from_ram(todo, dst_row, cached_row, src_row, base, src, *dst)
+            else:
+                # Publish the SSD request, expand the experts that are in RAM
+                # while the host reads, then wait and expand the rest. Every
+                # listed SSD expert must fit the request slot, or one left
+                # out would be expanded from a row the host never wrote.
+                if ssd_todo.shape[0] > store.block:
+                    raise RuntimeError(f"layer {layer}: {ssd_todo.shape[0]} SSD entries exceed the ring block "
+                                       f"{store.block}")
+                ticket = store.ticket_chunk[:1]
+                fetch_publish_rows(ssd_todo, src_row, base, layer, store, ticket)
+                with trace.range(f"expert_pager L{layer} decode"):
+                    decode_rows_from_ram(todo, dst_row, cached_row, src_row, base, src, *dst, skip=ssd_todo)
+                with trace.range(f"expert_pager L{layer} ssd wait"):
+                    fetch_wait_rows(ssd_todo, store, ticket)
+                with trace.range(f"expert_pager L{layer} decode ssd rows"):
+                    decode_rows_from_ram(ssd_todo, dst_row, cached_row, src_row, base, src, *dst)
+        elif store.path is None:
+            rows = ([store.view[n] for n in PARAMS], self.cache_rows[:2], self.cache_rows[:2], None,
+                    self.scale_rows, self.cache_rows[2:])
             # Every expert is in RAM (R = E): the RAM table always hits, so
             # there is never an SSD read and one copy does it all.
             with trace.range(f"expert_pager L{layer} gather"):
                 gather_rows(todo, dst_row, cached_row, src_row, base, *rows)
-            if store.compress:
-                with trace.range(f"expert_pager L{layer} decode"):
-                    decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut)
         else:
+            rows = ([store.view[n] for n in PARAMS], self.cache_rows[:2], self.cache_rows[:2], None,
+                    self.scale_rows, self.cache_rows[2:])
             # One launch publishes the SSD request and copies the experts
             # that are in RAM while the host reads; then the ones read from SSD.
             with trace.range(f"expert_pager L{layer} gather + ssd wait"):
                 gather_rows(todo, dst_row, cached_row, src_row, base, *rows, fetch=(ssd_todo, layer, store))
-            if store.compress:
-                with trace.range(f"expert_pager L{layer} decode"):
-                    decode_rows(todo, dst_row, cached_row, staging, self.cache_bytes, lut, skip=ssd_todo)
             with trace.range(f"expert_pager L{layer} gather ssd rows"):
                 gather_rows(ssd_todo, dst_row, cached_row, src_row, base, *rows)
-            if store.compress:
-                with trace.range(f"expert_pager L{layer} decode ssd rows"):
-                    decode_rows(ssd_todo, dst_row, cached_row, staging, self.cache_bytes, lut)
 
         with trace.range(f"expert_pager L{layer} experts"):
             if moe.decode_fits(x, topk_ids, self.pager.intermediate):
