@@ -340,7 +340,10 @@ __device__ __forceinline__ void flush16(uint4 (&ob)[8], uint8_t* chunk0, int64_t
   }
 }
 
-template <int F>
+// kFromRam: expert e's record is stg row src_row[e] + base and the scale
+// rows are copied; otherwise staging row j (a separate instantiation, so the
+// staging path's code is not touched by the RAM-tier one).
+template <int F, bool kFromRam>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) decode_kernel(DecodeArgs a) {
   __shared__ uint16_t s_lut[XP_LUT_BYTES];
   __shared__ uint32_t s_ring[kGroupsPerBlock][kRingPad];
@@ -359,14 +362,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   if (!active || a.cache_row[e] >= 0) return;
   // A destination or record row outside its tensor is skipped, never clamped.
   const int64_t drow = a.dst_row[e];
-  const int64_t srow = a.src_row ? a.src_row[e] + a.base : j;
+  const int64_t srow = kFromRam ? a.src_row[e] + a.base : j;
   if (drow < 0 || drow >= nm.dst_rows || srow < 0 || srow >= nm.stg_rows) return;
 
   const int tid = threadIdx.x;
   // Read from the RAM tier, the name's first workgroup of the row also
   // copies the expert's scale row, which a staging gather would have moved.
-  if (nm.scale && r == 0)
-    for (int i = tid; i < nm.scale_words; i += kThreads) nm.scale_dst[drow * nm.scale_words + i] = nm.scale[e * nm.scale_words + i];
+  if constexpr (kFromRam) {
+    if (r == 0)
+      for (int i = tid; i < nm.scale_words; i += kThreads)
+        nm.scale_dst[drow * nm.scale_words + i] = nm.scale[e * nm.scale_words + i];
+  }
   const uint8_t* lut = a.lut + (e * a.num_names + name) * XP_LUT_BYTES;
   // The row's 9-bit table (entry = symbol << 4 | length) as length |
   // (exponent field << 3) << 8. Lengths are clamped to [1, LIMIT], which
@@ -553,12 +559,21 @@ int launch_decode(const char* what, const int64_t* todo, int64_t K, int64_t num_
   const int64_t grid = K * per_row;
   XP_REQUIRE(grid <= (int64_t(1) << 31) - 1, "%s: grid too large", what);
   // Runs of 128 bytes per store (8-lane sets) when the chunk allows it, else 64 or 32.
-  if (chunk % 128 == 0)
-    hipLaunchKernelGGL(decode_kernel<16>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
-  else if (chunk % 64 == 0)
-    hipLaunchKernelGGL(decode_kernel<8>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
-  else
-    hipLaunchKernelGGL(decode_kernel<4>, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, as_stream(stream), a);
+  const dim3 g(static_cast<unsigned>(grid)), b(kThreads);
+  if (src_row) {
+    if (chunk % 128 == 0)
+      hipLaunchKernelGGL((decode_kernel<16, true>), g, b, 0, as_stream(stream), a);
+    else if (chunk % 64 == 0)
+      hipLaunchKernelGGL((decode_kernel<8, true>), g, b, 0, as_stream(stream), a);
+    else
+      hipLaunchKernelGGL((decode_kernel<4, true>), g, b, 0, as_stream(stream), a);
+  } else if (chunk % 128 == 0) {
+    hipLaunchKernelGGL((decode_kernel<16, false>), g, b, 0, as_stream(stream), a);
+  } else if (chunk % 64 == 0) {
+    hipLaunchKernelGGL((decode_kernel<8, false>), g, b, 0, as_stream(stream), a);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<4, false>), g, b, 0, as_stream(stream), a);
+  }
   return check_launch("decode_kernel");
 }
 
