@@ -94,7 +94,7 @@ def same(a, b):
     return torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-@pytest.mark.parametrize("compress, R", [(True, 16), (False, 64)])
+@pytest.mark.parametrize("compress, R", [(True, 16), (True, 64), (False, 64)])
 def test_decode_steps_match_one_shot(model, compress, R):
     m = model(64, 4, R, 8, compress)
     rng = np.random.default_rng(1)
@@ -108,7 +108,7 @@ def test_decode_steps_match_one_shot(model, compress, R):
     assert m.pager.store.failed is None
 
 
-@pytest.mark.parametrize("compress, R", [(True, 16), (False, 64)])
+@pytest.mark.parametrize("compress, R", [(True, 16), (True, 64), (False, 64)])
 @pytest.mark.parametrize("T", [3, 48])
 def test_prefill_overflow_matches_one_shot(model, compress, R, T):
     """T=3 x top-4 = 12 ids: the RAM tier acquires; T=48: 192 ids > R, the RAM tier is seeded."""
