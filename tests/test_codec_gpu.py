@@ -163,7 +163,9 @@ def _ram_tier(records_by_row, rows, pitch):
     return buf, DeviceRows(host, buf.device_ptr)
 
 
-def test_decode_from_ram_follows_rows_and_copies_scales():
+# 128-byte runs (512), 64-byte (64), plain stores (32, 96)
+@pytest.mark.parametrize("chunk", [32, 64, 96, 512])
+def test_decode_from_ram_follows_rows_and_copies_scales(chunk):
     """xp_decode_rows_from_ram: expert e's record is RAM-tier row
     src_row[e] + base and its scale row goes to scale_dst[dst_row[e]];
     todo -1 entries, cached experts, listed skips and record or destination
@@ -171,7 +173,7 @@ def test_decode_from_ram_follows_rows_and_copies_scales():
     codec = _codec()
     dev = torch.device("cuda")
     E, rows_ram, base = 10, 16, 4
-    ns = (N, N // 2)
+    ns = (2 * chunk * 32, chunk * 32)
     pitches = [codec_ref.pitch_of(n, 1.25, 4096) for n in ns]
     src_row = torch.tensor([0, 3, 7, -9, 9, 12, 2, 5, 8, 1], dtype=torch.int64)  # row - base per expert
     dst_row = torch.tensor([0, 3, 1, 0, 5, 2, 0, 4, 0, 0], dtype=torch.int64)  # dst_rows = 5: expert 4 is outside
@@ -181,7 +183,7 @@ def test_decode_from_ram_follows_rows_and_copies_scales():
     placed = [{}, {}]
     for e in used:
         for k in range(2):
-            rec, lt = codec_ref.encode(raws[e][k], pitches[k], CHUNK)
+            rec, lt = codec_ref.encode(raws[e][k], pitches[k], chunk)
             lut[e, k] = torch.from_numpy(lt).to(dev)
             r = base + int(src_row[e])
             if 0 <= r < rows_ram:
@@ -200,7 +202,7 @@ def test_decode_from_ram_follows_rows_and_copies_scales():
 
     def run(sk):
         codec.decode_rows_from_ram(todo, dst_row.to(dev), cache_row, ram[0], ram[1], src, dst, lut, scale, scale_dst,
-                                   skip=sk, chunk=CHUNK)
+                                   skip=sk, chunk=chunk)
         torch.cuda.synchronize()
 
     run(skip)
