@@ -155,7 +155,10 @@ typedef struct xp_ring {
  * src_row[e] + base: to staging row j (its index in todo) when the name has
  * stg, else to dst row dst_row[e]. The scale row of e is copied to
  * scale_dst row dst_row[e]. An expert whose dst_row[e] is outside
- * [0, dst_rows) is skipped (nothing of it is copied). With ring != NULL, the
+ * [0, dst_rows), or (with stg) whose staging row j is not below stg_rows,
+ * is skipped (nothing of it is copied): with stg set and stg_rows = 0 the
+ * launch copies only the cached experts, for a caller that expands the
+ * others with xp_decode_rows_from_ram. With ring != NULL, the
  * same launch publishes the experts of ssd_todo[K] (K <= ring->block) to the
  * host ring for layer `layer`, waits for their done, and skips them in the
  * copy.

@@ -83,6 +83,7 @@ def gather_rows(
     scale: list[torch.Tensor],
     scale_dst: list[torch.Tensor],
     fetch: tuple[torch.Tensor, int, object] | None = None,
+    cached_only: bool = False,
 ) -> None:
     """Copy the rows and scales of the experts in ``todo`` (gather.py:328-393).
 
@@ -93,7 +94,10 @@ def gather_rows(
     (compressed, ``stg`` given) or to ``dst[dst_row[e]]`` (raw). Scales go to
     ``scale_dst[dst_row[e]]``. With ``fetch=(ssd_todo, layer, store)`` the
     same launch publishes ``ssd_todo`` to the host and waits for it while
-    copying the experts of ``todo`` that are not in ``ssd_todo``.
+    copying the experts of ``todo`` that are not in ``ssd_todo``. With
+    ``cached_only`` (``stg`` given, for its pitch) only the experts with
+    ``cache_row[e] >= 0`` are copied: the launch gets zero staging rows, so
+    the RAM-tier experts are skipped, for ``decode_rows_from_ram`` to expand.
     """
     todo = _index(todo, "todo")
     dst_row = _index(dst_row, "dst_row")
@@ -106,6 +110,8 @@ def gather_rows(
     srcs = [_rows(s) for s in src]
     P = [s[2] for s in srcs]
     compress = stg is not None
+    if cached_only and not compress:
+        raise ValueError("cached_only needs stg (its rows give the tier's pitch)")
     if compress:
         if tuple(P) != tuple(s.shape[1] * s.element_size() for s in stg):
             raise ValueError("staging rows must have the RAM tier's pitch")
@@ -123,7 +129,7 @@ def gather_rows(
             sp, spitch, srows,
             cache[i].data_ptr(), cache[i].shape[0],
             dst[i].data_ptr(), dst[i].shape[0], W[i],
-            stg[i].data_ptr() if compress else None, stg[i].shape[0] if compress else 0,
+            stg[i].data_ptr() if compress else None, stg[i].shape[0] if compress and not cached_only else 0,
             scale[i].data_ptr(), scale_dst[i].data_ptr(), scale[i].shape[1] * scale[i].element_size(),
         )
     ring = None

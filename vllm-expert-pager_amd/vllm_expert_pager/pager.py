@@ -24,7 +24,7 @@ import torch
 
 from vllm_expert_pager import moe, trace
 from vllm_expert_pager.acquire import AcquirePair
-from vllm_expert_pager.codec import decode_rows, decode_rows_from_ram
+from vllm_expert_pager.codec import decode_rows_from_ram
 from vllm_expert_pager.gather import as_rows, fetch_publish_rows, fetch_wait_rows, gather_rows
 from vllm_expert_pager.store import Store
 from vllm_expert_pager.table import ExpertTable
@@ -77,12 +77,13 @@ def _shapes(hidden: int, intermediate: int) -> dict[str, tuple[tuple[int, ...], 
 
 
 class Pager:
-    """One per model: the store, the shared working slab and the prefill staging.
+    """One per model: the store and the shared working slab.
 
-    Mirrors the module-level ``_store``, ``_working_slab`` and
-    ``_prefill_staging`` of the reference (experts.py:78-83, 114-146,
-    290-318): layers run one after another on one stream, so they share the
-    working rows.
+    Mirrors the module-level ``_store`` and ``_working_slab`` of the
+    reference (experts.py:78-83, 114-146, 290-318): layers run one after
+    another on one stream, so they share the working rows. Its
+    ``_prefill_staging`` has no counterpart: compressed rows are expanded
+    straight from the RAM tier.
     """
 
     def __init__(self, settings: Settings, num_layers: int, num_experts: int, hidden: int, intermediate: int,
@@ -118,8 +119,13 @@ class Pager:
         self.working_slab = {
             n: torch.empty((W, *shape), dtype=dt, device=self.device) for n, (shape, dt) in self.shapes.items()
         }
-        self.prefill_staging = (
-            [torch.empty((W, self.store.pitch[n]), dtype=torch.uint8, device=self.device) for n in PARAMS]
+        # Compressed prefill chunks gather only their cached experts (the
+        # decoder expands the others straight from pinned RAM); the gather
+        # takes the tier's pitch from these one-row views, which it never
+        # writes (no memory of their own).
+        self.pitch_rows = (
+            [self.working_slab[n].view(torch.uint8).reshape(-1)[: self.store.pitch[n]].view(torch.int32)
+             .view(1, -1) for n in PARAMS]
             if compress else None
         )
 
@@ -305,22 +311,19 @@ class PagedExperts:
         dst_row, src_row, maps, todo, ssd, late = ram.plan_chunks(
             before, need, cached_row, W, layer * R, store.working_base
         )
-        staging = p.prefill_staging
         lut = store.layer_lut(layer)
-        rows = (
-            [store.view[n] for n in PARAMS],
-            self.cache_rows[:2],
-            self.working_rows[:2],
-            [t.view(torch.int32) for t in staging] if staging is not None else None,
-            self.scale_rows,
-            self.working_rows[2:],
-        )
+        src = [store.view[n] for n in PARAMS]
+        rows = (src, self.cache_rows[:2], self.working_rows[:2], p.pitch_rows, self.scale_rows,
+                self.working_rows[2:])
         tickets = store.ticket_chunk
 
         def copy(part: torch.Tensor) -> None:
-            gather_rows(part, dst_row, cached_row, src_row, 0, *rows)
+            # Cached experts raw from the cache slab; with a compressed tier
+            # the others are expanded straight from the RAM tier.
+            gather_rows(part, dst_row, cached_row, src_row, 0, *rows, cached_only=store.compress)
             if store.compress:
-                decode_rows(part, dst_row, cached_row, staging, self.working_bytes, lut)
+                decode_rows_from_ram(part, dst_row, cached_row, src_row, 0, src, self.working_bytes, lut,
+                                     self.scale_rows, self.working_rows[2:])
 
         def chunk(t: torch.Tensor, k: int) -> torch.Tensor:
             return t[k * W : (k + 1) * W]
