@@ -7,7 +7,8 @@ raw; a record of ``pitch`` bytes = int32 gstart[G+1] | nibble words in
 512-byte LUT ((sym << 4) | len) lives outside the record.
 
 ``encode`` runs on the host (C++, csrc/codec_host.cpp); ``decode_rows``
-expands staging rows on the GPU (csrc/codec.hip).
+expands staging rows on the GPU and ``decode_rows_from_ram`` RAM-tier rows
+(csrc/codec.hip).
 """
 
 from __future__ import annotations

@@ -34,7 +34,7 @@ logger = init_logger(f"vllm.{__name__}")
 
 SETTINGS = Settings.from_env()
 
-# One pager per model: the store, the shared working slab and staging.
+# One pager per model: the store and the shared working slab.
 _pager: Pager | None = None
 
 
