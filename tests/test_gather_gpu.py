@@ -167,3 +167,57 @@ def test_negative_destination_rows_are_skipped(compress):
         s = stg[0].cpu().numpy()
         assert np.array_equal(s[0], recs[2][0])                # todo entry 0 staged
         assert (s[1] == 0x5A).all() and (s[2] == 0x5A).all()   # entries 1 and 2 (negative rows) not staged
+
+
+def test_cached_only_copies_cached_experts():
+    """gather_rows(cached_only=True) (zero staging rows) copies the experts
+    with cache_row >= 0 raw from the cache slab, with their scales, and
+    leaves every RAM-tier expert to the decoder: no slab, staging or scale
+    row of those is written. With the RAM-tier ones expanded by
+    decode_rows_from_ram, the slab matches a staging gather + decode."""
+    gather = _gather()
+    from vllm_expert_pager import codec
+
+    from oracle import codec_ref
+
+    dev = torch.device("cuda")
+    E, S, N = 6, 5, 16384
+    rng = np.random.default_rng(5)
+    raw = [(rng.integers(0, 256, N, dtype=np.uint8) & 0x87) | (rng.integers(9, 14, N, dtype=np.uint8) << 3)
+           for _ in range(E)]
+    P = codec_ref.pitch_of(N, 1.0, 4096)
+    recs = [codec_ref.encode(r, P) for r in raw]
+    src = [torch.from_numpy(np.stack([rc for rc, _ in recs])).pin_memory()]
+    lut = torch.from_numpy(np.stack([l for _, l in recs])).view(E, 1, 512).to(dev)
+    cache = [torch.from_numpy(np.stack([raw[4], raw[1]])).to(dev)]  # experts 4 and 1 cached in rows 0, 1
+    scale = [torch.arange(E * 4, dtype=torch.int32, device=dev).view(E, 4) + 1]
+    todo = torch.tensor([1, 3, 4, 0], dtype=torch.int64, device=dev)
+    dst_row = torch.tensor([1, 4, 9, 2, 0, 9], dtype=torch.int64, device=dev)  # 2 and 5 are not listed
+    cache_row = torch.full((E,), -1, dtype=torch.int64, device=dev)
+    cache_row[4], cache_row[1] = 0, 1
+    src_row = torch.arange(E, dtype=torch.int64, device=dev)
+    pitch_rows = [torch.zeros((1, P), dtype=torch.uint8, device=dev).view(torch.int32)]
+
+    def fresh():
+        return ([torch.full((S, N), 0x5A, dtype=torch.uint8, device=dev)],
+                [torch.zeros((S, 4), dtype=torch.int32, device=dev)])
+
+    dst, sdst = fresh()
+    gather.gather_rows(todo, dst_row, cache_row, src_row, 0, src, cache, dst, pitch_rows, scale, sdst,
+                       cached_only=True)
+    torch.cuda.synchronize()
+    got = dst[0].cpu().numpy()
+    assert np.array_equal(got[0], raw[4]) and np.array_equal(got[4], raw[1])  # the cached experts
+    for r in (1, 2, 3):
+        assert (got[r] == 0x5A).all() and not sdst[0][r].any(), r              # RAM-tier ones untouched
+    assert torch.equal(sdst[0][0], scale[0][4]) and torch.equal(sdst[0][4], scale[0][1])
+    assert not pitch_rows[0].any()                                              # never written
+    codec.decode_rows_from_ram(todo, dst_row, cache_row, src_row, 0, src, dst, lut, scale, sdst)
+    ref, rsdst = fresh()
+    stg = [torch.zeros((len(todo), P), dtype=torch.uint8, device=dev)]
+    gather.gather_rows(todo, dst_row, cache_row, src_row, 0, src, cache, ref, [stg[0].view(torch.int32)], scale,
+                       rsdst)
+    codec.decode_rows(todo, dst_row, cache_row, stg, ref, lut)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[0], ref[0]) and torch.equal(sdst[0], rsdst[0])
+    assert np.array_equal(dst[0][2].cpu().numpy(), raw[3]) and np.array_equal(dst[0][1].cpu().numpy(), raw[0])
