@@ -1030,7 +1030,11 @@ def main() -> None:
         extras["acquire"] = bench_acquire(args, dev)
         extras["moe"] = bench_moe(args, dev)
         extras["model_decode"] = bench_model_decode(args, dev)
-        extras["model_decode_compressed"] = bench_model_decode_compressed(args, dev)
+        try:
+            extras["model_decode_compressed"] = bench_model_decode_compressed(args, dev)
+        except (RuntimeError, MemoryError, ValueError) as e:  # reported, so the other legs still print
+            extras["model_decode_compressed"] = {"failed": f"{type(e).__name__}: {e}"}
+            log(f"compressed RAM-tier decode trace failed: {e}")
         if not args.no_tiered:
             extras["tiered"] = bench_tiered(args, dev, args.tiered_decode_steps)
     line = {
