@@ -1,8 +1,13 @@
-"""The C ABI library loads and exports every function include/xp.h declares (CPU, no GPU calls)."""
+"""The C ABI library loads and exports every function include/xp.h declares, and the ctypes
+structures of the bindings have the header's layout (CPU, no GPU calls)."""
 
 import ctypes
 import os
 import re
+import shutil
+import subprocess
+
+import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -51,3 +56,31 @@ def test_roctx_ranges_are_free_when_off(monkeypatch):
     with trace.range("x"):
         pass
     assert trace._lib is None
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every struct the bindings pass by pointer has, in ctypes, the size and
+    field offsets a C compiler gives it from include/xp.h."""
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    from vllm_expert_pager import _native
+
+    structs = {"xp_table": _native.XpTable, "xp_gather_name": _native.XpGatherName, "xp_ring": _native.XpRing,
+               "xp_decode_name": _native.XpDecodeName, "xp_decode_scale": _native.XpDecodeScale}
+    header = open(os.path.join(ROOT, "include", "xp.h")).read()
+    assert set(re.findall(r"typedef struct (xp_[a-z_]+) \{", header)) == set(structs), "a struct without a check"
+    lines = ["#include <stddef.h>", "#include <stdio.h>", '#include "xp.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cname}.{field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src, exe = tmp_path / "layout.c", tmp_path / "layout"
+    src.write_text("\n".join(lines) + "\n")
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                               check=True).stdout.splitlines())
+    for cname, cls in structs.items():
+        assert int(got[cname]) == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert int(got[f"{cname}.{field}"]) == getattr(cls, field).offset, f"{cname}.{field}"
