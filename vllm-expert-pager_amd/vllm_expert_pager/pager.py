@@ -121,11 +121,10 @@ class Pager:
         }
         # Compressed prefill chunks gather only their cached experts (the
         # decoder expands the others straight from pinned RAM); the gather
-        # takes the tier's pitch from these one-row views, which it never
-        # writes (no memory of their own).
+        # takes the tier's pitch from these one-row tensors and never
+        # writes them.
         self.pitch_rows = (
-            [self.working_slab[n].view(torch.uint8).reshape(-1)[: self.store.pitch[n]].view(torch.int32)
-             .view(1, -1) for n in PARAMS]
+            [torch.zeros((1, self.store.pitch[n] // 4), dtype=torch.int32, device=self.device) for n in PARAMS]
             if compress else None
         )
 
