@@ -10,8 +10,10 @@ multiply, moe_sum) in numpy/torch on the CPU:
   quant_groups  x -> fp8 per 128 columns: s = max(amax, 1e-10) / 448 (fp32),
                 q = rne(clamp(x / s, -448, 448))
   expert_ffn    per (token, k) pair: h = dequant(xq) . dequant(w13)^T,
-                gate/up -> bf16, a = bf16(silu(gate) * up), a -> fp8 per 128
-                columns, y = dequant(aq) . dequant(w2)^T,
+                gate/up -> bf16, a = bf16(bf16(silu(gate)) * up) (vLLM's
+                silu_and_mul returns silu in the activation dtype and then
+                multiplies two bf16 values), a -> fp8 per 128 columns,
+                y = dequant(aq) . dequant(w2)^T,
                 contribution = bf16(y * routed weight)
   topk_sum      bf16(fp32 sum over k ascending of the contributions)
 
@@ -105,6 +107,7 @@ def dequant_weight(w: np.ndarray, ws: np.ndarray) -> np.ndarray:
 VARIANTS = (
     "gate_up_unrounded",   # gate and up kept in fp32 instead of rounded to bf16
     "gate_up_truncated",   # gate and up rounded to bf16 toward zero
+    "silu_unrounded",      # silu(gate) kept in fp32 before the product with up
     "act_unrounded",       # silu(gate) * up not rounded to bf16 before quantisation
     "quant_reciprocal",    # activation scale applied as a * (448 / amax) instead of a / (amax / 448)
     "fp8_truncated",       # activations converted to fp8 toward zero
@@ -179,6 +182,8 @@ def expert_ffn(x: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray, w1
             gate, up = bf16(h[:, :I]), bf16(h[:, I:])
         with np.errstate(over="ignore"):
             silu = (gate / (np.float32(1) + np.exp(-gate))).astype(np.float32)
+        if variant != "silu_unrounded":
+            silu = bf16(silu)
         a = (silu * up).astype(np.float32) if variant == "act_unrounded" else bf16(silu * up)
         aq, as_ = _quant_variant(a, variant)
         y = (dequant_rows(aq, as_) @ dequant_weight(w2[e], w2_scale[e]).T).astype(np.float32)
@@ -187,23 +192,60 @@ def expert_ffn(x: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray, w1
     return out
 
 
-def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk: int):
-    """A MoE case on which every sum is exact in fp32 and SiLU is exact, while
-    every rounding step of the sequence still rounds: the rounding sequence,
-    not summation order, decides the output bits.
+def bf16_midpoint_margin(v: np.ndarray) -> np.ndarray:
+    """Relative distance of each non-zero float64 value to the nearest point
+    halfway between two neighbouring bf16 values (where rounding to bf16
+    changes direction)."""
+    m, _ = np.frexp(np.abs(np.asarray(v, np.float64)))  # |v| = m * 2^e, m in [0.5, 1)
+    k = m * 256.0  # |v| in units of the bf16 spacing at its binade: 8 significant bits
+    return np.abs(k - np.floor(k) - 0.5) / k
 
-    - x: per token one or two active 128-column groups, each with one value
-      of +-448 * 2^a (so the group scale is exactly 2^a) and a few of +-1..3
-      * 2^a; the other groups are zero.
-    - w13 gate rows: only the first 128 (the first activation group) are
-      non-zero, with codes in {0, +-1, +-2} and block scale 2^10, so each
-      block dot is an integer below 2^10 and every gate is 0 or at least
-      1024 in magnitude: silu(g) is g or -0 whatever exp's last bit.
-      Up rows: codes in {0, +-1, +-2, +-3}, scale 2^-4.
+
+# Probe gates of exact_inputs are v * c / 4: v the token's column-0 value
+# (m * 2^a, m in 1..3), c the weight code (+-1..4). The (m, a) pairs for which
+# silu of every such gate is at least PROBE_MARGIN (relative) away from a bf16
+# rounding midpoint, so that bf16(silu(g)) does not depend on how an fp32 exp
+# and division round (a few fp32 ulps, about 2^-21).
+PROBE_MARGIN = 2.0**-14
+
+
+def _safe_probe_values() -> list[tuple[int, int]]:
+    safe = []
+    for a in range(-3, 4):
+        for m in (1, 2, 3):
+            g = np.array([s * m * 2.0**a * c / 4 for s in (1, -1) for c in (1, 2, 3, 4, -1, -2, -3, -4)])
+            silu = g / (1 + np.exp(-g))
+            if bf16_midpoint_margin(silu).min() >= PROBE_MARGIN:
+                safe.append((m, a))
+    return safe
+
+
+def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk: int):
+    """A MoE case on which every sum is exact in fp32 and every SiLU is exact
+    or rounds to bf16 unambiguously, while every rounding step of the
+    sequence still rounds: the rounding sequence, not summation order,
+    decides the output bits.
+
+    - x: per token one or two active 128-column groups, group 0 always
+      among them; each has one value of +-448 * 2^a (so the group scale is
+      exactly 2^a) and a few of +-1..3 * 2^a; the other groups are zero.
+      Column 0 holds +-m * 2^a with (m, a) drawn from _safe_probe_values.
+    - w13 gate rows 0-127 (the first activation group) have codes in
+      {0, +-1, +-2} over every column and block scale 2^10, so each block
+      dot is an integer below 2^11 and every such gate is 0 or at least 104
+      in magnitude: silu(g) is g or -0 whatever exp's last bit.
+    - w13 gate rows 128-255 (the second activation group, when I >= 256)
+      are probes: one code c in {+-1..4} at column 0, block scale 2^-2, so
+      the gate is v * c / 4, between 2^-5 and 24 in magnitude, where silu
+      is a general value; its bf16 rounding is unambiguous (PROBE_MARGIN),
+      and bf16(silu(g)) * up rounds differently from silu(g) * up.
+    - Up rows: codes in {0, +-1, +-2, +-3}, scale 2^-4.
     - gate and up then carry up to 11 significant bits (bf16 keeps 8), and
-      a = bf16(gate * up) up to 16: both roundings round, ties included.
-    - w2 rows: one non-zero code in {+-1..+-4} per row, in the first
-      activation group, scale 2^-2: each dot is a single exact product, the
+      a = bf16(bf16(silu(gate)) * up) up to 16: the roundings round, ties
+      included.
+    - w2 rows: one non-zero code in {+-1..+-4} per row, scale 2^-2, in the
+      first activation group for even rows and in the second (the probes)
+      for odd rows when I >= 256: each dot is a single exact product, the
       activation scale amax/448 is a general float and a / scale a general
       quotient, so the requantisation's division and fp8 rounding are
       exercised.
@@ -213,6 +255,7 @@ def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk:
     """
     G, GI = H // BLOCK, I // BLOCK
     code = {v: int(to_fp8(np.array([v], np.float32))[0]) for v in (0, 1, 2, 3, 4, -1, -2, -3, -4)}
+    probes = GI >= 2
 
     def codes(values, p, shape):
         pick = rng.choice(len(values), size=shape, p=p)
@@ -224,15 +267,29 @@ def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk:
     w13s = np.ones((E, 2 * GI, G), np.float32)
     w13s[:, 0] = 2.0**10
     w13s[:, GI:] = 2.0**-4
+    if probes:
+        w13[:, BLOCK : 2 * BLOCK, 0] = codes([1, -1, 2, -2, 3, -3, 4, -4], [0.125] * 8, (E, BLOCK))
+        w13s[:, 1, 0] = 2.0**-2
     w2 = np.zeros((E, H, I), np.uint8)
     cols = rng.integers(0, BLOCK, (E, H))
+    if probes:
+        cols[:, 1::2] += BLOCK
     vals = codes([1, -1, 2, -2, 3, -3, 4, -4], [0.125] * 8, (E, H))
     np.put_along_axis(w2, cols[:, :, None], vals[:, :, None], axis=2)
     w2s = np.full((E, H // BLOCK, GI), 2.0**-2, np.float32)
 
+    safe = _safe_probe_values()
     x = np.zeros((T, H), np.float32)
     for t in range(T):
-        for g in rng.choice(G, size=int(rng.integers(1, 3)), replace=False):
+        extra = rng.choice(np.arange(1, G), size=int(rng.integers(0, 2)), replace=False) if G > 1 else []
+        for g in [0, *extra]:
+            if g == 0:
+                m, a = safe[int(rng.integers(len(safe)))]
+                cols_t = rng.choice(np.arange(1, BLOCK), size=3, replace=False)
+                x[t, 0] = rng.choice([-1.0, 1.0]) * m * 2.0**a
+                x[t, cols_t[0]] = rng.choice([-448.0, 448.0]) * 2.0**a
+                x[t, cols_t[1:]] = rng.choice([-3.0, -2.0, -1.0, 1.0, 2.0, 3.0], size=2) * 2.0**a
+                continue
             a = int(rng.integers(-3, 4))
             cols_t = rng.choice(BLOCK, size=4, replace=False) + g * BLOCK
             x[t, cols_t[0]] = rng.choice([-448.0, 448.0]) * 2.0**a

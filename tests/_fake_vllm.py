@@ -1,9 +1,10 @@
 """A stand-in for the few vLLM names the plugin touches (vLLM is not installed).
 
 Installs modules ``vllm.config``, ``vllm.logger``,
-``vllm.model_executor.layers.fused_moe.oracle.fp8`` and
-``vllm.model_executor.layers.fused_moe.routed_experts`` into ``sys.modules``
-with a ``RoutedExperts`` base that carries the layer's ``activation``,
+``vllm.model_executor.layers.fused_moe.oracle.fp8``,
+``vllm.model_executor.layers.fused_moe.routed_experts`` and
+``...fused_moe.shared_experts`` (a ``SharedExperts`` that records its calls
+and keeps its output) into ``sys.modules`` with a ``RoutedExperts`` base that carries the layer's ``activation``,
 ``apply_router_weight_on_input`` and shared experts (as vLLM's MoE layers
 do) and creates block-fp8 expert parameters the way a w8a8 block-quantised
 MoE layer does: ``w13_weight (E, 2I, H)``,
@@ -38,6 +39,21 @@ class _QuantMethod:
 
     def process_weights_after_loading(self, layer) -> None:
         self.processed += 1
+
+
+class SharedExperts(torch.nn.Module):
+    """Shared experts as the MoE kernel sees them: called once with their
+    input, they keep their output themselves. Records every input."""
+
+    def __init__(self) -> None:
+        super().__init__()
+        self.inputs: list[torch.Tensor] = []
+        self.output: torch.Tensor | None = None
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        self.inputs.append(x)
+        self.output = x * 2
+        return self.output
 
 
 class RoutedExperts(torch.nn.Module):
@@ -101,6 +117,7 @@ def install() -> None:
         mod(pkg)
     mod("vllm.model_executor.layers.fused_moe.oracle.fp8", Fp8MoeBackend=Fp8MoeBackend)
     mod("vllm.model_executor.layers.fused_moe.routed_experts", RoutedExperts=RoutedExperts)
+    mod("vllm.model_executor.layers.fused_moe.shared_experts", SharedExperts=SharedExperts)
 
 
 def uninstall() -> None:

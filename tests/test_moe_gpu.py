@@ -80,7 +80,8 @@ def _check_close(got: np.ndarray, ref: np.ndarray, what: str) -> None:
 
 @pytest.mark.parametrize("E, T, topk, seed", [(64, 150, 4, 0), (8, 8, 8, 108)], ids=["wide", "narrow"])
 def test_exact_inputs_bit_exact(E, T, topk, seed):
-    """On inputs where every sum is exact and SiLU is exact (moe_ref.exact_inputs),
+    """On inputs where every sum is exact and every SiLU is exact or rounds to
+    bf16 unambiguously (moe_ref.exact_inputs),
     the kernels' output is decided by their rounding sequence alone, and it
     equals the oracle's bit for bit, for the prefill-sized kernels (tile bound
     >= 64) and the decode-sized ones. test_oracle_moe.py shows that each

@@ -86,7 +86,7 @@ def test_expert_ffn_one_hot_closed_form():
         h = (c * col).astype(np.float32)
         gate, up = M.bf16(h[:I]), M.bf16(h[I:])
         with np.errstate(over="ignore"):
-            a = M.bf16((gate / (np.float32(1) + np.exp(-gate))).astype(np.float32) * up)
+            a = M.bf16(M.bf16((gate / (np.float32(1) + np.exp(-gate))).astype(np.float32)) * up)
         aq, as_ = M.quant_groups(a[None, :])
         ad = v[aq[0]] * np.repeat(as_[0].astype(np.float64), 128)
         y = ad[(np.arange(H) + 5 * e) % I].astype(np.float32)
@@ -136,11 +136,12 @@ EXACT_CASES = [(64, 150, 4, 0), (8, 8, 8, 108)]
 
 @pytest.mark.parametrize("E, T, topk, seed", EXACT_CASES)
 def test_exact_inputs_tell_every_rounding_step_apart(E, T, topk, seed):
-    """On exact_inputs every sum is exact and SiLU is exact, so the output is
-    decided by the rounding sequence alone; each planted mistake in that
+    """On exact_inputs every sum is exact and every SiLU is exact or rounds to
+    bf16 unambiguously, so the output is decided by the rounding sequence alone; each planted mistake in that
     sequence (M.VARIANTS) changes it. A GPU kernel that equals the oracle bit
     for bit on these inputs (tests/test_moe_gpu.py) therefore rounds gate and
-    up to bf16 to nearest even, rounds silu(gate) * up to bf16, divides by
+    up to bf16 to nearest even, rounds silu(gate) to bf16 and then
+    bf16(silu(gate)) * up to bf16, divides by
     amax / 448, converts to fp8 to nearest even and weights y before its one
     bf16 rounding."""
     rng = np.random.default_rng(seed)
@@ -152,9 +153,11 @@ def test_exact_inputs_tell_every_rounding_step_apart(E, T, topk, seed):
 
 
 def test_exact_inputs_keep_their_promises():
-    """Group scales of x are powers of two, every gate is 0 or of magnitude
-    >= 104 (exp(-|g|) below half an fp32 ulp of 1, exp(|g|) beyond fp32), and
-    every block dot is an integer below 2^11 (exact in any fp32 accumulation)."""
+    """Group scales of x are powers of two; every gate of the first 128 rows
+    is 0 or of magnitude >= 104 (exp(-|g|) below half an fp32 ulp of 1,
+    exp(|g|) beyond fp32); every probe gate (rows 128-255) is non-zero with
+    silu(g) at least PROBE_MARGIN from a bf16 rounding midpoint; every
+    block dot is an integer below 2^11 (exact in any fp32 accumulation)."""
     rng = np.random.default_rng(5)
     x, tw, ids, w13, w13s, w2, w2s = M.exact_inputs(rng, 8, 512, 256, 64, 4)
     xq, xs = M.quant_groups(x)
@@ -167,6 +170,9 @@ def test_exact_inputs_keep_their_promises():
         dots = np.einsum("tgk,ngk->tng", xv, w)
         assert np.all(dots == np.round(dots)) and np.abs(dots).max() < 2**11
         gate = (M.dequant_rows(xq, xs) @ M.dequant_weight(w13[e], w13s[e]).T)[:, :256]
-        nz = gate[gate != 0]
+        nz = gate[:, :128][gate[:, :128] != 0]
         assert nz.size and np.abs(nz).min() >= 104
+        probe = gate[:, 128:]
+        assert (probe != 0).all() and np.abs(probe).min() >= 2.0**-5 and np.abs(probe).max() <= 24
+        assert M.bf16_midpoint_margin(probe / (1 + np.exp(-probe))).min() >= M.PROBE_MARGIN
     assert ((w2 != 0).sum(axis=2) == 1).all()

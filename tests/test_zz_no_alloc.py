@@ -5,10 +5,16 @@ caller-provided workspace) on the same routing, twice in a row on one device
 with the second call smaller than the first: a prefill-sized call (the wide
 GEMM kernels) then a decode-sized one (the narrow kernels), which leaves the
 first call's contents in the shared array. A call whose workspace would not
-fit is refused with XP_E_LIMIT before anything is launched.
+fit is refused with XP_E_LIMIT before anything is launched. The static
+array sits in a code object of its own, so a process that never calls the
+no-alloc entry point does not give up its 32 MiB.
 """
 
 import ctypes
+import json
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -81,3 +87,36 @@ def test_noalloc_refuses_a_workspace_above_its_limit():
     assert rc == nat.XP_E_LIMIT
     assert b"above the library's" in lib.xp_last_error()
     torch.cuda.synchronize()
+
+
+_MEMORY_PROBE = """
+import json, sys
+sys.path[:0] = sys.argv[1:]
+import numpy as np, torch
+torch.zeros(1, device="cuda"); torch.cuda.synchronize()
+from test_zz_no_alloc import _inputs, _run
+
+def snap():
+    torch.cuda.synchronize()
+    return torch.cuda.mem_get_info()[0], torch.cuda.memory_reserved()
+
+case = _inputs(np.random.default_rng(0), 32, 2048, 512, 3, 8)
+s0 = snap(); _run("xp_moe_experts", *case); s1 = snap()
+_run("xp_moe_experts_noalloc", *case); s2 = snap()
+outside = lambda a, b: ((a[0] - b[0]) - (b[1] - a[1])) / 2**20
+print(json.dumps({"first_experts_mib": outside(s0, s1), "first_noalloc_mib": outside(s1, s2)}))
+"""
+
+
+def test_noalloc_array_is_reserved_only_when_called():
+    """In a fresh process, device memory taken outside torch's allocator:
+    the first xp_moe_experts launch loads the expert kernels without the
+    32 MiB array; the first xp_moe_experts_noalloc call then reserves it."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = [root, os.path.join(root, "vllm-expert-pager_amd"), here]
+    r = subprocess.run([sys.executable, "-c", _MEMORY_PROBE, *paths], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    got = json.loads(r.stdout.strip().splitlines()[-1])
+    assert got["first_experts_mib"] < 16, got
+    assert got["first_noalloc_mib"] >= 32, got

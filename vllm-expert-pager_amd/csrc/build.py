@@ -39,7 +39,7 @@ GPU_FLAGS = [
 ]
 HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
-GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "encode.hip", "moe.hip"]
+GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "encode.hip", "moe.hip", "scratch.hip"]
 HIP_HOST_SOURCES = ["host.cpp", "codec_host.cpp"]  # HIP runtime API or headers
 HOST_SOURCES = ["error.cpp", "ssd.cpp", "ssd_probe.cpp"]
 

@@ -26,6 +26,10 @@ int check_launch(const char* what);
 // (hipDeviceAttributeWallClockRate), cached per device.
 int64_t wallclock_ticks_per_us();
 
+// Device address of the no-alloc expert workspace (scratch.hip) on the
+// current device, XP_MOE_SCRATCH_BYTES long; looked up once per device.
+int moe_scratch_address(uint8_t** out);
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 

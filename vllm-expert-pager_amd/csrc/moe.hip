@@ -14,7 +14,9 @@
 // Numerics of one pair follow the rounding sequence of a w8a8 block-fp8 MoE:
 // x -> fp8 per 128-group (scale = max(amax, 1e-10) / 448, q = clamp(x / s));
 // h = sum over K blocks of (xq . wq) * (sx * sw) in fp32; gate, up -> bf16;
-// a = bf16(silu(gate) * up); a -> fp8 per 128-group; y likewise with w2;
+// a = bf16(bf16(silu(gate)) * up) (silu is returned in bf16 and then
+// multiplied, as vLLM's silu_and_mul does); a -> fp8 per 128-group; y
+// likewise with w2;
 // contribution = bf16(y * routed weight).
 //
 // Work decomposition: route lists the pairs of each slab slot in CSR form
@@ -534,7 +536,7 @@ __device__ __forceinline__ AOffsets a_offsets(const int* s_row, int64_t lda, int
 // GEMM1 at prefill sizes: gate and up for 128 activation columns of a wide
 // tile per item; each wave owns 16 columns (16 gate and 16 up rows) and runs
 // the K blocks in order, so a column's value does not depend on the
-// workgroup width or the tile height. Then a = bf16(silu(bf16 gate) *
+// workgroup width or the tile height. Then a = bf16(bf16(silu(bf16 gate)) *
 // bf16 up) is quantised to fp8 per row over the workgroup's 128 columns, one
 // scale group. Only the 16-row subtiles that hold pairs are multiplied.
 __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* __restrict__ xq,
@@ -706,7 +708,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float gv = bf16_round(acc[mi][0][r]), uv = bf16_round(acc[mi][1][r]);
-          const float a = bf16_round(gv / (1.0f + expf(-gv)) * uv);
+          const float a = bf16_round(bf16_round(gv / (1.0f + expf(-gv))) * uv);
           acc[mi][0][r] = a;
           float m = fabsf(a);
           m = row16_max(m);
@@ -891,7 +893,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
-      const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+      const float a = bf16_round(bf16_round(g / (1.0f + expf(-g))) * u);
       float m = fabsf(a);
       m = row16_max(m);
       const int row = 4 * q + r;
@@ -1116,7 +1118,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
-      const float a = bf16_round(g / (1.0f + expf(-g)) * u);
+      const float a = bf16_round(bf16_round(g / (1.0f + expf(-g))) * u);
       float m = fabsf(a);
       m = row16_max(m);
       const int row = 4 * q + r;
@@ -1807,42 +1809,6 @@ int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
 }  // namespace
 }  // namespace xp
 
-// Workspace of xp_moe_experts_noalloc, one copy on every device the library
-// runs on (held until the process ends). Host code never passes this name to
-// a kernel: it stands for the host-side shadow, and each device's own
-// address comes from hipGetSymbolAddress (scratch_address).
-static __device__ __align__(256) uint8_t scratch[XP_MOE_SCRATCH_BYTES];
-
-namespace xp {
-namespace {
-
-constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-uint8_t* g_scratch[kMaxDevices];  // device address of `scratch`, per device
-
-// The current device's address of `scratch`, looked up on the first call on
-// that device (with it current) and kept.
-int scratch_address(uint8_t** out) {
-  int dev = -1;
-  XP_HIP(hipGetDevice(&dev));
-  XP_REQUIRE(dev >= 0 && dev < kMaxDevices, "xp_moe_experts_noalloc: device %d (at most %d devices)", dev,
-             kMaxDevices);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch[dev] == nullptr) {
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr)
-      return fail(XP_E_HIP, "xp_moe_experts_noalloc: hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
-                  hipGetErrorString(e));
-    g_scratch[dev] = static_cast<uint8_t*>(p);
-  }
-  *out = g_scratch[dev];
-  return XP_OK;
-}
-
-}  // namespace
-}  // namespace xp
-
 extern "C" {
 
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
@@ -1875,7 +1841,7 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T, int64_
                 "%lld B; call xp_moe_experts with a workspace instead",
                 (long long)(T * topk), (long long)I, (long long)need, (long long)XP_MOE_SCRATCH_BYTES);
   uint8_t* work = nullptr;
-  rc = scratch_address(&work);
+  rc = moe_scratch_address(&work);
   if (rc) return rc;
   return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
                         tiles, work, out, stream);

@@ -125,6 +125,15 @@ def encode(raw: torch.Tensor, pitch: int, chunk: int = CHUNK) -> tuple[torch.Ten
     return torch.from_numpy(record).to(raw.device), torch.from_numpy(lut).to(raw.device)
 
 
+def _require_rows(t: torch.Tensor, what: str, i: int) -> None:
+    """A 2-D contiguous GPU tensor: the kernels address row r at
+    ``r * shape[1] * element_size`` bytes from its start."""
+    nat.require_device(t, f"{what}[{i}]")
+    if t.dim() != 2 or not t.is_contiguous():
+        raise ValueError(f"{what}[{i}] must be a contiguous 2-D tensor of rows, got shape {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+
+
 def decode_rows(
     todo: torch.Tensor,
     dst_row: torch.Tensor,
@@ -154,9 +163,13 @@ def decode_rows(
         raise ValueError(f"lut has {lut.numel()} B, needs {E} x {n} x {LUT_BYTES}")
     if skip_t is not None and skip_t.shape[0] < todo.shape[0]:
         raise ValueError("skip must have at least as many entries as todo")
+    if len(staging) != n:
+        raise ValueError("staging and dst need one entry per name")
     names = (nat.XpDecodeName * n)()
     for i in range(n):
         s, d = staging[i], dst[i]
+        _require_rows(s, "staging", i)
+        _require_rows(d, "dst", i)
         names[i] = nat.XpDecodeName(
             s.data_ptr(), s.shape[1] * s.element_size(), s.shape[0],
             d.data_ptr(), d.shape[0], d.shape[1] * d.element_size(),
@@ -215,8 +228,9 @@ def decode_rows_from_ram(
     names = (nat.XpDecodeName * n)()
     scales = (nat.XpDecodeScale * n)()
     for i in range(n):
-        sp, srows, spitch = _rows(src[i])
         d, c, cd = dst[i], scale[i], scale_dst[i]
+        _require_rows(d, "dst", i)
+        sp, srows, spitch = _rows(src[i])
         for t, what in ((c, "scale"), (cd, "scale_dst")):
             nat.require_device(t, what)
             if not t.is_contiguous():

@@ -10,11 +10,16 @@ built right after it; ``forward_modular`` runs the decode or the prefill
 overflow path of the layer's ``PagedExperts`` (pager.py). The expert FFN is
 this package's own fp8 MFMA kernels (csrc/moe.hip) rather than vLLM's fused
 MoE, so no ``moe_sum`` intercept is needed: the top-k sum runs once by
-construction. Because those kernels compute only ``silu(gate) * up`` with the
-routed weight applied to each expert's output, layers that ask for another
-activation, for ``apply_router_weight_on_input`` or for shared experts are
-refused with ``RuntimeError``. Settings are the ``VLLM_EXPERT_PAGER_*``
-environment variables, read at import.
+construction. Shared experts handed to ``forward_modular`` run once per
+forward, right before the first expert launch (the reference passes them to
+the decode run and to chunk 0 of the overflow path, experts.py:452, 569-573),
+and the routed sum alone is returned, the shared output staying with the
+shared experts object (experts.py:475-477). ``apply_router_weight_on_input``
+scales the tokens by their routed weight before the experts and leaves the
+outputs unweighted, as vLLM's no-EP prepare step does (top-k must be 1).
+The kernels compute ``silu(gate) * up``, so layers that ask for another
+activation are refused with ``RuntimeError``. Settings are the
+``VLLM_EXPERT_PAGER_*`` environment variables, read at import.
 
 Importing this module requires vLLM; ``plugin.register`` imports it only
 after vLLM has loaded.
@@ -51,13 +56,11 @@ def _mode_name(value) -> str:
 def _unsupported_modes(layer) -> list[str]:
     """What the layer asks of the expert FFN that csrc/moe.hip does not compute.
 
-    The kernels compute ``silu(gate) * up`` over w13's gate rows then up rows,
-    multiply each pair's output by its routed weight after ``w2`` and return
-    the routed sum alone. The reference leaves all of this to vLLM's fused MoE
-    (experts.py:594-600), which reads the layer's ``activation`` and
-    ``apply_router_weight_on_input`` (on the layer or its ``moe_config``) and
-    runs any shared experts. Each mode the kernels would get silently wrong is
-    listed here so construction can refuse it.
+    The kernels compute ``silu(gate) * up`` over w13's gate rows then up
+    rows. The reference leaves the activation to vLLM's fused MoE
+    (experts.py:594-600), which reads the layer's ``activation`` (on the
+    layer or its ``moe_config``). Each activation the kernels would get
+    silently wrong is listed here so construction can refuse it.
     """
     found = []
     for owner in (layer, getattr(layer, "moe_config", None)):
@@ -68,13 +71,17 @@ def _unsupported_modes(layer) -> list[str]:
             found.append(f"activation {_mode_name(act)!r} (the kernels compute silu(gate) * up)")
         if getattr(owner, "is_act_and_mul", True) is False:
             found.append("an activation without the gate/up product")
-        if getattr(owner, "apply_router_weight_on_input", False):
-            found.append("apply_router_weight_on_input (the kernels weight each expert's output)")
-    for name in ("shared_experts", "_shared_experts"):
-        if getattr(layer, name, None) is not None:
-            found.append("shared experts (their output contract belongs to vLLM's modular kernel)")
-            break
     return list(dict.fromkeys(found))
+
+
+def _router_weight_on_input(layer) -> bool:
+    """Whether the layer (or its ``moe_config``) applies the routed weight to
+    the expert input instead of the expert output."""
+    return any(
+        bool(getattr(owner, "apply_router_weight_on_input", False))
+        for owner in (layer, getattr(layer, "moe_config", None))
+        if owner is not None
+    )
 
 
 class ExpertPagerRoutedExperts(RoutedExperts):
@@ -210,19 +217,32 @@ class ExpertPagerRoutedExperts(RoutedExperts):
         shared_experts=None,
         shared_experts_input: torch.Tensor | None = None,
     ) -> torch.Tensor:
-        # The reference hands shared experts to vLLM's modular kernel, which
-        # keeps their output inside SharedExperts (experts.py:475-477, 594-600).
-        # That contract is vLLM's and is not reproduced here, so a layer that
-        # passes them is refused rather than given a routed-only result.
+        # The reference hands shared experts to vLLM's modular kernel with the
+        # first expert run of the forward (experts.py:452, 569-573); that run
+        # returns the routed output alone and the shared output stays inside
+        # the shared experts object (experts.py:475-477). The pager calls this
+        # once, right before its first expert launch.
+        shared = None
         if shared_experts is not None:
-            raise RuntimeError(
-                f"{self.layer_name}: vllm-expert-pager runs its own fp8 expert kernels, which do not "
-                "support shared experts (their output contract belongs to vLLM's modular kernel)"
-            )
+            shared_input = x if shared_experts_input is None else shared_experts_input
+
+            def shared() -> None:
+                shared_experts(shared_input)
+
+        if _router_weight_on_input(self):
+            # vLLM's prepare step for this mode scales the tokens by their
+            # routed weight (rounded to the token dtype) and the experts then
+            # add their outputs unweighted; it allows top-k 1 only.
+            if topk_ids.shape[1] != 1:
+                raise RuntimeError(
+                    f"{self.layer_name}: apply_router_weight_on_input needs top-k 1, got {topk_ids.shape[1]}"
+                )
+            x = x * topk_weights.to(x.dtype)
+            topk_weights = torch.ones_like(topk_weights, dtype=torch.float32)
         pager = self._expert_pager
         self._expert_pager_expert_map = pager.expert_map
         try:
-            return pager.forward(x, topk_weights, topk_ids)
+            return pager.forward(x, topk_weights, topk_ids, shared)
         finally:
             self._expert_pager_expert_map = None
 

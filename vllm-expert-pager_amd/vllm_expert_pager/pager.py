@@ -19,6 +19,7 @@ from __future__ import annotations
 import logging
 import os
 from dataclasses import dataclass
+from typing import Callable
 
 import torch
 
@@ -208,8 +209,16 @@ class PagedExperts:
 
     # ---- forward ----
 
-    def forward(self, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
-        """The routed-expert output ``(T, H)`` bf16 of this layer (experts.py:380-453)."""
+    def forward(self, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                shared: Callable[[], object] | None = None) -> torch.Tensor:
+        """The routed-expert output ``(T, H)`` bf16 of this layer (experts.py:380-453).
+
+        ``shared``, if given, runs the layer's shared experts. It is called
+        once per forward, right before the first expert launch: on the
+        decode path before the expert FFN, on the overflow path before
+        chunk 0's (experts.py:452, 569-573). Its result is not part of the
+        returned routed sum.
+        """
         if not self.ready:
             raise RuntimeError(f"layer {self.layer}: setup() has not run")
         store = self.store
@@ -220,7 +229,7 @@ class PagedExperts:
         # The path is chosen from the shape alone, so capture and replay of a
         # graph take the same path.
         if topk_ids.numel() > self.table.num_slots:
-            return self._forward_working(x, topk_weights, topk_ids)
+            return self._forward_working(x, topk_weights, topk_ids, shared)
 
         layer, E = self.layer, self.pager.num_experts
         with trace.range(f"expert_pager L{layer} acquire"):
@@ -271,6 +280,8 @@ class PagedExperts:
             with trace.range(f"expert_pager L{layer} gather ssd rows"):
                 gather_rows(ssd_todo, dst_row, cached_row, src_row, base, *rows)
 
+        if shared is not None:
+            shared()
         with trace.range(f"expert_pager L{layer} experts"):
             if moe.decode_fits(x, topk_ids, self.pager.intermediate):
                 slab = self.cache_slab
@@ -284,7 +295,8 @@ class PagedExperts:
         self._log()
         return moe.topk_sum(contrib, topk_ids, E)
 
-    def _forward_working(self, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
+    def _forward_working(self, x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+                         shared: Callable[[], object] | None = None) -> torch.Tensor:
         """Prefill (K > S): the experts go through the W-row working slab in chunks (experts.py:455-577).
 
         The VRAM table is not updated; VRAM hits are copied raw from the cache
@@ -294,6 +306,7 @@ class PagedExperts:
         copy the experts that were read -> run the experts of chunk k. Every
         pair's contribution is written once; the top-k sum runs once at the
         end, so the result is that of a single run over all experts.
+        ``shared`` runs once, before chunk 0's experts.
         """
         p, store = self.pager, self.store
         vram, ram = self.table, self.ram
@@ -343,6 +356,8 @@ class PagedExperts:
                     fetch_wait_rows(chunk(ssd, k), store, ticket(k))
                 copy(chunk(late, k))
                 self.expert_map.copy_(maps[k])
+                if k == 0 and shared is not None:
+                    shared()
                 self._run(p.working_slab, xq, xs, topk_weights, topk_ids, contrib)
         self._log()
         return moe.topk_sum(contrib, topk_ids, E)
