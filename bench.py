@@ -735,6 +735,7 @@ def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None)
     torch.cuda.synchronize()
     before = [lay.hit_rates() for lay in layers]
     ssd0 = (store.fetches, store.reads, store.io_seconds) if store.path else None
+    ph0 = store.phase_stats() if store.path else None
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
@@ -747,7 +748,8 @@ def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None)
     ssd = None
     if ssd0 is not None:
         ssd = {"fetches": store.fetches - ssd0[0], "reads": store.reads - ssd0[1],
-               "io_seconds": round(store.io_seconds - ssd0[2], 4), "failed": store.failed}
+               "io_seconds": round(store.io_seconds - ssd0[2], 4), "failed": store.failed,
+               "phases": _phase_delta(store.phase_stats(), ph0)}
     # The paging path alone on a continuing trace: acquire, gather (+ SSD
     # fetch, expansion), expert FFN and top-k sum of the 40 layers in one graph.
     x = torch.randn((1, H), device=dev).to(torch.bfloat16)
@@ -830,8 +832,8 @@ def bench_model_decode_compressed(args, dev):
 
 
 def disk_ceiling(path: str, record_bytes: int, records: int, seconds: float = 0.5) -> dict:
-    """Record-sized O_DIRECT reads of the paging file at 1, 8 and 32 in flight, from a thread pool
-    (the SSD server's way) and from io_uring: the disk's ceiling in this run."""
+    """Record-sized O_DIRECT reads of the paging file at 1, 2, 4, 8 and 32 in flight, from a thread
+    pool (the SSD server's way) and from io_uring: the disk's ceiling in this run."""
     from vllm_expert_pager import _native
 
     lib = _native.lib()
@@ -842,7 +844,7 @@ def disk_ceiling(path: str, record_bytes: int, records: int, seconds: float = 0.
     try:
         # Two passes in different orders; each configuration keeps its better pass (a disk that
         # has just been written can serve some reads from its own cache).
-        for order in ((8, 32, 1), (1, 32, 8)):
+        for order in ((8, 32, 4, 2, 1), (1, 2, 4, 32, 8)):
             for mode, name in ((0, "threads"), (1, "io_uring")):
                 for depth in order:
                     # about `seconds` of reads at 3 GB/s, at least 4 per reader
@@ -863,6 +865,104 @@ def disk_ceiling(path: str, record_bytes: int, records: int, seconds: float = 0.
         out.setdefault(f"{name}_gbps", {})[depth] = max(nums) if nums else vals[-1]
         out.setdefault(f"{name}_passes", {})[depth] = vals
     log(f"disk ceiling: {out}")
+    return out
+
+
+def _phase_delta(after: dict, before: dict) -> dict:
+    out = {k: round(after[k] - before.get(k, 0), 4) for k in ("busy_s", "queue_s", "read_s", "copy_s", "preads")}
+    out.update(readers=after["readers"], bounce=after["bounce"])
+    return out
+
+
+def server_sweep(store, path: str, readers=(1, 2, 4, 8), seconds: float = 0.6) -> dict:
+    """The SSD server alone, driven from the host: a second server instance on the paging file and
+    the pinned RAM tier, at several reader counts, for requests of 8 random records (the size of a
+    prefill chunk's SSD listing; two kept outstanding, as chunks are published one ahead) and of
+    one record (a decode step's miss, one at a time). It writes only the working rows."""
+    from vllm_expert_pager import _native
+
+    lib = _native.lib()
+    names = store.names
+    n, rb = len(names), store.record_bytes
+    ring, block = 4, 16
+    slot_words = 2 + 2 * block
+    records = store.num_layers * store.num_experts
+    rng = np.random.default_rng(19)
+
+    def aligned(count):
+        raw = np.zeros(count + 512, np.int64)
+        off = (-raw.ctypes.data % 4096) // 8
+        return raw[off : off + count]
+
+    out = {"record_bytes": rb, "readers": {}}
+    fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+    try:
+        for nr in readers:
+            req, done = aligned(2 + ring * slot_words), aligned(512)
+            pinned = (ctypes.c_void_p * n)(*(store.pinned[k].data_ptr() for k in names))
+            pitch = (ctypes.c_long * n)(*(store.pitch[k] for k in names))
+            h = lib.ssd_start(fd, ctypes.c_void_p(req.ctypes.data), ctypes.c_void_p(done.ctypes.data), ring, block,
+                              store.num_layers, store.num_experts, store.rows, rb, n, pinned, pitch, nr - 1)
+            if not h:
+                out["readers"][str(nr)] = "ssd_start failed"
+                continue
+            seq = 0
+
+            def publish(k, first_row):
+                nonlocal seq
+                seq += 1
+                rec = rng.choice(records, size=k, replace=False)
+                base = 2 + (seq % ring) * slot_words
+                req[base + 2 : base + 2 + block] = -1
+                req[base + 2 : base + 2 + k] = rec % store.num_experts  # layer taken from the first
+                req[base + 1] = int(rec[0] // store.num_experts)
+                req[base + 2 + block : base + 2 + block + k] = first_row + np.arange(k)
+                req[base] = seq
+                return seq
+
+            def wait(s_):
+                t_end = time.perf_counter() + 30.0
+                while int(done[0]) < s_:
+                    if time.perf_counter() > t_end:
+                        raise RuntimeError(f"server sweep: done stuck at {int(done[0])} < {s_}")
+
+            try:
+                wb = store.working_base
+                # 8-record requests, two outstanding
+                t0 = time.perf_counter()
+                pending = [publish(8, wb)]
+                reqs = 0
+                while time.perf_counter() - t0 < seconds or reqs < 4:
+                    pending.append(publish(8, wb + 8 * (len(pending) % 2)))
+                    wait(pending.pop(0))
+                    reqs += 1
+                wait(pending.pop(0))
+                reqs += 1
+                t8 = time.perf_counter() - t0
+                # one record at a time
+                t0 = time.perf_counter()
+                ones = 0
+                while time.perf_counter() - t0 < seconds / 2 or ones < 8:
+                    wait(publish(1, wb))
+                    ones += 1
+                t1 = time.perf_counter() - t0
+                b, q, r, c = (ctypes.c_double() for _ in range(4))
+                preads, nrd, bounce = ctypes.c_long(), ctypes.c_int(), ctypes.c_int()
+                lib.xp_ssd_phase_stats(ctypes.c_void_p(h), ctypes.byref(b), ctypes.byref(q), ctypes.byref(r),
+                                       ctypes.byref(c), ctypes.byref(preads), ctypes.byref(nrd), ctypes.byref(bounce))
+                err = lib.ssd_error(ctypes.c_void_p(h))
+            finally:
+                lib.ssd_stop(ctypes.c_void_p(h))
+            out["readers"][str(nr)] = {
+                "gbps_8_record_requests": round(reqs * 8 * rb / t8 / 1e9, 3),
+                "ms_per_1_record_request": round(t1 / ones * 1e3, 3),
+                "read_s": round(r.value, 3), "copy_s": round(c.value, 3), "queue_s": round(q.value, 3),
+                "preads": preads.value, "bounce": bool(bounce.value),
+                "error": err.decode() if err else None,
+            }
+    finally:
+        os.close(fd)
+    log(f"server sweep: {out}")
     return out
 
 
@@ -895,6 +995,7 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
     store = pager.store
     try:
         ceiling = disk_ceiling(path, store.record_bytes, L * E)
+        sweep = server_sweep(store, path)
         g = torch.Generator(device=dev).manual_seed(77)
         xs, ws, ids = [], [], []
         for l in range(L):
@@ -904,6 +1005,7 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
             ids.append(i)
         torch.cuda.synchronize()
         f0, r0, io0 = store.fetches, store.reads, store.io_seconds
+        ph0 = store.phase_stats()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record()
@@ -927,6 +1029,7 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
             "ssd_fetches": store.fetches - f0,
             "ssd_reads": store.reads - r0,
             "ssd_io_seconds": round(store.io_seconds - io0, 3),
+            "ssd_phases": _phase_delta(store.phase_stats(), ph0),
             "layers_bit_exact_vs_one_shot": f"{exact}/{L}",
         }
         log(f"prefill: {prefill}")
@@ -939,18 +1042,25 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
                               "rows compressed at pitch 0.89, the rest read from the paging file (O_DIRECT), "
                               f"batch 1, top-8, Zipf(1.1) with 0.7 reuse, {steps} steps in one "
                               "captured hipGraph per step", steps=steps)
-        # The server's read rate while it has requests (reads x record / time serving them),
-        # against the ceiling at its own depth (the server thread and 7 workers: 8 in flight).
+        # The server's read rate while it has a request in flight (records read x record bytes /
+        # busy seconds; requests overlap, so the summed request time would undercount), against
+        # the disk's ceiling at the server's own depth (its reader threads) and at 1 (a decode
+        # step's miss is read alone).
         rb = store.record_bytes
-        top = ceiling.get("threads_gbps", {}).get("8")
-        for leg, reads, io in (("prefill", prefill["ssd_reads"], prefill["ssd_io_seconds"]),
-                               ("decode", (decode.get("ssd") or {}).get("reads", 0),
-                                (decode.get("ssd") or {}).get("io_seconds", 0.0))):
-            rate = reads * rb / io / 1e9 if io > 0 else None
-            tgt = prefill if leg == "prefill" else decode
+        tops = ceiling.get("threads_gbps", {})
+        for tgt, reads, phases in ((prefill, prefill["ssd_reads"], prefill["ssd_phases"]),
+                                   (decode, (decode.get("ssd") or {}).get("reads", 0),
+                                    (decode.get("ssd") or {}).get("phases", {}))):
+            busy = phases.get("busy_s", 0.0)
+            rate = reads * rb / busy / 1e9 if busy > 0 else None
             tgt["ssd_gbps_while_reading"] = round(rate, 3) if rate else None
-            tgt["ssd_frac_of_disk_ceiling_8"] = round(rate / top, 3) if rate and isinstance(top, float) else None
-        return {"disk_ceiling": ceiling, "prefill": prefill, "decode": decode}
+            for name, depth in (("server_depth", str(store.readers)), ("1", "1")):
+                top = tops.get(depth)
+                tgt[f"ssd_frac_of_disk_ceiling_{name}"] = (
+                    round(rate / top, 3) if rate and isinstance(top, float) else None)
+        server = {"readers": store.readers, "sized_from_probe_gbps": store.reader_probe}
+        return {"disk_ceiling": ceiling, "server": server, "server_sweep": sweep, "prefill": prefill,
+                "decode": decode}
     finally:
         pager.close()
         if os.path.exists(path):

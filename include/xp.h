@@ -313,6 +313,20 @@ void ssd_stats(ssd_t* s, long* fetches, long* reads, double* io_seconds,
                long* missed);
 const char* ssd_error(ssd_t* s);
 void ssd_test_delay(ssd_t* s, double seconds);
+/* No counterpart in the reference, whose stats give fetches, reads and the
+ * summed request time only: the seconds with at least one request in flight
+ * (requests overlap, so this is below the summed time), and where the time
+ * went, summed over the records read -- seconds a record waited in the
+ * readers' queue, seconds in preadv, seconds copying out of bounce buffers
+ * (all copy chunks) -- with the records read (one preadv each), the reader
+ * threads, and whether reads go through bounce buffers (the pinned rows
+ * refused O_DIRECT). */
+/* No counterpart in the reference (a test hook like ssd_test_delay): read
+ * through the bounce buffers from now on, as when the pinned rows refuse
+ * O_DIRECT, so tests on ordinary host memory cover that path. */
+void xp_ssd_test_bounce(ssd_t* s);
+void xp_ssd_phase_stats(ssd_t* s, double* busy_s, double* queue_s, double* read_s,
+                        double* copy_s, long* preads, int* readers, int* bounce);
 
 /* ---- MoE expert compute on the slab (prefill overflow and decode) ----
  * These replace the vLLM fused fp8 MoE the reference hands expert_map to

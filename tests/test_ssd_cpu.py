@@ -79,23 +79,29 @@ def pattern(layer, e, name):
 
 
 class Server:
-    def __init__(self, path, nworkers=7, which="xp"):
+    def __init__(self, path, nworkers=7, which="xp", pitches=PITCH):
         self.lib = _lib(which)
+        self.pitches = pitches
         with open(path, "wb") as f:
             for layer in range(L):
                 for e in range(E):
-                    f.write(pattern(layer, e, 0).tobytes() + pattern(layer, e, 1).tobytes())
+                    f.write(b"".join(self.expected(layer, e, n).tobytes() for n in range(len(pitches))))
         self.fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
         self.rows = L * R + 2 * W
         self.req = aligned(8 * (2 + RING * (2 + 2 * BLOCK)), np.int64)
         self.done = aligned(4096, np.int64)[:1]
-        self.pinned = [aligned(self.rows * p).view(np.int32).reshape(self.rows, -1) for p in PITCH]
-        ptrs = (ctypes.c_void_p * 2)(*(a.ctypes.data for a in self.pinned))
-        pitch = (ctypes.c_long * 2)(*PITCH)
+        self.pinned = [aligned(self.rows * p).view(np.int32).reshape(self.rows, -1) for p in pitches]
+        ptrs = (ctypes.c_void_p * len(pitches))(*(a.ctypes.data for a in self.pinned))
+        pitch = (ctypes.c_long * len(pitches))(*pitches)
         self.h = self.lib.ssd_start(self.fd, self.req.ctypes.data, self.done.ctypes.data, RING, BLOCK, L, E,
-                                    self.rows, RECORD, 2, ptrs, pitch, nworkers)
+                                    self.rows, sum(pitches), len(pitches), ptrs, pitch, nworkers)
         assert self.h
         self.seq = 0
+
+    def expected(self, layer, e, name):
+        if self.pitches == PITCH:
+            return pattern(layer, e, name)
+        return _tiers.expert_row(layer, e, name, self.pitches[name]).view(np.int32)
 
     def publish(self, layer, experts, rows, seq=None):
         seq = self.seq + 1 if seq is None else seq
@@ -264,3 +270,58 @@ def test_read_probe_reads_every_record(tmp_path, use_uring, depth):
         assert lib.xp_ssd_read_probe(fd, rec, past, 1, depth, use_uring, ctypes.byref(sec)) != 0
     finally:
         os.close(fd)
+
+
+@pytest.mark.parametrize("bounce", [False, True], ids=["direct", "bounce"])
+def test_records_larger_than_a_copy_chunk(tmp_path, which, bounce):
+    """Records whose names are longer than 1 MiB (258 and 515 pages, so a
+    bounced copy is cut into 1 MiB chunks with short last ones, spread over
+    the readers) land whole in their rows, one preadv per record."""
+    if bounce and which != "xp":
+        pytest.skip("the bounce hook is this build's")
+    pitches = (258 * 4096, 515 * 4096)
+    s = Server(str(tmp_path / "big.bin"), nworkers=3, which=which, pitches=pitches)
+    if bounce:
+        s.lib.xp_ssd_test_bounce(s.h)
+    try:
+        for i in range(3):
+            experts, rows = [5 + i, 30 - i, 17], [i, R + i, 2 * R + 1]
+            s.wait(s.publish(i % L, experts, rows))
+            for e, row in zip(experts, rows):
+                for n in range(2):
+                    np.testing.assert_array_equal(s.pinned[n][row], s.expected(i % L, e, n))
+        assert s.error() is None and s.stats()[:2] == (3, 9)
+        if which == "xp":
+            bounce_on = bounce
+            b, q, r, c = (ctypes.c_double() for _ in range(4))
+            preads, readers, bounce = ctypes.c_long(), ctypes.c_int(), ctypes.c_int()
+            s.lib.xp_ssd_phase_stats(s.h, ctypes.byref(b), ctypes.byref(q), ctypes.byref(r), ctypes.byref(c),
+                                     ctypes.byref(preads), ctypes.byref(readers), ctypes.byref(bounce))
+            # One read per record; plain host memory takes O_DIRECT, so only the hook bounces.
+            assert preads.value == 9 and readers.value == 4 and bounce.value == int(bounce_on)
+            assert r.value > 0 and q.value >= 0 and (c.value > 0) == bounce_on
+            # Requests one at a time: the busy time is the summed request time.
+            assert abs(b.value - s.stats()[2]) < 1e-3 * max(1.0, b.value)
+    finally:
+        s.close()
+
+
+@pytest.mark.parametrize("bounce", [False, True], ids=["direct", "bounce"])
+def test_requests_published_together_answer_in_order(server, which, bounce):
+    """A long request and a short one published back to back: done reaches
+    the short one's seq only once every row of the long one is in."""
+    if bounce:
+        if which != "xp":
+            pytest.skip("the bounce hook is this build's")
+        server.lib.xp_ssd_test_bounce(server.h)
+    for rep in range(4):
+        a = server.publish(1, list(range(rep, rep + 16)), list(range(16)))
+        b = server.publish(0, [30 + rep], [16 + rep])  # rows 16-19: past the long request's
+        server.wait(b)
+        assert int(server.done[0]) == b
+        for k in range(16):
+            for n in range(2):
+                np.testing.assert_array_equal(server.pinned[n][k], pattern(1, rep + k, n))
+        np.testing.assert_array_equal(server.pinned[0][16 + rep], pattern(0, 30 + rep, 0))
+        assert a == b - 1
+    assert server.stats()[:2] == (8, 4 * 17) and server.error() is None

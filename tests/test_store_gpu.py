@@ -188,10 +188,9 @@ def test_empty_requests_stay_on_the_device(tiers):
 
 
 def test_one_request_uses_every_reader(tiers):
-    """A request of twice as many experts as there are reader threads."""
-    from vllm_expert_pager.store import _read_workers
-
-    n = 2 * _read_workers()
+    """A request of twice as many experts as the most reader threads the
+    server sizes itself to (8)."""
+    n = 16
     t = tiers(layers=1, experts=3 * n, ram=n)
     fetch = Fetch(t, n, layer=0)
     placement = {e: e - 2 * n for e in range(2 * n, 3 * n)}
@@ -200,6 +199,31 @@ def test_one_request_uses_every_reader(tiers):
     assert (t.store.fetches, t.store.reads) == (1, n)
     for e, s in placement.items():
         t.assert_slot_holds(0, s, e)
+
+
+def test_readers_are_sized_from_the_disk_after_sync(tiers, monkeypatch):
+    """sync() probes the paging file at 1, 2, 4 and 8 reads in flight and
+    restarts the server with the depth that read fastest; it still serves the
+    ring afterwards. VLLM_EXPERT_PAGER_READ_WORKERS fixes the count instead."""
+    monkeypatch.delenv("VLLM_EXPERT_PAGER_READ_WORKERS", raising=False)
+    t = tiers(layers=2, experts=12, ram=4)
+    st = t.store
+    assert st.readers == 2 and st.reader_probe is None
+    st.sync()
+    assert set(st.reader_probe) == {"1", "2", "4", "8"} and st.readers in (1, 2, 4, 8)
+    assert all(r > 0 for r in st.reader_probe.values())
+    fetch = Fetch(t, 4, layer=1)
+    fetch({5: 0, 9: 3, 11: 1})
+    assert st.failed is None and (st.fetches, st.reads) == (1, 3)
+    for e, slot in ((5, 0), (9, 3), (11, 1)):
+        t.assert_slot_holds(1, slot, e)
+    assert st.size_readers() is None  # requests were made: the server keeps its seq
+
+    monkeypatch.setenv("VLLM_EXPERT_PAGER_READ_WORKERS", "3")
+    t2 = tiers(layers=1, experts=6, ram=2)
+    assert t2.store.readers == 3
+    t2.store.sync()
+    assert t2.store.readers == 3 and t2.store.reader_probe is None
 
 
 @pytest.mark.parametrize("compress", [True, False], ids=["compressed", "raw"])

@@ -1,28 +1,49 @@
-// Host side of the SSD tier: a server thread that answers the GPU's read
-// requests from the pinned request ring, with a pool of reader threads.
+// Host side of the SSD tier: answers the GPU's read requests from the pinned
+// request ring.
 //
-// Protocol (store.py:25-30, 83-251, gather.py:197-277):
+// Protocol (layout and rules are the reference's, store.py:25-30, 83-251,
+// gather.py:197-277):
 //   req  = [re-publishes, give-ups] + `ring` slots of
 //          [seq, layer, expert[block], row[block]]        (int64, pinned)
-//   done = the last seq served                            (int64, pinned)
-// The GPU writes a slot, then publishes its seq with a release store. The
-// server serves requests strictly in seq order: it watches the slot of
-// last+1, reads every listed expert (one record = all names' pitches, back to
-// back, at (layer*E + expert)*record_bytes of the paging file) into RAM-tier
-// row `row` with preadv, and release-stores done = seq. A seq that jumps past
-// last+1 counts the skipped requests as missed. While idle, the server
-// re-stores done when the GPU's re-publish counter moves, or every second, so
-// a done that did not reach a waiting GPU is sent again. A read failure
-// records the first error and still releases the GPU.
+//   done = the last seq answered                          (int64, pinned)
+// The GPU fills a slot and publishes its seq with a release store. Requests
+// are answered in seq order: done = seq is release-stored once every listed
+// record of that request (all names' pitches, back to back at
+// (layer*E + expert)*record_bytes of the paging file) is in RAM-tier row
+// `row`, and every earlier request is answered; a failed read still answers.
+// A seq past the next expected one counts the skipped requests as missed.
+// done is stored again when the GPU's re-publish counter moves and once per
+// idle second. The first failure is kept for ssd_error.
 //
-// Exported with the reference's C ABI (store.py:253-308) so the Python side
-// binds it the same way.
+// Structure:
+//   * A watcher thread polls the slot of the next expected seq. It copies a
+//     published request out of the slot at once, checks every entry, and
+//     appends one read task per record to a queue shared by the readers.
+//     It goes straight back to polling, so a request published while an
+//     earlier one is still being read (prefill chunks are published one
+//     ahead) starts at once.
+//   * Reader threads take tasks from the front of the queue. A record is
+//     read whole, in one preadv: the paging file's disk serves a record in
+//     about the time it serves a third of one, so reads are never split.
+//     The read goes straight into the record's pinned rows with O_DIRECT;
+//     where the pinned memory cannot be an O_DIRECT target (preadv fails
+//     with EFAULT, seen with the GPU driver's pinned allocations) it goes
+//     into the reader's aligned bounce buffer instead, and the copy into the
+//     rows is cut into chunks that are put at the front of the queue, so
+//     idle readers copy beside the one that read (non-temporal stores).
+//   * Each request counts its records down. The reader that finishes a
+//     request's last record marks it, then answers every marked request at
+//     the head of the in-flight list in seq order.
+//   * Idle readers sleep on a condition variable, and the watcher yields
+//     the CPU between polls instead of spinning on pause instructions: on a
+//     virtual machine host, pause loops exit to the hypervisor, and a
+//     watcher that spun on them served single-record requests in about
+//     twice the time of one that yields (0.78 against 0.43 ms, measured).
+//   * Time is kept per phase (queue, read, copy), and the time with any
+//     request in flight, for xp_ssd_phase_stats.
 //
-// Reads go straight into the pinned rows when the kernel accepts them as an
-// O_DIRECT target. Memory from the GPU driver's pinned allocator may not be
-// (preadv fails with EFAULT); then every thread reads into its own aligned
-// bounce buffer with O_DIRECT and copies the record into the rows, which
-// still keeps the page cache from holding a second copy.
+// Exported with the reference's C ABI (store.py:253-308).
+#include <immintrin.h>
 #include <sched.h>
 #include <sys/uio.h>
 #include <unistd.h>
@@ -34,8 +55,9 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
-#include <cstring>
 #include <cstdlib>
+#include <cstring>
+#include <deque>
 #include <memory>
 #include <mutex>
 #include <new>
@@ -45,7 +67,10 @@
 namespace {
 
 constexpr int kMaxNames = 4;
-constexpr int kHead = 2;  // [re-publishes, give-ups]
+constexpr int kHead = 2;                  // [re-publishes, give-ups]
+constexpr long kAlign = 4096;             // O_DIRECT alignment of offsets, lengths and buffers
+constexpr long kCopyChunk = 1L << 20;     // longest run of a bounce copy one thread takes
+constexpr int kMaxInFlight = 64;          // requests picked up and not yet answered
 
 inline void cpu_relax() {
 #if defined(__x86_64__) || defined(__i386__)
@@ -53,14 +78,68 @@ inline void cpu_relax() {
 #endif
 }
 
-inline double mono_seconds() {
+inline int64_t now_ns() {
   using namespace std::chrono;
-  return duration<double>(steady_clock::now().time_since_epoch()).count();
+  return duration_cast<nanoseconds>(steady_clock::now().time_since_epoch()).count();
+}
+
+// Copy n bytes (a multiple of 128, both pointers 32-byte aligned) with
+// non-temporal stores: the destination is read next by the GPU over the host
+// link, so it is not worth a place in the CPU's caches, and streaming stores
+// skip the read-for-ownership of each destination line.
+__attribute__((target("avx2"))) void stream_copy_avx2(uint8_t* dst, const uint8_t* src, size_t n) {
+  for (size_t i = 0; i < n; i += 128) {
+    const __m256i a = _mm256_load_si256(reinterpret_cast<const __m256i*>(src + i));
+    const __m256i b = _mm256_load_si256(reinterpret_cast<const __m256i*>(src + i + 32));
+    const __m256i c = _mm256_load_si256(reinterpret_cast<const __m256i*>(src + i + 64));
+    const __m256i d = _mm256_load_si256(reinterpret_cast<const __m256i*>(src + i + 96));
+    _mm256_stream_si256(reinterpret_cast<__m256i*>(dst + i), a);
+    _mm256_stream_si256(reinterpret_cast<__m256i*>(dst + i + 32), b);
+    _mm256_stream_si256(reinterpret_cast<__m256i*>(dst + i + 64), c);
+    _mm256_stream_si256(reinterpret_cast<__m256i*>(dst + i + 96), d);
+  }
+  _mm_sfence();  // the streaming stores land before the release that answers the request
+}
+
+void copy_out(uint8_t* dst, const uint8_t* src, size_t n) {
+  static const bool avx2 = __builtin_cpu_supports("avx2");
+  if (avx2 && n % 128 == 0 && (reinterpret_cast<uintptr_t>(dst) & 31) == 0 &&
+      (reinterpret_cast<uintptr_t>(src) & 31) == 0)
+    stream_copy_avx2(dst, src, n);
+  else
+    std::memcpy(dst, src, n);
 }
 
 }  // namespace
 
 struct ssd_t {
+  // One request between pickup and answer.
+  struct Request {
+    int64_t seq = 0;
+    int64_t picked_ns = 0;
+    long records = 0;
+    std::atomic<long> left{0};  // records not yet in their rows, plus the watcher's hold
+    std::atomic<bool> finished{false};
+  };
+
+  // The copy chunks of one bounced record still to be done.
+  struct CopyGroup {
+    std::atomic<long> left{0};
+  };
+
+  // A queued task: the read of one record (group == nullptr), or one chunk
+  // of the copy of a bounced record into its row.
+  struct Task {
+    Request* req = nullptr;
+    long layer = 0, expert = 0, row = 0;
+    int64_t queued_ns = 0;
+    CopyGroup* group = nullptr;
+    uint8_t* dst = nullptr;
+    const uint8_t* src = nullptr;
+    long bytes = 0;
+  };
+
+  // ---- configuration ----
   int fd = -1;
   int64_t* req = nullptr;
   int64_t* done = nullptr;
@@ -69,259 +148,353 @@ struct ssd_t {
   int names = 0;
   uint8_t* pinned[kMaxNames] = {};
   long pitch[kMaxNames] = {};
+  int nreaders = 1;
 
-  std::atomic<long> fetches{0}, reads{0}, missed{0};
-  std::atomic<long long> io_ns{0};
-  std::atomic<int> failed{0};
+  // ---- state ----
+  std::atomic<bool> stopping{false};
+  std::atomic<long long> delay_ns{0};
+  std::atomic<bool> direct{true};  // O_DIRECT straight into the pinned rows works
+
+  std::mutex queue_mu;  // queue, sleepers
+  std::condition_variable queue_cv;
+  std::deque<Task> queue;
+  int sleepers = 0;
+
+  std::mutex answer_mu;  // in_flight, free_requests, answered, busy time and every store to `done`
+  std::condition_variable slot_cv;
+  std::deque<Request*> in_flight;
+  std::vector<std::unique_ptr<Request>> pool;
+  std::vector<Request*> free_requests;
+  int64_t answered = 0;
+  int64_t busy_ns = 0, busy_since = 0;
+
+  // ---- statistics ----
+  std::atomic<long> fetches{0}, reads{0}, missed{0}, preads{0};
+  std::atomic<long long> io_ns{0}, queue_ns{0}, read_ns{0}, copy_ns{0};
+  std::atomic<bool> failed{false};
   std::atomic<bool> failing{false};
   char err[512] = {0};
-  std::atomic<long long> delay_ns{0};
-  std::atomic<bool> direct{true};  // preadv straight into the pinned rows works
 
-  // Job board of the request being served.
-  std::mutex mu;
-  std::condition_variable cv;
-  long generation = 0;
-  bool stop = false;
-  std::atomic<bool> stop_flag{false};
-  long layer = 0, njobs = 0, next_job = 0, finished = 0;
-  std::vector<long> job_expert, job_row;
-  std::vector<std::thread> workers;
-  std::thread server;
+  std::thread watcher;
+  std::vector<std::thread> readers;
 
   void fail(const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-  long read_iov(const iovec* iov, int n, off_t off, int* err);
-  void read_job(long layer_, long e, long row);
-  void drain_jobs();
-  void worker_loop();
-  void server_loop();
+  Request* take_request();
+  void finish_record(Request* r);
+  void answer_ready();
+  bool enqueue(int64_t seq, const int64_t* slot, int64_t picked_ns);
+  void watch();
+  void read_loop();
+  bool next_task(Task* out);
+  bool take_copy(Task* out);
+  void run_copy(const Task& t);
+  long preadv_full(iovec* iov, int n, off_t off, int* error);
+  void serve(const Task& t, uint8_t** bounce);
 };
 
 void ssd_t::fail(const char* fmt, ...) {
   bool expected = false;
-  if (!failing.compare_exchange_strong(expected, true)) return;  // keep the first failure only
+  if (!failing.compare_exchange_strong(expected, true)) return;  // the first failure is kept
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(err, sizeof err, fmt, ap);
   va_end(ap);
-  failed.store(1, std::memory_order_release);
+  failed.store(true, std::memory_order_release);
 }
 
-// preadv until the iovecs are full, EOF or an error; returns the bytes read
-// and the errno of a failure in *err.
-long ssd_t::read_iov(const iovec* iov, int n, off_t off, int* err) {
-  long got = 0, total = 0;
-  for (int i = 0; i < n; ++i) total += static_cast<long>(iov[i].iov_len);
-  *err = 0;
-  while (got < total) {
-    iovec part[kMaxNames];
-    int np = 0;
-    long skip = got;
-    for (int i = 0; i < n; ++i) {
-      if (skip >= static_cast<long>(iov[i].iov_len)) {
-        skip -= static_cast<long>(iov[i].iov_len);
-        continue;
-      }
-      part[np].iov_base = static_cast<uint8_t*>(iov[i].iov_base) + skip;
-      part[np].iov_len = iov[i].iov_len - static_cast<size_t>(skip);
-      skip = 0;
-      ++np;
+// A free request record; waits while kMaxInFlight requests are unanswered.
+ssd_t::Request* ssd_t::take_request() {
+  std::unique_lock<std::mutex> lock(answer_mu);
+  slot_cv.wait(lock, [&] { return !free_requests.empty() || stopping.load(); });
+  if (free_requests.empty()) return nullptr;
+  Request* r = free_requests.back();
+  free_requests.pop_back();
+  return r;
+}
+
+void ssd_t::finish_record(Request* r) {
+  if (r->left.fetch_sub(1, std::memory_order_acq_rel) != 1) return;
+  r->finished.store(true, std::memory_order_release);
+  answer_ready();
+}
+
+// Answer, in seq order, every finished request at the head of the list.
+void ssd_t::answer_ready() {
+  std::lock_guard<std::mutex> lock(answer_mu);
+  bool freed = false;
+  while (!in_flight.empty() && in_flight.front()->finished.load(std::memory_order_acquire)) {
+    Request* r = in_flight.front();
+    in_flight.pop_front();
+    const int64_t t = now_ns();
+    fetches.fetch_add(1, std::memory_order_relaxed);
+    reads.fetch_add(r->records, std::memory_order_relaxed);
+    io_ns.fetch_add(t - r->picked_ns, std::memory_order_relaxed);
+    answered = r->seq;
+    __atomic_store_n(done, answered, __ATOMIC_RELEASE);
+    free_requests.push_back(r);
+    if (in_flight.empty()) busy_ns += t - busy_since;
+    freed = true;
+  }
+  if (freed) slot_cv.notify_one();
+}
+
+// Queue the reads of the request in `slot`. Returns false when stopping.
+bool ssd_t::enqueue(int64_t seq, const int64_t* slot, int64_t picked_ns) {
+  Request* r = take_request();
+  if (!r) return false;
+  const long layer = static_cast<long>(__atomic_load_n(&slot[1], __ATOMIC_RELAXED));
+  std::vector<Task> tasks;
+  long records = 0;
+  for (long j = 0; j < block; ++j) {
+    const long e = static_cast<long>(__atomic_load_n(&slot[2 + j], __ATOMIC_RELAXED));
+    if (e < 0) continue;  // unused entry
+    const long row = static_cast<long>(__atomic_load_n(&slot[2 + block + j], __ATOMIC_RELAXED));
+    ++records;
+    if (layer < 0 || layer >= L || e >= E) {
+      fail("expert %ld of layer %ld is out of range (%ld layers, %ld experts)", e, layer, L, E);
+      continue;
     }
-    const ssize_t r = preadv(fd, part, np, off + got);
+    if (row < 0 || row >= rows) {
+      fail("row %ld for expert %ld of layer %ld is outside the RAM tier of %ld rows", row, e, layer, rows);
+      continue;
+    }
+    Task t;
+    t.req = r;
+    t.layer = layer;
+    t.expert = e;
+    t.row = row;
+    tasks.push_back(t);
+  }
+  r->seq = seq;
+  r->picked_ns = picked_ns;
+  r->records = records;
+  r->finished.store(false, std::memory_order_relaxed);
+  r->left.store(static_cast<long>(tasks.size()) + 1, std::memory_order_relaxed);  // +1: the watcher's hold
+  {
+    std::lock_guard<std::mutex> lock(answer_mu);
+    if (in_flight.empty()) busy_since = picked_ns;
+    in_flight.push_back(r);
+  }
+  if (!tasks.empty()) {
+    const int64_t t = now_ns();
+    bool wake;
+    {
+      std::lock_guard<std::mutex> lock(queue_mu);
+      for (Task& task : tasks) {
+        task.queued_ns = t;
+        queue.push_back(task);
+      }
+      wake = sleepers > 0;
+    }
+    if (wake) queue_cv.notify_all();
+  }
+  finish_record(r);  // drop the watcher's hold: a request with no readable record is answered here
+  return true;
+}
+
+void ssd_t::watch() {
+  int64_t expected = 1;  // the seq the watcher waits for next
+  int64_t republished = __atomic_load_n(&req[0], __ATOMIC_ACQUIRE);
+  int64_t idle_since = now_ns();
+  unsigned polls = 0;
+  while (!stopping.load(std::memory_order_acquire)) {
+    const int64_t* slot = req + kHead + (expected % ring) * slot_words;
+    const int64_t seq = __atomic_load_n(&slot[0], __ATOMIC_ACQUIRE);
+    if (seq >= expected) {
+      const int64_t picked = now_ns();
+      if (seq > expected) missed.fetch_add(static_cast<long>(seq - expected), std::memory_order_relaxed);
+      // Test hook: hold the request for delay_ns before reading it.
+      for (;;) {
+        const long long d = delay_ns.load(std::memory_order_acquire);
+        if (d <= 0 || now_ns() - picked >= d || stopping.load(std::memory_order_acquire)) break;
+        usleep(1000);
+      }
+      if (stopping.load(std::memory_order_acquire) || !enqueue(seq, slot, picked)) return;
+      expected = seq + 1;
+      idle_since = now_ns();
+      polls = 0;
+      continue;
+    }
+    const int64_t r = __atomic_load_n(&req[0], __ATOMIC_ACQUIRE);
+    bool resend = r != republished;
+    republished = r;
+    if (++polls >= 4096) {
+      polls = 0;
+      const int64_t now = now_ns();
+      if (now - idle_since > 1000000000LL) {
+        idle_since = now;
+        resend = true;
+      }
+    }
+    sched_yield();
+    if (resend) {
+      std::lock_guard<std::mutex> lock(answer_mu);
+      __atomic_store_n(done, answered, __ATOMIC_RELEASE);
+    }
+  }
+}
+
+bool ssd_t::next_task(Task* out) {
+  std::unique_lock<std::mutex> lock(queue_mu);
+  while (queue.empty() && !stopping.load(std::memory_order_acquire)) {
+    ++sleepers;
+    queue_cv.wait(lock);
+    --sleepers;
+  }
+  if (stopping.load(std::memory_order_acquire)) return false;
+  *out = queue.front();
+  queue.pop_front();
+  return true;
+}
+
+// A copy chunk from the front of the queue, if one is there.
+bool ssd_t::take_copy(Task* out) {
+  std::lock_guard<std::mutex> lock(queue_mu);
+  if (queue.empty() || queue.front().group == nullptr) return false;
+  *out = queue.front();
+  queue.pop_front();
+  return true;
+}
+
+void ssd_t::run_copy(const Task& t) {
+  const int64_t t0 = now_ns();
+  copy_out(t.dst, t.src, static_cast<size_t>(t.bytes));
+  copy_ns.fetch_add(now_ns() - t0, std::memory_order_relaxed);
+  t.group->left.fetch_sub(1, std::memory_order_acq_rel);
+}
+
+// preadv until the iovecs are full, end of file or an error; returns the
+// bytes read. The iovecs are advanced past what was read.
+long ssd_t::preadv_full(iovec* iov, int n, off_t off, int* error) {
+  long got = 0;
+  *error = 0;
+  int first = 0;
+  while (first < n) {
+    const ssize_t r = preadv(fd, iov + first, n - first, off + got);
     if (r < 0) {
       if (errno == EINTR) continue;
-      *err = errno;
-      return got;
+      *error = errno;
+      break;
     }
     if (r == 0) break;
     got += r;
+    size_t left = static_cast<size_t>(r);
+    while (first < n && left >= iov[first].iov_len) left -= iov[first++].iov_len;
+    if (first < n && left) {
+      iov[first].iov_base = static_cast<uint8_t*>(iov[first].iov_base) + left;
+      iov[first].iov_len -= left;
+    }
   }
   return got;
 }
 
-namespace {
-struct Bounce {
-  void* p = nullptr;
-  size_t n = 0;
-  ~Bounce() { std::free(p); }
-  uint8_t* get(size_t bytes) {
-    if (n < bytes) {
-      std::free(p);
-      p = nullptr;
-      n = 0;
-      if (posix_memalign(&p, 4096, bytes) != 0) return nullptr;
-      n = bytes;
-    }
-    return static_cast<uint8_t*>(p);
-  }
-};
-thread_local Bounce t_bounce;
-}  // namespace
-
-void ssd_t::read_job(long layer_, long e, long row) {
-  if (layer_ < 0 || layer_ >= L || e < 0 || e >= E) {
-    fail("expert %ld of layer %ld is out of range", e, layer_);
-    return;
-  }
-  if (row < 0 || row >= rows) {
-    fail("row %ld for expert %ld of layer %ld is outside the RAM tier of %ld rows", row, e, layer_, rows);
-    return;
-  }
-  const off_t off = static_cast<off_t>(layer_ * E + e) * record_bytes;
-  int err = 0;
-  long got;
-  if (direct.load(std::memory_order_relaxed)) {
+void ssd_t::serve(const Task& t, uint8_t** bounce) {
+  const int64_t t0 = now_ns();
+  queue_ns.fetch_add(t0 - t.queued_ns, std::memory_order_relaxed);
+  const off_t off = static_cast<off_t>(t.layer * E + t.expert) * record_bytes;
+  int error = 0;
+  long got = 0;
+  bool via_bounce = !direct.load(std::memory_order_relaxed);
+  if (!via_bounce) {
     iovec iov[kMaxNames];
-    for (int i = 0; i < names; ++i) {
-      iov[i].iov_base = pinned[i] + row * pitch[i];
-      iov[i].iov_len = static_cast<size_t>(pitch[i]);
+    for (int n = 0; n < names; ++n) iov[n] = iovec{pinned[n] + t.row * pitch[n], static_cast<size_t>(pitch[n])};
+    got = preadv_full(iov, names, off, &error);
+    if (error == EFAULT) {
+      direct.store(false, std::memory_order_relaxed);  // the rows cannot be an O_DIRECT target
+      via_bounce = true;
     }
-    got = read_iov(iov, names, off, &err);
-    if (err != EFAULT) {
-      if (err) fail("preadv of expert %ld of layer %ld failed: %s", e, layer_, strerror(err));
-      else if (got != record_bytes)
-        fail("short read: %ld of %ld B for expert %ld of layer %ld", got, record_bytes, e, layer_);
-      return;
+  }
+  if (via_bounce) {
+    if (!*bounce) {
+      void* mem = nullptr;
+      if (posix_memalign(&mem, kAlign, static_cast<size_t>(record_bytes)) != 0) {
+        fail("cannot allocate a %ld B read buffer", record_bytes);
+        return;
+      }
+      *bounce = static_cast<uint8_t*>(mem);
     }
-    direct.store(false, std::memory_order_relaxed);  // the rows cannot be an O_DIRECT target
+    iovec one{*bounce, static_cast<size_t>(record_bytes)};
+    got = preadv_full(&one, 1, off, &error);
   }
-  uint8_t* b = t_bounce.get(static_cast<size_t>(record_bytes));
-  if (!b) {
-    fail("cannot allocate a %ld B read buffer", record_bytes);
-    return;
-  }
-  iovec one{b, static_cast<size_t>(record_bytes)};
-  got = read_iov(&one, 1, off, &err);
-  if (err) {
-    fail("preadv of expert %ld of layer %ld failed: %s", e, layer_, strerror(err));
+  const int64_t t1 = now_ns();
+  read_ns.fetch_add(t1 - t0, std::memory_order_relaxed);
+  preads.fetch_add(1, std::memory_order_relaxed);
+  if (error) {
+    fail("reading expert %ld of layer %ld from the paging file failed: %s", t.expert, t.layer, strerror(error));
     return;
   }
   if (got != record_bytes) {
-    fail("short read: %ld of %ld B for expert %ld of layer %ld", got, record_bytes, e, layer_);
+    fail("short read: %ld of %ld B of expert %ld of layer %ld", got, record_bytes, t.expert, t.layer);
     return;
   }
+  if (!via_bounce) return;
+
+  // Copy out of the bounce buffer: chunk 0 here, the rest at the front of
+  // the queue for idle readers (and for this one, while it waits).
+  std::vector<Task> chunks;
+  CopyGroup group;
   long pos = 0;
-  for (int i = 0; i < names; ++i) {
-    std::memcpy(pinned[i] + row * pitch[i], b + pos, static_cast<size_t>(pitch[i]));
-    pos += pitch[i];
+  for (int n = 0; n < names; ++n) {
+    uint8_t* dst = pinned[n] + t.row * pitch[n];
+    for (long at = 0; at < pitch[n]; at += kCopyChunk) {
+      Task c;
+      c.group = &group;
+      c.dst = dst + at;
+      c.src = *bounce + pos + at;
+      c.bytes = pitch[n] - at < kCopyChunk ? pitch[n] - at : kCopyChunk;
+      chunks.push_back(c);
+    }
+    pos += pitch[n];
+  }
+  group.left.store(static_cast<long>(chunks.size()), std::memory_order_relaxed);
+  if (chunks.size() > 1) {
+    bool wake;
+    {
+      std::lock_guard<std::mutex> lock(queue_mu);
+      for (size_t i = chunks.size() - 1; i >= 1; --i) queue.push_front(chunks[i]);
+      wake = sleepers > 0;
+    }
+    if (wake) queue_cv.notify_all();
+  }
+  run_copy(chunks[0]);
+  Task other;
+  while (group.left.load(std::memory_order_acquire) > 0) {
+    if (take_copy(&other))
+      run_copy(other);  // ours, or another record's
+    else
+      cpu_relax();  // the rest of ours are being copied by other readers
   }
 }
 
-// Take jobs of the current request until none is left (server and workers).
-void ssd_t::drain_jobs() {
-  for (;;) {
-    long j, e, row, lay;
-    {
-      std::lock_guard<std::mutex> lock(mu);
-      if (next_job >= njobs) return;
-      j = next_job++;
-      e = job_expert[static_cast<size_t>(j)];
-      row = job_row[static_cast<size_t>(j)];
-      lay = layer;
+void ssd_t::read_loop() {
+  uint8_t* bounce = nullptr;
+  Task t;
+  while (next_task(&t)) {
+    if (t.group) {
+      run_copy(t);
+      continue;
     }
-    read_job(lay, e, row);
-    std::lock_guard<std::mutex> lock(mu);
-    ++finished;
+    serve(t, &bounce);
+    finish_record(t.req);
   }
-}
-
-void ssd_t::worker_loop() {
-  long seen = 0;
-  for (;;) {
-    {
-      std::unique_lock<std::mutex> lock(mu);
-      cv.wait(lock, [&] { return stop || generation != seen; });
-      if (stop) return;
-      seen = generation;
-    }
-    drain_jobs();
-  }
-}
-
-void ssd_t::server_loop() {
-  int64_t last = 0;
-  int64_t republished = __atomic_load_n(&req[0], __ATOMIC_ACQUIRE);
-  for (;;) {
-    int64_t* slot = req + kHead + ((last + 1) % ring) * slot_words;
-    int64_t seq;
-    long spins = 0;
-    double idle_since = mono_seconds();
-    while ((seq = __atomic_load_n(&slot[0], __ATOMIC_ACQUIRE)) <= last) {
-      if (stop_flag.load(std::memory_order_acquire)) return;
-      const int64_t r = __atomic_load_n(&req[0], __ATOMIC_ACQUIRE);
-      if (r != republished) {
-        republished = r;
-        __atomic_store_n(done, last, __ATOMIC_RELEASE);
-      }
-      if (++spins >= 4096) {
-        spins = 0;
-        const double now = mono_seconds();
-        if (now - idle_since > 1.0) {
-          idle_since = now;
-          __atomic_store_n(done, last, __ATOMIC_RELEASE);
-        }
-        sched_yield();
-      } else {
-        cpu_relax();
-      }
-    }
-    const double t0 = mono_seconds();
-    if (seq > last + 1) missed.fetch_add(static_cast<long>(seq - last - 1));
-    for (;;) {  // test hook: hold the request for delay_ns
-      const long long d = delay_ns.load(std::memory_order_acquire);
-      if (d <= 0 || (mono_seconds() - t0) * 1e9 >= static_cast<double>(d)) break;
-      if (stop_flag.load(std::memory_order_acquire)) return;
-      usleep(1000);
-    }
-    long n = 0;
-    {
-      std::lock_guard<std::mutex> lock(mu);
-      layer = static_cast<long>(__atomic_load_n(&slot[1], __ATOMIC_RELAXED));
-      for (long j = 0; j < block; ++j) {
-        const int64_t e = __atomic_load_n(&slot[2 + j], __ATOMIC_RELAXED);
-        if (e < 0) continue;
-        job_expert[static_cast<size_t>(n)] = static_cast<long>(e);
-        job_row[static_cast<size_t>(n)] = static_cast<long>(__atomic_load_n(&slot[2 + block + j], __ATOMIC_RELAXED));
-        ++n;
-      }
-      njobs = n;
-      next_job = 0;
-      finished = 0;
-      if (n > 1) {  // a single read is done here without waking the pool
-        ++generation;
-        cv.notify_all();
-      }
-    }
-    drain_jobs();
-    for (spins = 0;;) {
-      {
-        std::lock_guard<std::mutex> lock(mu);
-        if (finished >= n) break;
-      }
-      if (++spins >= 1024) {
-        spins = 0;
-        sched_yield();
-      } else {
-        cpu_relax();
-      }
-    }
-    fetches.fetch_add(1);
-    reads.fetch_add(n);
-    io_ns.fetch_add(static_cast<long long>((mono_seconds() - t0) * 1e9));
-    // Re-publishes made while this request was being read are not lost
-    // handoffs.
-    republished = __atomic_load_n(&req[0], __ATOMIC_ACQUIRE);
-    __atomic_store_n(done, seq, __ATOMIC_RELEASE);  // also after a failed read
-    last = seq;
-  }
+  std::free(bounce);
 }
 
 extern "C" {
 
+// `nworkers` + 1 reader threads serve the records (the reference's server
+// reads with itself and `nworkers` workers).
 ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L, long E, long rows, long record_bytes,
                  int names, void** pinned, long* pitch, int nworkers) {
-  if (names < 1 || names > kMaxNames || !req || !done || ring < 1 || block < 1 || nworkers < 0 || !pinned || !pitch)
+  if (names < 1 || names > kMaxNames || !req || !done || ring < 1 || block < 1 || nworkers < 0 || nworkers > 255 ||
+      !pinned || !pitch || record_bytes <= 0)
     return nullptr;
+  long sum = 0;
+  for (int i = 0; i < names; ++i) {
+    if (!pinned[i] || pitch[i] <= 0) return nullptr;
+    sum += pitch[i];
+  }
+  if (sum != record_bytes) return nullptr;
   ssd_t* s = new (std::nothrow) ssd_t;
   if (!s) return nullptr;
   s->fd = fd;
@@ -335,23 +508,25 @@ ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L, l
   s->rows = rows;
   s->record_bytes = record_bytes;
   s->names = names;
+  s->nreaders = nworkers + 1;
   for (int i = 0; i < names; ++i) {
     s->pinned[i] = static_cast<uint8_t*>(pinned[i]);
     s->pitch[i] = pitch[i];
   }
   try {
-    s->job_expert.assign(static_cast<size_t>(block), 0);
-    s->job_row.assign(static_cast<size_t>(block), 0);
-    for (int i = 0; i < nworkers; ++i) s->workers.emplace_back([s] { s->worker_loop(); });
-    s->server = std::thread([s] { s->server_loop(); });
+    for (int i = 0; i < kMaxInFlight; ++i) {
+      s->pool.emplace_back(new ssd_t::Request);
+      s->free_requests.push_back(s->pool.back().get());
+    }
+    for (int i = 0; i < s->nreaders; ++i) s->readers.emplace_back([s] { s->read_loop(); });
+    s->watcher = std::thread([s] { s->watch(); });
   } catch (...) {
     {
-      std::lock_guard<std::mutex> lock(s->mu);
-      s->stop = true;
+      std::lock_guard<std::mutex> q(s->queue_mu);
+      s->stopping.store(true);
     }
-    s->stop_flag.store(true);
-    s->cv.notify_all();
-    for (auto& t : s->workers)
+    s->queue_cv.notify_all();
+    for (auto& t : s->readers)
       if (t.joinable()) t.join();
     delete s;
     return nullptr;
@@ -362,13 +537,14 @@ ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L, l
 void ssd_stop(ssd_t* s) {
   if (!s) return;
   {
-    std::lock_guard<std::mutex> lock(s->mu);
-    s->stop = true;
+    std::lock_guard<std::mutex> a(s->answer_mu);
+    std::lock_guard<std::mutex> q(s->queue_mu);
+    s->stopping.store(true, std::memory_order_release);
   }
-  s->stop_flag.store(true, std::memory_order_release);
-  s->cv.notify_all();
-  if (s->server.joinable()) s->server.join();
-  for (auto& t : s->workers)
+  s->queue_cv.notify_all();
+  s->slot_cv.notify_all();
+  if (s->watcher.joinable()) s->watcher.join();
+  for (auto& t : s->readers)
     if (t.joinable()) t.join();
   delete s;
 }
@@ -384,6 +560,22 @@ const char* ssd_error(ssd_t* s) { return s->failed.load(std::memory_order_acquir
 
 void ssd_test_delay(ssd_t* s, double seconds) {
   s->delay_ns.store(static_cast<long long>(seconds * 1e9), std::memory_order_release);
+}
+
+void xp_ssd_test_bounce(ssd_t* s) { s->direct.store(false, std::memory_order_relaxed); }
+
+void xp_ssd_phase_stats(ssd_t* s, double* busy_s, double* queue_s, double* read_s, double* copy_s, long* preads,
+                        int* readers, int* bounce) {
+  {
+    std::lock_guard<std::mutex> lock(s->answer_mu);
+    *busy_s = static_cast<double>(s->busy_ns + (s->in_flight.empty() ? 0 : now_ns() - s->busy_since)) * 1e-9;
+  }
+  *queue_s = static_cast<double>(s->queue_ns.load()) * 1e-9;
+  *read_s = static_cast<double>(s->read_ns.load()) * 1e-9;
+  *copy_s = static_cast<double>(s->copy_ns.load()) * 1e-9;
+  *preads = s->preads.load();
+  *readers = s->nreaders;
+  *bounce = s->direct.load() ? 0 : 1;
 }
 
 }  // extern "C"

@@ -117,6 +117,8 @@ _SIGNATURES = {
     "ssd_stats": (None, [_P, _P, _P, _P, _P]),
     "ssd_error": (ctypes.c_char_p, [_P]),
     "ssd_test_delay": (None, [_P, ctypes.c_double]),
+    "xp_ssd_phase_stats": (None, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "xp_ssd_test_bounce": (None, [_P]),
     "xp_quant_tokens": (_I, [_P, _L, _L, _P, _P, _P]),
     "xp_moe_max_tiles": (_L, [_L, _L]),
     "xp_moe_route": (_I, [_P, _I, _L, _L, _P, _L, _L, _P, _P, _P, _P]),

@@ -34,16 +34,22 @@ logger = logging.getLogger(f"vllm.{__name__}")
 
 # O_DIRECT alignment of rows, records and the pinned base (store.py:51-53).
 _ALIGN = 4096
-# Concurrent reads per request: the server thread and 7 workers
-# (store.py:59-64). VLLM_EXPERT_PAGER_READ_WORKERS overrides it (1..64) for
-# disks that want a deeper queue; it is not a reference setting.
-_READ_WORKERS = 8
+# Reader threads of the SSD server. The reference fixes 8 concurrent reads
+# (store.py:59-64), sized by hand for its NVMe disk. Here the server starts
+# with _READERS_UNSIZED and, once the paging file is complete (sync), probes
+# the disk with record-sized O_DIRECT reads of the file from each of
+# _READER_DEPTHS threads and restarts with the depth that read fastest: disks
+# differ in how much a deeper queue helps, and on some every extra read in
+# flight only slows the others down. VLLM_EXPERT_PAGER_READ_WORKERS (1..64),
+# not a reference setting, fixes the count and skips the probe.
+_READERS_UNSIZED = 2
+_READER_DEPTHS = (1, 2, 4, 8)
 
 
-def _read_workers() -> int:
+def _read_workers_setting() -> int | None:
     v = os.environ.get("VLLM_EXPERT_PAGER_READ_WORKERS")
     if not v:
-        return _READ_WORKERS
+        return None
     n = int(v)
     if not 1 <= n <= 64:
         raise ValueError(f"VLLM_EXPERT_PAGER_READ_WORKERS must be in [1, 64], got {n}")
@@ -188,6 +194,8 @@ class Store:
         self._ring = nat.XpRing(self._req_buf.device_ptr, self._done_buf.device_ptr, self.seq.data_ptr(),
                                 self.block, self.ring)
 
+        self.readers = 0  # SSD server reader threads (set when it starts)
+        self.reader_probe: dict | None = None  # disk GB/s by probe depth, from size_readers()
         self.path = path if R < E else None
         self.fd_w = self.fd_r = None
         self.synced: float | None = None  # seconds of the last sync()
@@ -208,7 +216,8 @@ class Store:
     def ring_struct(self) -> nat.XpRing:
         return self._ring
 
-    def _start_server(self) -> None:
+    def _start_server(self, readers: int | None = None) -> None:
+        self.readers = readers or _read_workers_setting() or _READERS_UNSIZED
         n = len(self.names)
         pinned = (ctypes.c_void_p * n)(*(self.pinned[k].data_ptr() for k in self.names))
         pitch = (ctypes.c_long * n)(*(self.pitch[k] for k in self.names))
@@ -216,7 +225,7 @@ class Store:
         self._handle = self._so.ssd_start(
             self.fd_r, ctypes.c_void_p(self.req.data_ptr()), ctypes.c_void_p(self.done.data_ptr()), self.ring,
             self.block, self.num_layers, self.num_experts, self.rows, self.record_bytes, n, pinned, pitch,
-            _read_workers() - 1,
+            self.readers - 1,
         )
         if not self._handle:
             raise RuntimeError("vllm-expert-pager: cannot start the SSD server")
@@ -269,11 +278,68 @@ class Store:
         os.fdatasync(self.fd_w)
         os.posix_fadvise(self.fd_w, 0, 0, os.POSIX_FADV_DONTNEED)
         self.synced = time.perf_counter() - t0
+        if _read_workers_setting() is None:
+            self.size_readers()
         return self.synced
+
+    def size_readers(self, seconds: float = 0.05) -> dict | None:
+        """Probe the paging file with record-sized O_DIRECT reads of random
+        records from 1, 2, 4 and 8 threads (two passes in opposite orders,
+        each about ``seconds`` long at 3 GB/s, the better kept), and restart
+        the server with the smallest depth within 5% of the fastest. Only
+        while no request has been made: a new server starts from seq 1.
+        Returns the rates (GB/s by depth), or None when nothing was done."""
+        if not self._handle or self.fd_r is None:
+            return None
+        slots = self.req[2:].view(self.ring, self.slot_words)
+        if int(self.done[0]) != 0 or bool((slots[:, 0] != 0).any()):
+            logger.info("vllm-expert-pager: SSD readers not re-sized: requests were already made")
+            return None
+        records = self.num_layers * self.num_experts
+        rng = np.random.default_rng(records)
+        rates: dict[int, float] = {}
+        for order in (_READER_DEPTHS, _READER_DEPTHS[::-1]):
+            for depth in order:
+                count = max(4 * depth, int(3e9 * seconds / self.record_bytes))
+                idx = rng.integers(0, records, size=count)
+                offs = (ctypes.c_int64 * count)(*(int(i) * self.record_bytes for i in idx))
+                sec = ctypes.c_double()
+                if self._so.xp_ssd_read_probe(self.fd_r, self.record_bytes, offs, count, depth, 0, ctypes.byref(sec)):
+                    logger.warning("vllm-expert-pager: SSD reader probe failed: %s",
+                                   self._so.xp_last_error().decode(errors="replace"))
+                    return None
+                rates[depth] = max(rates.get(depth, 0.0), count * self.record_bytes / sec.value / 1e9)
+        best = max(rates.values())
+        readers = min(d for d, r in rates.items() if r >= 0.95 * best)
+        self.reader_probe = {str(d): round(r, 3) for d, r in sorted(rates.items())}
+        if readers != self.readers:
+            self._so.ssd_stop(ctypes.c_void_p(self._handle))
+            self._handle = None
+            self._start_server(readers)
+        logger.info("vllm-expert-pager: SSD server reads with %d thread(s); disk GB/s by depth %s", self.readers,
+                    self.reader_probe)
+        return self.reader_probe
 
     def stats(self) -> tuple[int, int, float, int]:
         """(requests served, experts read, seconds from request to done, requests missed)."""
         return self._stats()
+
+    def phase_stats(self) -> dict:
+        """The seconds with a request in flight (``busy_s``), and where the
+        server's time went, summed over the records it read: seconds waiting
+        in the readers' queue, in preadv and copying out of bounce buffers;
+        the records read (one preadv each, ``preads``), the reader threads,
+        and whether the rows refused O_DIRECT (``bounce``)."""
+        if not self._handle:
+            return {}
+        b, q, r, c = (ctypes.c_double() for _ in range(4))
+        preads = ctypes.c_long()
+        readers, bounce = ctypes.c_int(), ctypes.c_int()
+        self._so.xp_ssd_phase_stats(ctypes.c_void_p(self._handle), ctypes.byref(b), ctypes.byref(q),
+                                    ctypes.byref(r), ctypes.byref(c), ctypes.byref(preads), ctypes.byref(readers),
+                                    ctypes.byref(bounce))
+        return {"busy_s": b.value, "queue_s": q.value, "read_s": r.value, "copy_s": c.value,
+                "preads": preads.value, "readers": readers.value, "bounce": bool(bounce.value)}
 
     @property
     def fetches(self) -> int:
