@@ -94,6 +94,37 @@ def decode_traffic(rows: int):
     return None
 
 
+# VALU issue model of one MI355X: 256 CUs x 4 SIMDs, one wave64 VALU instruction per SIMD
+# every 4 clocks, 2.4 GHz peak engine clock.
+SIMDS, VALU_CLOCKS, ENGINE_GHZ = 1024, 4, 2.4
+
+
+def decode_valu(rows: int, alg_bytes: int, achieved_gbps: float, n_bytes: list[int], chunk: int = 512):
+    """The decoder's VALU bound: VALU instructions per wave and symbol step (SQ_INSTS_VALU per
+    dispatch / waves / steps, from the committed rocprofv3 --pmc summary of the same launch),
+    the launch time that many instructions take on every SIMD at the peak clock, the
+    algorithmic GB/s that allows, and the measured rate as a fraction of it; None when there
+    is no summary for this row count."""
+    path = os.path.join(ROOT, "profiles", f"decode_pmc_{rows}rows.md")
+    if not os.path.exists(path):
+        return None
+    per_step = None
+    for line in open(path):
+        if line.startswith("| SQ_INSTS_VALU |"):
+            per_step = float(line.split("|")[3])
+    if per_step is None:
+        return None
+    groups = sum(n // (chunk * 32) for n in n_bytes)
+    waves = rows * groups / 2  # two 32-lane groups per wave
+    ms = waves * chunk * per_step * VALU_CLOCKS / (SIMDS * ENGINE_GHZ * 1e9) * 1e3
+    ceiling = alg_bytes / (ms * 1e-3) / 1e9
+    return {"insts_per_wave_step": per_step, "symbols_per_wave_step": 64, "ms_at_peak_issue": round(ms, 4),
+            "ceiling_gbps": round(ceiling, 1), "ceiling_frac_of_hbm": round(ceiling / HBM_PEAK_GBPS, 4),
+            "frac": round(achieved_gbps / ceiling, 4),
+            "model": f"{SIMDS} SIMDs, one wave64 VALU instruction per {VALU_CLOCKS} clocks, {ENGINE_GHZ} GHz",
+            "source": f"profiles/decode_pmc_{rows}rows.md"}
+
+
 def warm_by_time(step, min_ms: float = 200.0, batch: int = 10, tol: float = 0.02, max_s: float = 5.0) -> dict:
     """Launch `step` in batches until at least `min_ms` of launches have run and
     two consecutive batches agree within `tol`, so the timed launches that
@@ -180,6 +211,44 @@ def bench_decode(args, dev, cores):
     sweep[str(count)] = round(gbps, 1)
     sweep_us[str(count)] = round(ms * 1e3, 1)
 
+    # The same rows read straight from pinned RAM (xp_decode_rows_from_ram, the decode step's
+    # path for compressed misses): 1-8 experts per launch, records read over the host link while
+    # they are expanded, scale rows copied alongside; checked against the raw rows.
+    from vllm_expert_pager.gather import DeviceRows
+    from vllm_expert_pager.store import PinnedBuffer
+
+    nr = min(8, count)
+    bufs = [PinnedBuffer(nr * s.shape[1], coherent=False) for s in stg_np]
+    hosts = [b.tensor(torch.uint8, (nr, s.shape[1])) for b, s in zip(bufs, stg_np)]
+    for h, s in zip(hosts, stg_np):
+        h.copy_(torch.from_numpy(s[:nr]))
+    ram = [DeviceRows(h, b.device_ptr) for h, b in zip(hosts, bufs)]
+    src_row = torch.arange(count, dtype=torch.int64, device=dev)
+    scale = [torch.arange(count * 32, dtype=torch.int32, device=dev).view(count, 32) for _ in stg_np]
+    scale_dst = [torch.zeros((count, 32), dtype=torch.int32, device=dev) for _ in stg_np]
+    ram_us = {}
+    for r in (1, 2, 4, 8):
+        if r > nr:
+            continue
+        for d in dst:
+            d[:r].zero_()
+        t = todo[:r]
+        args_r = (t, dst_row, no_cache, src_row, 0, ram, dst, lut, scale, scale_dst)
+        codec.decode_rows_from_ram(*args_r)
+        torch.cuda.synchronize()
+        if not all(torch.equal(d[:r], w[:r]) for d, w in zip(dst, raws)):
+            raise SystemExit("decode from the RAM tier differs from the raw rows")
+        e0.record()
+        for _ in range(5):
+            codec.decode_rows_from_ram(*args_r)
+        e1.record()
+        torch.cuda.synchronize()
+        ram_us[str(r)] = round(e0.elapsed_time(e1) / 5 * 1e3, 1)
+    del ram, hosts
+    for b in bufs:
+        b.free()
+    log(f"decode from pinned RAM, us by rows: {ram_us}")
+
     # CPU baseline: the oracle's C decoder on a bounded sample, all cores.
     sample = max(1, min(args.cpu_rows, count))
     t0 = time.perf_counter()
@@ -200,8 +269,10 @@ def bench_decode(args, dev, cores):
         "gbps": gbps,
         "raw_gbps": raw_gbps,
         "alg_bytes": alg,
+        "n_bytes": n_bytes,
         "sweep": sweep,
         "sweep_us": sweep_us,
+        "ram_us": ram_us,
         "cpu": {"value": round(cpu_gbps, 3), "unit": "GB/s", "cores": cores, "kind": "port",
                 "sample": f"oracle C decoder (the reference's sequential decode rule), {sample} of the "
                           f"{count} experts (w13+w2 rows), {reps} repetitions, threads over groups"},
@@ -709,9 +780,11 @@ def build_paged_model(dev, settings, keep_weights: bool = False):
     return pager, layers, weights
 
 
-def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None) -> dict:
+def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None,
+                 paging_steps: int | None = None) -> dict:
     """Run the Zipf(1.1)/0.7-reuse decode trace through a captured 40-layer step; tok/s, hit rates,
-    and the paging path alone per layer."""
+    and the paging path alone per layer (over `paging_steps` steps of a second trace, by default
+    as many as the first)."""
     c = QWEN
     L, E, H, k = c["layers"], c["experts"], c["hidden"], c["topk"]
     steps, warm = steps or args.decode_steps, args.decode_warmup
@@ -772,12 +845,13 @@ def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None)
     for _ in range(max(0, warm - 1)):
         pgraph.replay()
     torch.cuda.synchronize()
+    psteps = paging_steps or steps
     e0.record()
-    for _ in range(steps):
+    for _ in range(psteps):
         pgraph.replay()
     e1.record()
     torch.cuda.synchronize()
-    pager_ms = e0.elapsed_time(e1) / steps
+    pager_ms = e0.elapsed_time(e1) / psteps
     out = {
         "workload": label,
         "tok_s": round(1e3 / ms, 2),
@@ -789,6 +863,8 @@ def decode_trace(args, dev, pager, layers, label: str, steps: int | None = None)
         "paging_path_us_per_layer": round(pager_ms * 1e3 / L, 2),
         "steps": steps,
     }
+    if psteps != steps:
+        out["paging_path_steps"] = psteps
     if ssd is not None:
         out["ssd"] = ssd
     log(f"decode trace: {out}")
@@ -1041,7 +1117,7 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
                               "40-layer decode trace, 256 experts x 3 MiB, 32 cache slots, 128 RAM slots of "
                               "rows compressed at pitch 0.89, the rest read from the paging file (O_DIRECT), "
                               f"batch 1, top-8, Zipf(1.1) with 0.7 reuse, {steps} steps in one "
-                              "captured hipGraph per step", steps=steps)
+                              "captured hipGraph per step", steps=steps, paging_steps=min(steps, 300))
         # The server's read rate while it has a request in flight (records read x record bytes /
         # busy seconds; requests overlap, so the summed request time would undercount), against
         # the disk's ceiling at the server's own depth (its reader threads) and at 1 (a decode
@@ -1086,8 +1162,8 @@ def main() -> None:
                          "needs ~30 GB of disk for the paging file)")
     ap.add_argument("--no-tiered", action="store_true",
                     help="leave the compressed-tier legs out of the default run")
-    ap.add_argument("--tiered-decode-steps", type=int, default=300,
-                    help="decode steps of the compressed tier in the default run")
+    ap.add_argument("--tiered-decode-steps", type=int, default=2000,
+                    help="decode steps of the compressed tier in the default run (the configured 2000)")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--paging-dir", default=os.environ.get("TMPDIR", "/tmp"))
     ap.add_argument("--decode-steps", type=int, default=2000)
@@ -1174,12 +1250,14 @@ def main() -> None:
             "unit": "GB/s",
             "frac": round(dec["gbps"] / HBM_PEAK_GBPS, 4),
             "traffic": decode_traffic(args.rows),
+            "valu": decode_valu(args.rows, dec["alg_bytes"], dec["gbps"], dec["n_bytes"]),
         },
         "cpu_baseline": dec["cpu"],
         "decode_warmup": dec["warm"],
         "decode_raw_output_gbps": round(dec["raw_gbps"], 2),
         "decode_gbps_by_rows": dec["sweep"],
         "decode_us_by_rows": dec["sweep_us"],
+        "decode_from_ram_us_by_rows": dec["ram_us"],
         **extras,
     }
     print(json.dumps(line), flush=True)
