@@ -380,7 +380,8 @@ constexpr int kMaxKB = 64;    // K blocks a workgroup keeps row scales for (H, I
 // overlap the loads.
 //
 // Vector memory operations complete in issue order, so "block k has landed"
-// is "at most the last step's kOps loads are in flight" (s_waitcnt vmcnt).
+// is "at most the loads this wave issued in the last step are in flight"
+// (s_waitcnt vmcnt; the count depends on the item, see issue()).
 // That holds only if nothing is issued after a step's operand loads, and if
 // the compiler adds no waits of its own: every other load in the loop goes
 // to LDS or through the scalar cache, and the epilogue's global stores are
@@ -398,6 +399,21 @@ template <int N>
 __device__ __forceinline__ void ring_barrier() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// ring_barrier<n> for a wave-uniform n in [lo, hi]: the loads a wave issues
+// per step depend on the item (see the prefill GEMMs), so the count left in
+// flight is chosen at run time from the immediates the wait takes.
+template <int LO, int HI>
+__device__ __forceinline__ void ring_barrier_n(int n) {
+  if constexpr (LO >= HI) {
+    ring_barrier<HI>();
+  } else {
+    if (n <= LO)
+      ring_barrier<LO>();
+    else
+      ring_barrier_n<LO + 1, HI>(n);
+  }
 }
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -548,7 +564,6 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
                                                                int64_t npairs, Work work) {
   constexpr int NW = kGemmWaves, NT = NW * 64, NC = NW * 16;
   constexpr int NB = 2 * NC;       // weight rows per item: per wave 16 gate, then 16 up
-  constexpr int kOps = 4 + 2 + 1;  // loads per wave and step: weight rows, A rows, A scales
   static_assert(NC == kKB, "a workgroup covers one 128-column scale group of the activations");
   __shared__ __attribute__((aligned(16))) uint8_t s_b[kRing][NB * kRowB];
   __shared__ __attribute__((aligned(16))) uint8_t s_a[kRing][kWM * kRowB];
@@ -589,14 +604,27 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
       dma4(w13_scale, static_cast<uint32_t>(4 * (blk * KB + (i < KB ? i : i - KB))), dst + 64 * wave);
     }
   };
-  auto issue = [&](int stage, const uint8_t* wb, const AOffsets& ao, int kb) {
+  // Block kb of an item with nmi live subtiles into `stage`: every wave its
+  // 32 weight rows; wave w its A rows 16w .. 16w + 15 only when they hold
+  // pairs (w < nmi); waves 0 and 1 the A rows' scales (wave 1's half only
+  // when rows 64 and up hold pairs). Returns the loads this wave issued,
+  // which the wait before the block after next leaves in flight.
+  auto issue = [&](int stage, const uint8_t* wb, const AOffsets& ao, int kb, int nmi) {
     const uint8_t* bsrc = wb + kb * kRowB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(bsrc, boff[i], s_b[stage] + (32 * wave + 8 * i) * kRowB);
-    const uint8_t* asrc = xq + kb * kRowB;
+    int ops = 4;
+    if (wave < nmi) {
+      const uint8_t* asrc = xq + kb * kRowB;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(asrc, ao.a[i], s_a[stage] + (16 * wave + 8 * i) * kRowB);
-    dma4(xs + kb, ao.s, &s_s[stage][64 * (wave & 1)]);
+      for (int i = 0; i < 2; ++i) dma16(asrc, ao.a[i], s_a[stage] + (16 * wave + 8 * i) * kRowB);
+      ops += 2;
+    }
+    if (wave == 0 || (wave == 1 && nmi > 4)) {
+      dma4(xs + kb, ao.s, &s_s[stage][64 * wave]);
+      ops += 1;
+    }
+    return ops;
   };
   // The fp8 rows and scales of the previous item, staged in LDS.
   int out_cb = 0, out_c0 = 0, out_rows = 0;
@@ -621,8 +649,8 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
   put_rows(cur, s_pn, topk, npairs, s_pair[0], s_row[0]);
   lds_barrier();
   AOffsets ao_cur = a_offsets(s_row[0], H, KB), ao_nxt = ao_cur;
-  issue(0, wbase(cur), ao_cur, 0);
-  issue(1, wbase(cur), ao_cur, KB > 1 ? 1 : 0);
+  issue(0, wbase(cur), ao_cur, 0, (cur.count + 15) >> 4);
+  int last_ops = issue(1, wbase(cur), ao_cur, KB > 1 ? 1 : 0, (cur.count + 15) >> 4);
 
   int st = 0;  // stage of the current step
   int cb = 0;  // row set of the current item
@@ -631,7 +659,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
     const bool more = nxt.count > 0;
     const uint8_t* wb_cur = wbase(cur);
     const uint8_t* wb_nxt = more ? wbase(nxt) : wb_cur;
-    const int nmi = (cur.count + 15) >> 4;
+    const int nmi = (cur.count + 15) >> 4, nmi_nxt = (nxt.count + 15) >> 4;
     Item after = nxt;
 
     with_subtiles(nmi, [&](auto nmi_c) {
@@ -641,7 +669,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
       for (int mi = 0; mi < MI; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
       for (int k = 0; k < KS; ++k) {
-        ring_barrier<kOps>();  // block k is in stage st
+        ring_barrier_n<4, 7>(last_ops);  // block k is in stage st
         const int sn = st == 0 ? kRing - 1 : st - 1;  // the stage multiplied one step ago
         if (k == 0 && out_rows > 0) {
           copy_out(s_a[sn]);  // staged there by the previous item's epilogue
@@ -664,9 +692,9 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
         // Block k + kAhead of this item, or the next item's first blocks.
         const int blk = k + kAhead;
         if (blk < KS || !more)
-          issue(sn, wb_cur, ao_cur, blk < KB ? blk : KB - 1);
+          last_ops = issue(sn, wb_cur, ao_cur, blk < KB ? blk : KB - 1, nmi);
         else
-          issue(sn, wb_nxt, ao_nxt, blk - KS < KB ? blk - KS : KB - 1);
+          last_ops = issue(sn, wb_nxt, ao_nxt, blk - KS < KB ? blk - KS : KB - 1, nmi_nxt);
         if (k < KB) {
           const float g = s_sw[cb][k], u = s_sw[cb][KB + k];
           u32x4 bg[2], bu[2];
@@ -1397,7 +1425,6 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64
                                                                const int32_t* __restrict__ wide, int64_t wmax,
                                                                int64_t npairs, Work work, uint16_t* __restrict__ out) {
   constexpr int NW = kGemmWaves, NT = NW * 64, NC = NW * 16 * TB;  // output columns per item
-  constexpr int kOps = 2 * TB + 2 + 1;
   constexpr int kStageRows = 64;  // output rows staged per epilogue round: 64 x NC bf16 = one weight stage
   static_assert(kStageRows * NC * 2 == NC * kRowB, "an epilogue round fills one weight stage");
   __shared__ __attribute__((aligned(16))) uint8_t s_b[kRing][NC * kRowB];
@@ -1439,14 +1466,24 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64
       dma4(topk_weight, static_cast<uint32_t>(4 * rows[tid]), wt + 64 * wave);
     }
   };
-  auto issue = [&](int stage, const uint8_t* wb, const AOffsets& ao, int kb) {
+  // As gemm1_kernel's: the weight rows always, the A rows of live
+  // subtiles, the A scales by waves 0 and 1; returns the loads issued.
+  auto issue = [&](int stage, const uint8_t* wb, const AOffsets& ao, int kb, int nmi) {
     const uint8_t* bsrc = wb + kb * kRowB;
 #pragma unroll
     for (int i = 0; i < 2 * TB; ++i) dma16(bsrc, boff[i], s_b[stage] + (16 * TB * wave + 8 * i) * kRowB);
-    const uint8_t* asrc = work.act + kb * kRowB;
+    int ops = 2 * TB;
+    if (wave < nmi) {
+      const uint8_t* asrc = work.act + kb * kRowB;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(asrc, ao.a[i], s_a[stage] + (16 * wave + 8 * i) * kRowB);
-    dma4(work.acts + kb, ao.s, &s_s[stage][64 * (wave & 1)]);
+      for (int i = 0; i < 2; ++i) dma16(asrc, ao.a[i], s_a[stage] + (16 * wave + 8 * i) * kRowB);
+      ops += 2;
+    }
+    if (wave == 0 || (wave == 1 && nmi > 4)) {
+      dma4(work.acts + kb, ao.s, &s_s[stage][64 * wave]);
+      ops += 1;
+    }
+    return ops;
   };
   // Output rows [r0, r0 + rows) of an item, staged in LDS.
   int out_cb = 0, out_n0 = 0, out_r0 = 0, out_rows = 0;
@@ -1466,8 +1503,8 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64
   request_scales(cur, s_row[0], s_sw[0], s_w[0]);
   AOffsets ao_cur = a_offsets(s_row[0], I, KB), ao_nxt = ao_cur;
   ring_barrier<0>();
-  issue(0, wbase(cur), ao_cur, 0);
-  issue(1, wbase(cur), ao_cur, KB > 1 ? 1 : 0);
+  issue(0, wbase(cur), ao_cur, 0, (cur.count + 15) >> 4);
+  int last_ops = issue(1, wbase(cur), ao_cur, KB > 1 ? 1 : 0, (cur.count + 15) >> 4);
 
   int st = 0;
   int cb = 0;
@@ -1476,7 +1513,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64
     const bool more = nxt.count > 0;
     const uint8_t* wb_cur = wbase(cur);
     const uint8_t* wb_nxt = more ? wbase(nxt) : wb_cur;
-    const int nmi = (cur.count + 15) >> 4;
+    const int nmi = (cur.count + 15) >> 4, nmi_nxt = (nxt.count + 15) >> 4;
     const int n0 = cur.col * NC;
     Item after = nxt;
 
@@ -1489,7 +1526,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64
         for (int t = 0; t < TB; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
       for (int k = 0; k < KS; ++k) {
-        ring_barrier<kOps>();
+        ring_barrier_n<2 * TB, 2 * TB + 3>(last_ops);
         const int sn = st == 0 ? kRing - 1 : st - 1;
         if (k == 0 && out_rows > 0) {
           copy_out(reinterpret_cast<const uint16_t*>(s_b[sn]));
@@ -1509,9 +1546,9 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm2_kernel(int64_t H, int64
         }
         const int blk = k + kAhead;
         if (blk < KS || !more)
-          issue(sn, wb_cur, ao_cur, blk < KB ? blk : KB - 1);
+          last_ops = issue(sn, wb_cur, ao_cur, blk < KB ? blk : KB - 1, nmi);
         else
-          issue(sn, wb_nxt, ao_nxt, blk - KS < KB ? blk - KS : KB - 1);
+          last_ops = issue(sn, wb_nxt, ao_nxt, blk - KS < KB ? blk - KS : KB - 1, nmi_nxt);
         if (k < KB) {
           const float w = s_sw[cb][(TB * wave / 8) * KB + k];
           u32x4 b[TB][2];
