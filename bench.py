@@ -597,17 +597,23 @@ def bench_moe(args, dev):
     ids1 = torch.stack([torch.randperm(E, generator=g, device=dev)[:topk] for _ in range(nd)]).view(nd, 1, topk)
     tw1 = torch.softmax(torch.randn((nd, 1, topk), generator=g, device=dev), dim=2).contiguous()
     ids1 = ids1.to(torch.int64).contiguous()
+    # Each step's pair slots, as the acquire kernel writes them for the pager.
+    pslot1 = emap[ids1].contiguous()
 
-    def decode_steps():
+    def decode_steps(pairs_from_acquire: bool):
         for i in range(nd):
-            moe.decode_experts(x1[i], tw1[i], ids1[i], emap, E, w13, w13s, w2, w2s, E)
+            moe.decode_experts(x1[i], tw1[i], ids1[i], emap, E, w13, w13s, w2, w2s, E,
+                               pair_slot=pslot1[i].view(-1) if pairs_from_acquire else None)
 
-    decode_steps()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        decode_steps()
-    us_decode = timed(graph.replay, reps) * 1e3 / nd
+    us_decode = {}
+    for mode in (True, False):
+        decode_steps(mode)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            decode_steps(mode)
+        us_decode[mode] = timed(graph.replay, reps) * 1e3 / nd
+        del graph
     decode_bytes = topk * (2 * I * H + H * I)
     pairs = T * topk
     flops = 2.0 * pairs * (2 * I * H + H * I)
@@ -626,8 +632,9 @@ def bench_moe(args, dev):
         "ms_layer_one_shot": round(ms_layer, 4),
         "ms_layer_chunked_4x64": round(ms_chunked, 4),
         "chunked_bit_exact": exact,
-        "decode_ffn_batch1_us": round(us_decode, 2),
-        "decode_ffn_batch1_weight_gbps": round(decode_bytes / (us_decode * 1e-6) / 1e9, 1),
+        "decode_ffn_batch1_us": round(us_decode[True], 2),
+        "decode_ffn_batch1_weight_gbps": round(decode_bytes / (us_decode[True] * 1e-6) / 1e9, 1),
+        "decode_ffn_batch1_us_ids_through_expert_map": round(us_decode[False], 2),
     }
     log(f"moe: {out}")
     return out

@@ -69,13 +69,17 @@ typedef struct xp_table {
  * K <= ram->num_slots. Writes expert_map[E] (int32, slot or -1 for unneeded
  * experts; from the VRAM table), vram_slot[E] / ram_slot[E] (slot of each
  * expert, meaningful for needed experts) and vram_todo[K] / ram_todo[K]
- * (misses in ascending expert id, then -1).
+ * (misses in ascending expert id, then -1). pair_slot (nullable, int32[K])
+ * receives the VRAM slot of each id in step order (-1 for an id outside
+ * [0, E)), which xp_moe_decode_experts can take instead of looking each id
+ * up in expert_map; the reference has no such output.
  * Replaces AcquirePair.__call__ (acquire.py:168-185) and its kernel
  * _acquire_pair_kernel / _acquire (acquire.py:25-141). */
 int xp_acquire_pair(const void* topk, int topk_elem_bytes, int64_t K,
                     const xp_table* vram, const xp_table* ram,
                     int32_t* expert_map, int64_t* vram_slot, int64_t* vram_todo,
-                    int64_t* ram_slot, int64_t* ram_todo, void* stream);
+                    int64_t* ram_slot, int64_t* ram_todo, int32_t* pair_slot,
+                    void* stream);
 
 /* One table's acquire. expert_map_i64 (nullable) receives slot or -1 as
  * int64 (the torch version's return value), expert_map_i32 (nullable) the
@@ -429,12 +433,15 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T,
  * whose experts are all in the slab (experts.py:579-604): every pair with a
  * valid id should have a slot (one without adds nothing here). work is
  * xp_moe_workspace_bytes(T * topk, I) bytes, 256-byte aligned. Fails with
- * XP_E_LIMIT (launching nothing) above those sizes. */
+ * XP_E_LIMIT (launching nothing) above those sizes. pair_slot (nullable)
+ * gives each pair's slot directly, as xp_acquire_pair writes it; then
+ * topk_ids and expert_map are not read (same bits when it equals
+ * expert_map[topk_ids]). */
 int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H,
                           const void* topk_ids, int topk_elem_bytes,
                           int64_t topk, const float* topk_weight,
-                          const int32_t* expert_map, int64_t num_experts,
-                          int64_t I, const uint8_t* w13,
+                          const int32_t* expert_map, const int32_t* pair_slot,
+                          int64_t num_experts, int64_t I, const uint8_t* w13,
                           const float* w13_scale, const uint8_t* w2,
                           const float* w2_scale, int64_t slots, void* work,
                           int64_t work_bytes, uint16_t* out, void* stream);

@@ -85,6 +85,9 @@ def test_pair_matches_oracle(E, S, R, warm, dtype):
         np.testing.assert_array_equal(pair.ram_slot.cpu().numpy(), rslot)
         np.testing.assert_array_equal(todo.cpu().numpy(), vtodo)
         np.testing.assert_array_equal(ssd.cpu().numpy(), rtodo)
+        # Each id's VRAM slot in step order: the oracle's expert_map at the id, -1 for an invalid id.
+        want_pairs = np.array([emap[i] if 0 <= i < E else -1 for i in ids], np.int32)
+        np.testing.assert_array_equal(pair.pair_slot[:k].cpu().numpy(), want_pairs, err_msg=f"step {step}")
 
 
 def test_pair_single_layer_decode_trace():

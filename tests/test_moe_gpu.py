@@ -343,9 +343,17 @@ def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits):
     emap_t = _dev(emap)[0]
     want = _separate(moe, xb, tw_t, ids_t, emap_t, E, slots, w)
     assert moe.decode_fits(xb, ids_t, I)
+    # Each pair's slot as the acquire writes it (-1 for an invalid id), in a
+    # longer buffer as the pager keeps it.
+    flat = ids.reshape(-1).astype(np.int64)
+    pslot = np.full(flat.size + 5, -1, np.int32)
+    pslot[: flat.size] = [emap[i] if 0 <= i < E else -1 for i in flat]
+    pslot_t = _dev(pslot)[0]
     for _ in range(2):
         got = moe.decode_experts(xb, tw_t, ids_t, emap_t, E, *w, slots)
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        got = moe.decode_experts(xb, tw_t, ids_t, emap_t, E, *w, slots, pair_slot=pslot_t)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "with pair slots"
 
 
 def test_decode_experts_in_a_graph():

@@ -964,13 +964,19 @@ struct DecodeRoute {
 };
 
 __device__ __forceinline__ DecodeRoute decode_route(int p, int n, const void* ids, int eb,
-                                                    const int32_t* __restrict__ expert_map, int E, int slots) {
+                                                    const int32_t* __restrict__ expert_map,
+                                                    const int32_t* __restrict__ pair_slot, int E, int slots) {
   int slot = -1;
   if (p < n) {
-    const int64_t e = load_id(ids, eb, p);
-    if (e >= 0 && e < E) {
-      const int sl = expert_map[e];
+    if (pair_slot) {  // each pair's slot, as the acquire wrote it: one load
+      const int sl = pair_slot[p];
       slot = sl >= 0 && sl < slots ? sl : -1;
+    } else {
+      const int64_t e = load_id(ids, eb, p);
+      if (e >= 0 && e < E) {
+        const int sl = expert_map[e];
+        slot = sl >= 0 && sl < slots ? sl : -1;
+      }
     }
   }
   int before = 0;
@@ -994,7 +1000,8 @@ __device__ __forceinline__ DecodeRoute decode_route(int p, int n, const void* id
 // quantisation of their token rows done here. Dynamic LDS: 16 x H fp8 rows.
 __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
     const uint16_t* __restrict__ x, int64_t H, int64_t I, const void* ids, int eb, int npairs, int topk,
-    const int32_t* __restrict__ expert_map, int E, int slots, const uint8_t* __restrict__ w13,
+    const int32_t* __restrict__ expert_map, const int32_t* __restrict__ pair_slot, int E, int slots,
+    const uint8_t* __restrict__ w13,
     const float* __restrict__ w13_scale, int nsub, Work work) {
   constexpr int kPerWave = kSplitRound / (kThreads / 64);
   extern __shared__ __attribute__((aligned(16))) uint8_t s_aq[];  // [16][H] fp8 token rows
@@ -1046,7 +1053,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
   const int ntok = npairs / topk;
   const bool by_token = ntok <= 16;
   if (wave == 0) {
-    const DecodeRoute r = decode_route(lane, npairs, ids, eb, expert_map, E, slots);
+    const DecodeRoute r = decode_route(lane, npairs, ids, eb, expert_map, pair_slot, E, slots);
     // gemm2_decode_kernel reads the pairs' slots from the workspace (the
     // activation-scale region, which the decode path does not use).
     if (blockIdx.x == 0 && lane < npairs) reinterpret_cast<int32_t*>(work.acts)[lane] = r.slot;
@@ -1885,8 +1892,8 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T, int64_
 }
 
 int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* topk_ids, int topk_elem_bytes,
-                          int64_t topk, const float* topk_weight, const int32_t* expert_map, int64_t num_experts,
-                          int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
+                          int64_t topk, const float* topk_weight, const int32_t* expert_map,
+                          const int32_t* pair_slot, int64_t num_experts, int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
                           const float* w2_scale, int64_t slots, void* work, int64_t work_bytes, uint16_t* out,
                           void* stream) {
   const char* what = "xp_moe_decode_experts";
@@ -1918,7 +1925,8 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
   const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
   hipLaunchKernelGGL(gemm1_decode_kernel, dim3(static_cast<unsigned>(tiles8 * nsub * (I / 16))), dim3(kThreads),
                      static_cast<size_t>(16 * H), as_stream(stream), x, H, I, topk_ids, topk_elem_bytes,
-                     static_cast<int>(npairs), static_cast<int>(topk), expert_map, static_cast<int>(num_experts),
+                     static_cast<int>(npairs), static_cast<int>(topk), expert_map, pair_slot,
+                     static_cast<int>(num_experts),
                      static_cast<int>(slots), w13, w13_scale, nsub, w);
   int rc = check_launch("gemm1_decode_kernel");
   if (rc) return rc;

@@ -255,12 +255,20 @@ struct GlobalIds {
 __global__ void __launch_bounds__(kThreads) acquire_pair_kernel(GlobalIds ids, int K, TableDev a, TableDev b,
                                                                  int32_t* expert_map, int64_t* a_slot,
                                                                  int64_t* a_todo, int64_t* b_slot,
-                                                                 int64_t* b_todo) {
+                                                                 int64_t* b_todo, int32_t* pair_slot) {
   __shared__ AcquireLds lds;
-  if (blockIdx.x == 0)
+  if (blockIdx.x == 0) {
     acquire_block(ids, K, a, nullptr, expert_map, a_slot, a_todo, true, false, lds);
-  else
+    // Each id's slot in table a, in step order: the expert FFN reads it in
+    // one load instead of id then expert_map.
+    if (pair_slot)
+      for (int k = threadIdx.x; k < K; k += kThreads) {
+        const int64_t id = ids(k);
+        pair_slot[k] = id >= 0 && id < a.E ? static_cast<int32_t>(lds.fin[id]) : -1;
+      }
+  } else {
     acquire_block(ids, K, b, nullptr, nullptr, b_slot, b_todo, true, false, lds);
+  }
 }
 
 __global__ void __launch_bounds__(kThreads) acquire_one_kernel(GlobalIds ids, int K, TableDev t, int64_t* map64,
@@ -472,7 +480,7 @@ extern "C" {
 
 int xp_acquire_pair(const void* topk, int topk_elem_bytes, int64_t K, const xp_table* vram, const xp_table* ram,
                     int32_t* expert_map, int64_t* vram_slot, int64_t* vram_todo, int64_t* ram_slot,
-                    int64_t* ram_todo, void* stream) {
+                    int64_t* ram_todo, int32_t* pair_slot, void* stream) {
   int rc;
   if ((rc = check_ids(topk, topk_elem_bytes, K, "xp_acquire_pair")) ||
       (rc = check_table(vram, "xp_acquire_pair(vram)")) || (rc = check_table(ram, "xp_acquire_pair(ram)")))
@@ -485,7 +493,7 @@ int xp_acquire_pair(const void* topk, int topk_elem_bytes, int64_t K, const xp_t
   XP_REQUIRE(expert_map && vram_slot && vram_todo && ram_slot && ram_todo, "xp_acquire_pair: null output");
   hipLaunchKernelGGL(acquire_pair_kernel, dim3(2), dim3(kThreads), 0, as_stream(stream),
                      GlobalIds{topk, topk_elem_bytes}, static_cast<int>(K), to_dev(vram), to_dev(ram), expert_map,
-                     vram_slot, vram_todo, ram_slot, ram_todo);
+                     vram_slot, vram_todo, ram_slot, ram_todo, pair_slot);
   return check_launch("acquire_pair_kernel");
 }
 

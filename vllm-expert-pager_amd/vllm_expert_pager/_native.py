@@ -92,7 +92,7 @@ _L = c_i64
 _SIGNATURES = {
     "xp_last_error": (ctypes.c_char_p, []),
     "xp_version": (ctypes.c_char_p, []),
-    "xp_acquire_pair": (_I, [_P, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "xp_acquire_pair": (_I, [_P, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "xp_table_acquire": (_I, [_P, _I, _L, _P, _P, _P, _P, _P, _P]),
     "xp_need_mask": (_I, [_P, _I, _L, _L, _P, _P]),
     "xp_pack": (_I, [_P, _L, _P, _P]),
@@ -126,7 +126,7 @@ _SIGNATURES = {
     "xp_moe_workspace_bytes": (_L, [_L, _L]),
     "xp_moe_experts": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _L, _P, _P]),
     "xp_ssd_read_probe": (_I, [_I, _L, _P, _L, _I, _I, _P]),
-    "xp_moe_decode_experts": (_I, [_P, _L, _L, _P, _I, _L, _P, _P, _L, _L, _P, _P, _P, _P, _L, _P, _L, _P, _P]),
+    "xp_moe_decode_experts": (_I, [_P, _L, _L, _P, _I, _L, _P, _P, _P, _L, _L, _P, _P, _P, _P, _L, _P, _L, _P, _P]),
     "xp_moe_experts_noalloc": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P]),
     "xp_encode_rows": (_I, [_P, _L, _L, _L, _L, _P, _L, _P, _L, _P, _P]),
     "xp_moe_topk_sum": (_I, [_P, _L, _L, _L, _P, _I, _L, _P, _P]),

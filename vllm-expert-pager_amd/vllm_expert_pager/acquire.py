@@ -3,7 +3,9 @@
 ``AcquirePair(vram, ram)(topk_ids)`` updates both tables with one launch of
 two workgroups (csrc/table.hip, ``xp_acquire_pair``) and writes the int32
 ``expert_map`` at a fixed device address, plus the per-expert slots and the
-miss lists. Same contract as the reference (acquire.py:144-185).
+miss lists. Same contract as the reference (acquire.py:144-185). It also
+writes ``pair_slot``, each id's VRAM slot in step order, which the decode
+step's expert FFN reads instead of looking the ids up in ``expert_map``.
 """
 
 from __future__ import annotations
@@ -32,6 +34,8 @@ class AcquirePair:
         self.expert_map = torch.full((E,), -1, dtype=torch.int32, device=device)
         self.vram_slot = torch.zeros((E,), **i64)
         self.ram_slot = torch.zeros((E,), **i64)
+        # Each id's VRAM slot in step order (K <= vram.num_slots ids).
+        self.pair_slot = torch.full((vram.num_slots,), -1, dtype=torch.int32, device=device)
         self._vram_todo = torch.full((vram.num_slots,), -1, **i64)
         self._ram_todo = torch.full((ram.num_slots,), -1, **i64)
         self._a = vram._struct()
@@ -40,14 +44,14 @@ class AcquirePair:
     def __call__(self, topk_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Update both tables; returns ``(vram_todo, ram_todo)`` of length K.
 
-        ``expert_map``, ``vram_slot`` and ``ram_slot`` are written in place.
-        Requires ``topk_ids.numel() <= vram.num_slots``.
+        ``expert_map``, ``vram_slot``, ``ram_slot`` and ``pair_slot[:K]`` are
+        written in place. Requires ``topk_ids.numel() <= vram.num_slots``.
         """
         ids, eb = nat.ids_arg(topk_ids)
         K = ids.numel()
         nat.call(
             "xp_acquire_pair", nat.ptr(ids), eb, K, nat.ctypes.byref(self._a), nat.ctypes.byref(self._b),
             self.expert_map.data_ptr(), self.vram_slot.data_ptr(), self._vram_todo.data_ptr(),
-            self.ram_slot.data_ptr(), self._ram_todo.data_ptr(), nat.stream(),
+            self.ram_slot.data_ptr(), self._ram_todo.data_ptr(), self.pair_slot.data_ptr(), nat.stream(),
         )
         return self._vram_todo[:K], self._ram_todo[:K]

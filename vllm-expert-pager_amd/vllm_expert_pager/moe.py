@@ -230,12 +230,15 @@ def decode_experts(
     w2: torch.Tensor,
     w2_scale: torch.Tensor,
     slots: int,
+    pair_slot: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``quant_route`` + ``run_experts`` + ``topk_sum`` of a decode step in two launches, same bits.
 
     Every pair with a valid expert id should have a slot below ``slots``
     (one without adds nothing, where the separate calls would read a
-    contribution never written).
+    contribution never written). ``pair_slot`` (int32, at least T * topk
+    entries), when given, holds each pair's slot as ``AcquirePair`` writes
+    it, and the routing reads it instead of ``expert_map[topk_ids]``.
     """
     nat.require_device(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2:
@@ -250,6 +253,10 @@ def decode_experts(
     if expert_map.dtype != torch.int32 or not expert_map.is_contiguous():
         raise ValueError("expert_map must be a contiguous int32 tensor")
     ids, eb = nat.ids_arg(topk_ids)
+    if pair_slot is not None:
+        nat.require_device(pair_slot, "pair_slot")
+        if pair_slot.dtype != torch.int32 or not pair_slot.is_contiguous() or pair_slot.numel() < T * topk:
+            raise ValueError(f"pair_slot must be a contiguous int32 tensor of at least {T * topk} entries")
     tw = topk_weights if topk_weights.dtype == torch.float32 else topk_weights.float()
     tw = _f32(tw.contiguous(), "topk_weights")
     S = w13.shape[0]
@@ -259,7 +266,7 @@ def decode_experts(
     out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
     nat.call(
         "xp_moe_decode_experts", x.data_ptr(), T, H, nat.ptr(ids), eb, topk, tw.data_ptr(), expert_map.data_ptr(),
-        num_experts, I, _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(), _fp8_ptr(w2, "w2"),
+        None if pair_slot is None else pair_slot.data_ptr(), num_experts, I, _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(), _fp8_ptr(w2, "w2"),
         _f32(w2_scale, "w2_scale").data_ptr(), min(slots, S), work.data_ptr(), nbytes, out.data_ptr(), nat.stream(),
     )
     return out

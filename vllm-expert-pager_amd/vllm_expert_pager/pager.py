@@ -286,7 +286,8 @@ class PagedExperts:
             if moe.decode_fits(x, topk_ids, self.pager.intermediate):
                 slab = self.cache_slab
                 out = moe.decode_experts(x, topk_weights, topk_ids, self.expert_map, E, slab[PARAMS[0]],
-                                         slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]], self.table.num_slots)
+                                         slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]], self.table.num_slots,
+                                         pair_slot=self.acquire.pair_slot)
                 self._log()
                 return out
             xq, xs, routing = moe.quant_route(x, topk_ids, self.expert_map, self.table.num_slots)
