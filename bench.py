@@ -951,6 +951,63 @@ def disk_ceiling(path: str, record_bytes: int, records: int, seconds: float = 0.
     return out
 
 
+def disk_ceiling_loaded(path: str, record_bytes: int, records: int, dev, depths=(1, 2, 4, 8),
+                        seconds: float = 0.5) -> dict:
+    """The same thread-pool probe while the GPU streams pinned host memory (host-to-device copies
+    of 1 GiB on a side stream, as a prefill chunk or decode step streams RAM-tier records while
+    the server reads): the disk's ceiling under the workload's own host-link traffic. Two passes
+    per depth, the better kept; the copy rate is reported beside it."""
+    import threading
+
+    from vllm_expert_pager import _native
+
+    lib = _native.lib()
+    src = torch.empty((1 << 30,), dtype=torch.uint8).pin_memory()
+    dst = torch.empty((1 << 30,), dtype=torch.uint8, device=dev)
+    stop = threading.Event()
+    moved = [0, 0.0]
+
+    def stream():
+        s = torch.cuda.Stream(device=dev)
+        t0 = time.perf_counter()
+        with torch.cuda.stream(s):
+            while not stop.is_set():
+                for _ in range(4):
+                    dst.copy_(src, non_blocking=True)
+                s.synchronize()
+                moved[0] += 4 * src.numel()
+        moved[1] = time.perf_counter() - t0
+
+    rng = np.random.default_rng(13)
+    fd = os.open(path, os.O_RDONLY | os.O_DIRECT)
+    out = {"threads_gbps": {}, "passes": {}}
+    th = threading.Thread(target=stream)
+    th.start()
+    try:
+        time.sleep(0.2)
+        for order in (depths, depths[::-1]):
+            for depth in order:
+                count = max(4 * depth, int(3e9 * seconds / record_bytes))
+                idx = rng.choice(records, size=count, replace=count > records)
+                offs = (ctypes.c_int64 * count)(*(int(i) * record_bytes for i in idx))
+                sec = ctypes.c_double()
+                if lib.xp_ssd_read_probe(fd, record_bytes, offs, count, depth, 0, ctypes.byref(sec)):
+                    out["passes"].setdefault(str(depth), []).append("failed")
+                    continue
+                out["passes"].setdefault(str(depth), []).append(round(count * record_bytes / sec.value / 1e9, 3))
+    finally:
+        stop.set()
+        th.join()
+        os.close(fd)
+    for depth, vals in out["passes"].items():
+        nums = [v for v in vals if isinstance(v, float)]
+        out["threads_gbps"][depth] = max(nums) if nums else None
+    out["h2d_gbps_alongside"] = round(moved[0] / moved[1] / 1e9, 1) if moved[1] > 0 else None
+    del src, dst
+    log(f"disk ceiling under host-link load: {out}")
+    return out
+
+
 def _phase_delta(after: dict, before: dict) -> dict:
     out = {k: round(after[k] - before.get(k, 0), 4) for k in ("busy_s", "queue_s", "read_s", "copy_s", "preads")}
     out.update(readers=after["readers"], bounce=after["bounce"])
@@ -1078,6 +1135,7 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
     store = pager.store
     try:
         ceiling = disk_ceiling(path, store.record_bytes, L * E)
+        loaded = disk_ceiling_loaded(path, store.record_bytes, L * E, dev)
         sweep = server_sweep(store, path)
         g = torch.Generator(device=dev).manual_seed(77)
         xs, ws, ids = [], [], []
@@ -1131,6 +1189,7 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
         # step's miss is read alone).
         rb = store.record_bytes
         tops = ceiling.get("threads_gbps", {})
+        ltops = loaded.get("threads_gbps", {})
         for tgt, reads, phases in ((prefill, prefill["ssd_reads"], prefill["ssd_phases"]),
                                    (decode, (decode.get("ssd") or {}).get("reads", 0),
                                     (decode.get("ssd") or {}).get("phases", {}))):
@@ -1138,12 +1197,13 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
             rate = reads * rb / busy / 1e9 if busy > 0 else None
             tgt["ssd_gbps_while_reading"] = round(rate, 3) if rate else None
             for name, depth in (("server_depth", str(store.readers)), ("1", "1")):
-                top = tops.get(depth)
-                tgt[f"ssd_frac_of_disk_ceiling_{name}"] = (
-                    round(rate / top, 3) if rate and isinstance(top, float) else None)
+                for kind, table in (("disk_ceiling", tops), ("loaded_disk_ceiling", ltops)):
+                    top = table.get(depth)
+                    tgt[f"ssd_frac_of_{kind}_{name}"] = (
+                        round(rate / top, 3) if rate and isinstance(top, float) else None)
         server = {"readers": store.readers, "sized_from_probe_gbps": store.reader_probe}
-        return {"disk_ceiling": ceiling, "server": server, "server_sweep": sweep, "prefill": prefill,
-                "decode": decode}
+        return {"disk_ceiling": ceiling, "disk_ceiling_under_host_link_load": loaded, "server": server,
+                "server_sweep": sweep, "prefill": prefill, "decode": decode}
     finally:
         pager.close()
         if os.path.exists(path):
