@@ -381,9 +381,18 @@ int xp_moe_quant_route(const uint16_t* x, int64_t T, int64_t H, uint8_t* xq,
  * (bf16 and fp8 activations with their scales). */
 int64_t xp_moe_workspace_bytes(int64_t npairs, int64_t I);
 
+/* Expert activations (vLLM's "silu" and "gelu" with act-and-mul): the
+ * activation of the gate in fp32, rounded to bf16, times up, rounded to
+ * bf16, as silu_and_mul / gelu_and_mul compute it in bf16
+ * (layers/activation.py). SiLU: g / (1 + exp(-g)); GELU, the erf form:
+ * g / 2 * (1 + erf(g / sqrt(2))). */
+#define XP_ACT_SILU 0
+#define XP_ACT_GELU 1
+
 /* Expert FFN of every routed pair, on the slab slot route chose:
  *   h = w13 . xq (block-scaled, fp32), gate = bf16(h[:I]), up = bf16(h[I:])
- *   a = bf16(silu(gate) * up), quantised like xp_quant_tokens per 128 columns
+ *   a = bf16(bf16(act(gate)) * up) for act = `activation` (XP_ACT_*),
+ *   quantised like xp_quant_tokens per 128 columns
  *   out[pair][H] = bf16(topk_weight[pair] * (w2 . a)) (bf16 bits)
  * topk_weight is fp32 [T*topk]; work is a 256-byte aligned device buffer of
  * xp_moe_workspace_bytes(T*topk, I) bytes (no initial contents needed).
@@ -399,7 +408,7 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T,
                    const uint8_t* w2, const float* w2_scale, int64_t slots,
                    const int32_t* offsets, const int32_t* pairs,
                    const int32_t* tiles, void* work, int64_t work_bytes,
-                   uint16_t* out, void* stream);
+                   uint16_t* out, int activation, void* stream);
 
 /* Workspace bytes xp_moe_experts_noalloc holds per device (32 MiB: a
  * 2048-token top-8 prefill at I = 512 needs 27.5 MB). */
@@ -422,7 +431,8 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T,
                            const float* w13_scale, const uint8_t* w2,
                            const float* w2_scale, int64_t slots,
                            const int32_t* offsets, const int32_t* pairs,
-                           const int32_t* tiles, uint16_t* out, void* stream);
+                           const int32_t* tiles, uint16_t* out, int activation,
+                           void* stream);
 
 /* A decode step's expert FFN in two launches, for at most 64 pairs
  * (T * topk), H <= 4096 and topk * I <= 32768: out[T][H] gets the bits of
@@ -444,7 +454,8 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H,
                           int64_t num_experts, int64_t I, const uint8_t* w13,
                           const float* w13_scale, const uint8_t* w2,
                           const float* w2_scale, int64_t slots, void* work,
-                          int64_t work_bytes, uint16_t* out, void* stream);
+                          int64_t work_bytes, uint16_t* out, int activation,
+                          void* stream);
 
 /* The single top-k combine (moe_sum after collect, experts.py:546-552):
  * out[t][H] = bf16(sum over k ascending of fp32(contrib[t*topk + k])),

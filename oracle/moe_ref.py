@@ -4,15 +4,17 @@ The reference runs vLLM's fused fp8 MoE on the slab (experts.py:579-604)
 and takes the top-k sum once over all chunks (experts.py:538-556); vLLM
 itself is not part of the reference tree, so this module restates the
 published w8a8 block-fp8 MoE of vLLM 0.29.0 (per-token-group activation
-quantisation, 128x128 weight scale blocks, SiLU-and-mul, routed-weight
-multiply, moe_sum) in numpy/torch on the CPU:
+quantisation, 128x128 weight scale blocks, SiLU-and-mul or GELU-and-mul,
+routed-weight multiply, moe_sum) in numpy/torch on the CPU:
 
   quant_groups  x -> fp8 per 128 columns: s = max(amax, 1e-10) / 448 (fp32),
                 q = rne(clamp(x / s, -448, 448))
   expert_ffn    per (token, k) pair: h = dequant(xq) . dequant(w13)^T,
-                gate/up -> bf16, a = bf16(bf16(silu(gate)) * up) (vLLM's
-                silu_and_mul returns silu in the activation dtype and then
-                multiplies two bf16 values), a -> fp8 per 128 columns,
+                gate/up -> bf16, a = bf16(bf16(act(gate)) * up) (vLLM's
+                silu_and_mul / gelu_and_mul return act in the activation
+                dtype and then multiply two bf16 values; act in fp32,
+                SiLU g / (1 + exp(-g)), GELU (g * 0.5) * (1 + erf(g * fp32(1/sqrt 2)))),
+                a -> fp8 per 128 columns,
                 y = dequant(aq) . dequant(w2)^T,
                 contribution = bf16(y * routed weight)
   topk_sum      bf16(fp32 sum over k ascending of the contributions)
@@ -29,12 +31,15 @@ maximum maps to +-448); expert_ffn on the one-hot closed form (x = c*e_i
 selects column i of w13, a permutation w2 selects activation entries),
 which fixes operand orientation and indexing; invariance under relabelling
 experts, exact scaling by powers of two of the routed weights, and
-independence of tokens; topk_sum against exact integer sums.
+independence of tokens; topk_sum against exact integer sums; activation
+against torch's silu and exact-erf gelu, and GELU's closed forms (odd part
+gelu(g) - gelu(-g) = g, saturation to g and -0).
 """
 
 from __future__ import annotations
 
 import numpy as np
+import scipy.special
 import torch
 
 BLOCK = 128
@@ -102,13 +107,44 @@ def dequant_weight(w: np.ndarray, ws: np.ndarray) -> np.ndarray:
     return _FP8[w] * np.kron(ws.astype(np.float64), np.ones((BLOCK, BLOCK)))
 
 
+ACTIVATIONS = ("silu", "gelu")
+_SQRT1_2 = np.float32(0.70710678118654752)
+
+
+def _ulp_step(v: np.ndarray, k: int) -> np.ndarray:
+    """v moved by k float32 ulps (toward +inf for k > 0)."""
+    v = np.asarray(v, np.float32)
+    to = np.float32(np.inf if k > 0 else -np.inf)
+    for _ in range(abs(k)):
+        v = np.nextafter(v, to).astype(np.float32)
+    return v
+
+
+def activation(gate: np.ndarray, name: str = "silu", erf_ulps: int = 0) -> np.ndarray:
+    """act(gate) in float32 as vLLM's act-and-mul kernels evaluate it, each
+    fp32 operation rounded: SiLU g / (1 + exp(-g)); GELU
+    (g * 0.5) * (1 + erf(g * fp32(1/sqrt 2))) with erf correctly rounded to
+    fp32, or moved by `erf_ulps` ulps (a device erff's error)."""
+    g = np.asarray(gate, np.float32)
+    if name == "silu":
+        with np.errstate(over="ignore"):
+            return (g / (np.float32(1) + np.exp(-g))).astype(np.float32)
+    if name == "gelu":
+        t = (g * _SQRT1_2).astype(np.float32)
+        e = scipy.special.erf(t.astype(np.float64)).astype(np.float32)
+        if erf_ulps:
+            e = _ulp_step(e, erf_ulps)
+        return ((g * np.float32(0.5)) * (np.float32(1) + e)).astype(np.float32)
+    raise ValueError(f"unknown activation {name!r}")
+
+
 # Planted mistakes for tests that show a set of inputs tells the rounding
 # sequence apart (expert_ffn's `variant`); each changes exactly one step.
 VARIANTS = (
     "gate_up_unrounded",   # gate and up kept in fp32 instead of rounded to bf16
     "gate_up_truncated",   # gate and up rounded to bf16 toward zero
-    "silu_unrounded",      # silu(gate) kept in fp32 before the product with up
-    "act_unrounded",       # silu(gate) * up not rounded to bf16 before quantisation
+    "silu_unrounded",      # act(gate) kept in fp32 before the product with up
+    "act_unrounded",       # bf16(act(gate)) * up not rounded to bf16 before quantisation
     "quant_reciprocal",    # activation scale applied as a * (448 / amax) instead of a / (amax / 448)
     "fp8_truncated",       # activations converted to fp8 toward zero
     "weight_after_round",  # routed weight applied to bf16(y) rather than to y
@@ -147,16 +183,20 @@ def _quant_variant(x: np.ndarray, variant: str | None) -> tuple[np.ndarray, np.n
 
 
 def expert_ffn(x: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray, w13: np.ndarray, w13_scale: np.ndarray,
-               w2: np.ndarray, w2_scale: np.ndarray, variant: str | None = None) -> np.ndarray:
+               w2: np.ndarray, w2_scale: np.ndarray, variant: str | None = None,
+               act: str = "silu") -> np.ndarray:
     """bf16 contributions (T*topk, H) as float32; pairs with an id outside [0, E) are 0.
 
     x: (T, H) float32 holding bf16 values; w13: (E, 2I, H) fp8 codes (gate
     rows then up rows), w2: (E, H, I); scales (E, 2I/128, H/128) and
-    (E, H/128, I/128) float32. `variant` (one of VARIANTS) plants one
-    mistake in the rounding sequence, for tests of test inputs only.
+    (E, H/128, I/128) float32; `act` one of ACTIVATIONS. `variant` (one of
+    VARIANTS) plants one mistake in the rounding sequence, for tests of test
+    inputs only.
     """
     if variant is not None and variant not in VARIANTS:
         raise ValueError(f"unknown variant {variant!r}")
+    if act not in ACTIVATIONS:
+        raise ValueError(f"unknown activation {act!r}")
     x = np.asarray(x, np.float32)
     T, H = x.shape
     ids = np.asarray(topk_ids).reshape(T, -1)
@@ -180,11 +220,10 @@ def expert_ffn(x: np.ndarray, topk_weights: np.ndarray, topk_ids: np.ndarray, w1
             gate, up = _bf16_toward_zero(h[:, :I]), _bf16_toward_zero(h[:, I:])
         else:
             gate, up = bf16(h[:, :I]), bf16(h[:, I:])
-        with np.errstate(over="ignore"):
-            silu = (gate / (np.float32(1) + np.exp(-gate))).astype(np.float32)
+        g = activation(gate, act)
         if variant != "silu_unrounded":
-            silu = bf16(silu)
-        a = (silu * up).astype(np.float32) if variant == "act_unrounded" else bf16(silu * up)
+            g = bf16(g)
+        a = (g * up).astype(np.float32) if variant == "act_unrounded" else bf16(g * up)
         aq, as_ = _quant_variant(a, variant)
         y = (dequant_rows(aq, as_) @ dequant_weight(w2[e], w2_scale[e]).T).astype(np.float32)
         w = tw.reshape(-1)[pairs][:, None]
@@ -203,45 +242,57 @@ def bf16_midpoint_margin(v: np.ndarray) -> np.ndarray:
 
 # Probe gates of exact_inputs are v * c / 4: v the token's column-0 value
 # (m * 2^a, m in 1..3), c the weight code (+-1..4). The (m, a) pairs for which
-# silu of every such gate is at least PROBE_MARGIN (relative) away from a bf16
-# rounding midpoint, so that bf16(silu(g)) does not depend on how an fp32 exp
-# and division round (a few fp32 ulps, about 2^-21).
+# the activation of every such gate rounds to bf16 the same whichever way a
+# device's fp32 transcendental rounds: for SiLU, silu(g) at least PROBE_MARGIN
+# (relative) away from a bf16 rounding midpoint (an fp32 exp and division are
+# off by a few fp32 ulps, about 2^-21); for GELU, the fp32 evaluation rounds
+# to the same bf16 bits with erf moved by up to ERF_ULPS fp32 ulps (1 + erf
+# cancels for negative gates, so the margin is taken through erf itself).
 PROBE_MARGIN = 2.0**-14
+ERF_ULPS = 4
 
 
-def _safe_probe_values() -> list[tuple[int, int]]:
-    safe = []
-    for a in range(-3, 4):
-        for m in (1, 2, 3):
-            g = np.array([s * m * 2.0**a * c / 4 for s in (1, -1) for c in (1, 2, 3, 4, -1, -2, -3, -4)])
-            silu = g / (1 + np.exp(-g))
-            if bf16_midpoint_margin(silu).min() >= PROBE_MARGIN:
-                safe.append((m, a))
-    return safe
+def _probe_gates(m: int, a: int) -> np.ndarray:
+    return np.array([s * m * 2.0**a * c / 4 for s in (1, -1) for c in (1, 2, 3, 4, -1, -2, -3, -4)], np.float32)
 
 
-def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk: int):
-    """A MoE case on which every sum is exact in fp32 and every SiLU is exact
-    or rounds to bf16 unambiguously, while every rounding step of the
-    sequence still rounds: the rounding sequence, not summation order,
-    decides the output bits.
+def probe_is_safe(g: np.ndarray, act: str) -> bool:
+    """Whether bf16(act(g)) is fixed for every gate in g (see PROBE_MARGIN)."""
+    if act == "silu":
+        g64 = np.asarray(g, np.float64)
+        return bool(bf16_midpoint_margin(g64 / (1 + np.exp(-g64))).min() >= PROBE_MARGIN)
+    bits = [bf16_bits(activation(g, act, k)) for k in range(-ERF_ULPS, ERF_ULPS + 1)]
+    return all(np.array_equal(b, bits[0]) for b in bits)
+
+
+def _safe_probe_values(act: str = "silu") -> list[tuple[int, int]]:
+    return [(m, a) for a in range(-3, 4) for m in (1, 2, 3) if probe_is_safe(_probe_gates(m, a), act)]
+
+
+def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk: int, act: str = "silu"):
+    """A MoE case on which every sum is exact in fp32 and every activation
+    (`act`) is exact or rounds to bf16 unambiguously, while every rounding
+    step of the sequence still rounds: the rounding sequence, not summation
+    order, decides the output bits.
 
     - x: per token one or two active 128-column groups, group 0 always
       among them; each has one value of +-448 * 2^a (so the group scale is
       exactly 2^a) and a few of +-1..3 * 2^a; the other groups are zero.
-      Column 0 holds +-m * 2^a with (m, a) drawn from _safe_probe_values.
+      Column 0 holds +-m * 2^a with (m, a) drawn from _safe_probe_values(act).
     - w13 gate rows 0-127 (the first activation group) have codes in
       {0, +-1, +-2} over every column and block scale 2^10, so each block
       dot is an integer below 2^11 and every such gate is 0 or at least 104
-      in magnitude: silu(g) is g or -0 whatever exp's last bit.
+      in magnitude: silu(g) is g or -0 whatever exp's last bit, and gelu(g)
+      g or -0 (erf(+-73.5) is +-1 in fp32, which every erff returns).
     - w13 gate rows 128-255 (the second activation group, when I >= 256)
       are probes: one code c in {+-1..4} at column 0, block scale 2^-2, so
-      the gate is v * c / 4, between 2^-5 and 24 in magnitude, where silu
-      is a general value; its bf16 rounding is unambiguous (PROBE_MARGIN),
-      and bf16(silu(g)) * up rounds differently from silu(g) * up.
+      the gate is v * c / 4, between 2^-5 and 24 in magnitude, where the
+      activation is a general value; its bf16 rounding is unambiguous
+      (probe_is_safe), and bf16(act(g)) * up rounds differently from
+      act(g) * up.
     - Up rows: codes in {0, +-1, +-2, +-3}, scale 2^-4.
     - gate and up then carry up to 11 significant bits (bf16 keeps 8), and
-      a = bf16(bf16(silu(gate)) * up) up to 16: the roundings round, ties
+      a = bf16(bf16(act(gate)) * up) up to 16: the roundings round, ties
       included.
     - w2 rows: one non-zero code in {+-1..+-4} per row, scale 2^-2, in the
       first activation group for even rows and in the second (the probes)
@@ -278,7 +329,7 @@ def exact_inputs(rng: np.random.Generator, E: int, H: int, I: int, T: int, topk:
     np.put_along_axis(w2, cols[:, :, None], vals[:, :, None], axis=2)
     w2s = np.full((E, H // BLOCK, GI), 2.0**-2, np.float32)
 
-    safe = _safe_probe_values()
+    safe = _safe_probe_values(act)
     x = np.zeros((T, H), np.float32)
     for t in range(T):
         extra = rng.choice(np.arange(1, G), size=int(rng.integers(0, 2)), replace=False) if G > 1 else []
@@ -314,9 +365,9 @@ def topk_sum(contrib: np.ndarray, topk_ids: np.ndarray, num_experts: int) -> np.
     return bf16(acc)
 
 
-def fused_moe_ref(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, variant=None) -> np.ndarray:
+def fused_moe_ref(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, variant=None, act="silu") -> np.ndarray:
     """The layer output (T, H) as float32 holding bf16 values."""
-    contrib = expert_ffn(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, variant)
+    contrib = expert_ffn(x, topk_weights, topk_ids, w13, w13_scale, w2, w2_scale, variant, act)
     return topk_sum(contrib, topk_ids, w13.shape[0])
 
 

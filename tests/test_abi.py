@@ -47,6 +47,51 @@ def test_every_symbol_has_a_python_signature():
     assert not missing, f"no ctypes signature for {missing}"
 
 
+def declarations() -> dict[str, list[str]]:
+    """Each declared function's parameter list (type text of each parameter)."""
+    text = open(os.path.join(ROOT, "include", "xp.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s*\b([a-z_][a-z0-9_]*)\s*\(([^;{]*?)\)\s*;",
+                         text, flags=re.M | re.S):
+        params = [" ".join(p.split()) for p in m.group(2).split(",")]
+        out[m.group(1)] = [] if params == ["void"] or params == [""] else params
+    return out
+
+
+def _kind(param: str) -> str:
+    """'ptr', 'i32' or 'i64' for a C parameter declaration."""
+    if "*" in param:
+        return "ptr"
+    if re.search(r"\b(int64_t|long|size_t)\b", param):
+        return "i64"
+    if re.search(r"\b(int|int32_t)\b", param):
+        return "i32"
+    if re.search(r"\bdouble\b", param):
+        return "f64"
+    raise AssertionError(f"unexpected parameter type {param!r}")
+
+
+def test_python_signatures_match_the_header():
+    """Every ctypes signature has the header's arity and, position by
+    position, its pointer / 32-bit / 64-bit integer kinds (a missing or
+    extra argument shifts every later one)."""
+    from vllm_expert_pager import _native as nat
+
+    ctype_kind = {ctypes.c_void_p: "ptr", ctypes.c_char_p: "ptr", ctypes.c_int: "i32", ctypes.c_int64: "i64",
+                  ctypes.c_long: "i64", ctypes.c_double: "f64"}
+    decl = declarations()
+    assert len(decl) >= 30
+    bad = []
+    for name, (_, args) in nat._SIGNATURES.items():
+        assert name in decl, f"{name} is not declared in include/xp.h"
+        want = [_kind(p) for p in decl[name]]
+        got = [ctype_kind[a] for a in args]
+        if want != got:
+            bad.append(f"{name}: header {want}, ctypes {got}")
+    assert not bad, "\n".join(bad)
+
+
 def test_roctx_ranges_are_free_when_off(monkeypatch):
     from vllm_expert_pager import trace
 

@@ -62,28 +62,41 @@ def test_refuses_expert_and_tensor_parallelism(hook):
 class _Act(__import__("enum").Enum):
     SILU = "silu"
     GELU = "gelu"
+    GELU_TANH = "gelu_tanh"
 
 
 @pytest.mark.parametrize(
     "kw, match",
     [
-        (dict(activation="gelu"), "activation 'gelu'"),
-        (dict(activation=_Act.GELU), "activation 'gelu'"),
+        (dict(activation="gelu_tanh"), "activation 'gelu_tanh'"),
+        (dict(activation=_Act.GELU_TANH), "activation 'gelu_tanh'"),
         (dict(config_activation="swigluoai"), "activation 'swigluoai'"),
+        (dict(activation="silu", config_activation="gelu"), "different activations"),
     ],
 )
 def test_refuses_modes_the_kernels_do_not_compute(hook, kw, match):
-    """The expert FFN is this package's own (silu(gate) * up, routed weight on
-    the output, routed sum only); anything else vLLM's fused MoE would have
-    done for the reference (experts.py:594-600) is refused at construction."""
+    """The expert FFN is this package's own (silu or gelu of the gate times
+    up, routed weight on the output, routed sum only); anything else vLLM's
+    fused MoE would have done for the reference (experts.py:594-600) is
+    refused at construction."""
     with pytest.raises(RuntimeError, match=match):
         hook.ExpertPagerRoutedExperts(E, H, I, device="cpu", **kw)
     assert hook._pager is None  # refused before any tier is allocated
 
 
-def test_accepts_silu_in_any_spelling(hook):
-    for act in ("silu", "SiLU", _Act.SILU):
-        assert hook._unsupported_modes(_fake_vllm.RoutedExperts(E, H, I, device="cpu", activation=act)) == []
+@pytest.mark.parametrize("act, name", [("silu", "silu"), ("SiLU", "silu"), (_Act.SILU, "silu"),
+                                       ("gelu", "gelu"), ("GELU", "gelu"), (_Act.GELU, "gelu")])
+def test_accepts_silu_and_gelu_in_any_spelling(hook, act, name):
+    layer = _fake_vllm.RoutedExperts(E, H, I, device="cpu", activation=act)
+    assert hook._unsupported_modes(layer) == []
+    assert hook._activation(layer) == name
+
+
+def test_activation_from_the_config_alone(hook):
+    layer = _fake_vllm.RoutedExperts(E, H, I, device="cpu", activation=None, config_activation="gelu")
+    assert hook._unsupported_modes(layer) == []
+    assert hook._activation(layer) == "gelu"
+    assert hook._activation(_fake_vllm.RoutedExperts(E, H, I, device="cpu", activation=None)) == "silu"
 
 
 class _StubPager:
@@ -237,3 +250,23 @@ def test_router_weight_on_input_bit_exact(hook):
         xin = (x.float() * tw.to(torch.bfloat16).float()).to(torch.bfloat16)
         ref = moe.fused_moe(xin, torch.ones_like(tw), ids, *weights)
         assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"step {step} T={T}"
+
+
+@pytest.mark.gpu
+def test_gelu_layer_bit_exact(hook):
+    """A layer whose activation is GELU: decode and overflow shapes equal a
+    one-shot GELU run, and differ from the SiLU one (the activation reaches
+    the kernels)."""
+    from vllm_expert_pager import moe
+
+    rng = np.random.default_rng(2)
+    layer, weights = _load_layer(hook, rng, 0, activation="gelu")
+    for step, T in enumerate([1, 2, 37, 1]):
+        x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16).cuda()
+        ids = torch.from_numpy(np.stack([rng.permutation(E)[:4] for _ in range(T)])).cuda()
+        tw = torch.softmax(torch.randn((T, 4), device="cuda"), dim=1)
+        out = layer.forward_modular(x, tw, ids)
+        ref = moe.fused_moe(x, tw, ids, *weights, activation="gelu")
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"step {step} T={T}"
+        silu = moe.fused_moe(x, tw, ids, *weights)
+        assert not torch.equal(out.view(torch.int16), silu.view(torch.int16)), f"step {step} T={T}"

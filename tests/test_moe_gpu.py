@@ -6,7 +6,7 @@
 - fused_moe on exact-arithmetic inputs: bit-exact against the w8a8 oracle
   (the rounding sequence), for the prefill-sized and the decode-sized kernels.
 - fused_moe (one-shot) on random inputs: within the stated bf16 tolerance of
-  the w8a8 oracle.
+  the w8a8 oracle, SiLU and GELU experts.
 - chunked == one-shot, bit for bit: the experts run W at a time through a
   W-row slab with a per-chunk expert_map, the top-k sum once at the end
   (experts.py:455-577), at small shapes and at 2048 tokens x top-8 over 256
@@ -78,23 +78,24 @@ def _check_close(got: np.ndarray, ref: np.ndarray, what: str) -> None:
     assert ulp2 >= MIN_ULP2, f"{what}: only {ulp2:.4f} of elements within 2 bf16 ulps"
 
 
+@pytest.mark.parametrize("act", ["silu", "gelu"])
 @pytest.mark.parametrize("E, T, topk, seed", [(64, 150, 4, 0), (8, 8, 8, 108)], ids=["wide", "narrow"])
-def test_exact_inputs_bit_exact(E, T, topk, seed):
-    """On inputs where every sum is exact and every SiLU is exact or rounds to
-    bf16 unambiguously (moe_ref.exact_inputs),
+def test_exact_inputs_bit_exact(E, T, topk, seed, act):
+    """On inputs where every sum is exact and every activation is exact or
+    rounds to bf16 unambiguously (moe_ref.exact_inputs),
     the kernels' output is decided by their rounding sequence alone, and it
     equals the oracle's bit for bit, for the prefill-sized kernels (tile bound
     >= 64) and the decode-sized ones. test_oracle_moe.py shows that each
     planted mistake in the sequence changes the oracle's output on these same
     cases, so each step is pinned here."""
     moe = _moe()
-    x, tw, ids, w13, w13s, w2, w2s = M.exact_inputs(np.random.default_rng(seed), E, 512, 256, T, topk)
+    x, tw, ids, w13, w13s, w2, w2s = M.exact_inputs(np.random.default_rng(seed), E, 512, 256, T, topk, act)
     bound = _tile_bound(T * topk, E)
     assert (bound >= 64) == (E == 64)  # which kernels run
     xb = _bf16(x)
     assert torch.equal(xb.float().cpu(), torch.from_numpy(x))  # x holds bf16 values
-    out = moe.fused_moe(xb, *_dev(tw, ids, w13, w13s, w2, w2s)).float().cpu().numpy()
-    ref = M.fused_moe_ref(x, tw, ids, w13, w13s, w2, w2s)
+    out = moe.fused_moe(xb, *_dev(tw, ids, w13, w13s, w2, w2s), activation=act).float().cpu().numpy()
+    ref = M.fused_moe_ref(x, tw, ids, w13, w13s, w2, w2s, act=act)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32)), f"{int((out != ref).sum())} elements differ"
 
 
@@ -196,6 +197,21 @@ def test_fused_moe_matches_oracle(E, H, I, T, topk, seed):
     out = moe.fused_moe(xb, tw_t, ids_t, w13_t, w13s_t, w2_t, w2s_t).float().cpu().numpy()
     ref = M.fused_moe_ref(xb.float().cpu().numpy(), tw, ids, w13, w13s, w2, w2s)
     _check_close(out, ref, f"E{E} H{H} I{I} T{T} top{topk}")
+
+
+@pytest.mark.parametrize("E, H, I, T, topk", [(8, 256, 128, 37, 4), (64, 2048, 768, 40, 8), (16, 640, 384, 1000, 4)])
+def test_fused_moe_gelu_matches_oracle(E, H, I, T, topk):
+    """GELU experts on random inputs, small-batch and prefill kernels: within
+    the same tolerance of the oracle's GELU layer."""
+    moe = _moe()
+    x, tw, ids, w13, w13s, w2, w2s = _case(77 + E + T, E, H, I, T, topk)
+    xb = _bf16(x)
+    dev = _dev(tw, ids, w13, w13s, w2, w2s)
+    out = moe.fused_moe(xb, *dev, activation="gelu").float().cpu().numpy()
+    ref = M.fused_moe_ref(xb.float().cpu().numpy(), tw, ids, w13, w13s, w2, w2s, act="gelu")
+    _check_close(out, ref, f"gelu E{E} H{H} I{I} T{T} top{topk}")
+    with pytest.raises(ValueError, match="activation 'relu'"):
+        moe.fused_moe(xb, *dev, activation="relu")
 
 
 def _chunked(moe, xb, tw_t, ids_t, w13_t, w13s_t, w2_t, w2s_t, W, order):
@@ -302,10 +318,10 @@ def test_quant_route_matches_separate_calls(T, topk, E, slots):
         assert np.array_equal(a, b)
 
 
-def _separate(moe, xb, tw_t, ids_t, emap, E, slots, w):
+def _separate(moe, xb, tw_t, ids_t, emap, E, slots, w, act="silu"):
     xq, xs, r = moe.quant_route(xb, ids_t, emap, slots)
     contrib = torch.zeros((ids_t.numel(), xb.shape[1]), dtype=torch.bfloat16, device="cuda")
-    moe.run_experts(xq, xs, tw_t, *w, r, contrib)
+    moe.run_experts(xq, xs, tw_t, *w, r, contrib, act)
     return moe.topk_sum(contrib, ids_t, E)
 
 
@@ -354,6 +370,10 @@ def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits):
         assert torch.equal(got.view(torch.int16), want.view(torch.int16))
         got = moe.decode_experts(xb, tw_t, ids_t, emap_t, E, *w, slots, pair_slot=pslot_t)
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), "with pair slots"
+    gelu = _separate(moe, xb, tw_t, ids_t, emap_t, E, slots, w, "gelu")
+    got = moe.decode_experts(xb, tw_t, ids_t, emap_t, E, *w, slots, pair_slot=pslot_t, activation="gelu")
+    assert torch.equal(got.view(torch.int16), gelu.view(torch.int16)), "gelu"
+    assert not torch.equal(gelu.view(torch.int16), want.view(torch.int16))
 
 
 def test_decode_experts_in_a_graph():

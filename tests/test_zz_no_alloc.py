@@ -39,8 +39,9 @@ def _inputs(rng, E, H, I, T, topk):
     return x, tw, ids, w13, w13s, w2, w2s
 
 
-def _run(entry, x, tw, ids, w13, w13s, w2, w2s):
-    """One expert call through the C ABI; returns the (T*topk, H) bf16 contributions."""
+def _run(entry, x, tw, ids, w13, w13s, w2, w2s, act=0):
+    """One expert call through the C ABI (activation code `act`); returns the
+    (T*topk, H) bf16 contributions."""
     nat, moe = _nat()
     E, T, topk, H, I = w13.shape[0], ids.shape[0], ids.shape[1], x.shape[1], w2.shape[2]
     xq, xs = moe.quant_tokens(x)
@@ -51,18 +52,18 @@ def _run(entry, x, tw, ids, w13, w13s, w2, w2s):
     if entry == "xp_moe_experts":
         nbytes = int(nat.lib().xp_moe_workspace_bytes(T * topk, I))
         work = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
-        rc = nat.lib().xp_moe_experts(*head, work.data_ptr(), nbytes, out.data_ptr(), nat.stream())
+        rc = nat.lib().xp_moe_experts(*head, work.data_ptr(), nbytes, out.data_ptr(), act, nat.stream())
     else:
-        rc = nat.lib().xp_moe_experts_noalloc(*head, out.data_ptr(), nat.stream())
+        rc = nat.lib().xp_moe_experts_noalloc(*head, out.data_ptr(), act, nat.stream())
     assert rc == 0, nat.lib().xp_last_error()
     torch.cuda.synchronize()
     return out
 
 
-@pytest.mark.parametrize("seed", [0])
-def test_noalloc_matches_the_workspace_entry_point_twice(seed):
+@pytest.mark.parametrize("act", [0, 1], ids=["silu", "gelu"])
+def test_noalloc_matches_the_workspace_entry_point_twice(act):
     nat, _ = _nat()
-    rng = np.random.default_rng(seed)
+    rng = np.random.default_rng(act)
     E, H, I = 32, 2048, 512
     # 600 tokens x top-8 = 4800 pairs (wide kernels, 8.1 MB of workspace),
     # then 3 tokens (narrow kernels) over the array the first call filled.
@@ -70,8 +71,8 @@ def test_noalloc_matches_the_workspace_entry_point_twice(seed):
         case = _inputs(rng, E, H, I, T, 8)
         need = int(nat.lib().xp_moe_workspace_bytes(T * 8, I))
         assert need <= 32 << 20
-        want = _run("xp_moe_experts", *case)
-        got = _run("xp_moe_experts_noalloc", *case)
+        want = _run("xp_moe_experts", *case, act=act)
+        got = _run("xp_moe_experts_noalloc", *case, act=act)
         assert torch.equal(got, want), f"T={T}"
         assert int((want == -1).sum()) == 0  # every pair was written
 
@@ -83,9 +84,11 @@ def test_noalloc_refuses_a_workspace_above_its_limit():
     assert int(lib.xp_moe_workspace_bytes(T * topk, I)) > 32 << 20
     dummy = torch.zeros((16,), dtype=torch.uint8, device="cuda")
     p = dummy.data_ptr()
-    rc = lib.xp_moe_experts_noalloc(p, p, T, topk, p, H, I, p, p, p, p, E, p, p, p, p, nat.stream())
+    rc = lib.xp_moe_experts_noalloc(p, p, T, topk, p, H, I, p, p, p, p, E, p, p, p, p, 0, nat.stream())
     assert rc == nat.XP_E_LIMIT
     assert b"above the library's" in lib.xp_last_error()
+    rc = lib.xp_moe_experts_noalloc(p, p, 1, topk, p, H, I, p, p, p, p, E, p, p, p, p, 7, nat.stream())
+    assert rc == nat.XP_E_ARG and b"unknown activation 7" in lib.xp_last_error()
     torch.cuda.synchronize()
 
 

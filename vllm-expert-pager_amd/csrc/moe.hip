@@ -73,6 +73,21 @@ __device__ __forceinline__ float quant_scale(float amax) { return fmaxf(amax, kE
 
 __device__ __forceinline__ float clamp_fp8(float v) { return fminf(fmaxf(v, -kFp8Max), kFp8Max); }
 
+// a = bf16(bf16(act(g)) * u) for bf16 values g (gate) and u (up): the
+// activation in fp32 as vLLM's activation kernels compute it, returned in
+// the activation dtype (bf16), then the product of two bf16 values.
+// SiLU: g / (1 + exp(-g)); GELU: g * 0.5 * (1 + erf(g / sqrt(2))).
+template <int ACT>
+__device__ __forceinline__ float act_and_mul(float g, float u) {
+  static_assert(ACT == XP_ACT_SILU || ACT == XP_ACT_GELU, "activation");
+  float a;
+  if constexpr (ACT == XP_ACT_GELU)
+    a = g * 0.5f * (1.0f + erff(g * 0.70710678118654752f));
+  else
+    a = g / (1.0f + expf(-g));
+  return bf16_round(bf16_round(a) * u);
+}
+
 // The maximum of v over the 16 lanes of its DPP row (lanes 16r .. 16r + 15):
 // quad swaps at lane distance 1 and 2, then the half-row and row mirrors,
 // each a DPP operand of v_max, with no LDS round trip. Max is exact and
@@ -555,6 +570,7 @@ __device__ __forceinline__ AOffsets a_offsets(const int* s_row, int64_t lda, int
 // workgroup width or the tile height. Then a = bf16(bf16(silu(bf16 gate)) *
 // bf16 up) is quantised to fp8 per row over the workgroup's 128 columns, one
 // scale group. Only the 16-row subtiles that hold pairs are multiplied.
+template <int ACT>
 __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* __restrict__ xq,
                                                                const float* __restrict__ xs, int64_t H, int64_t I,
                                                                int topk, const uint8_t* __restrict__ w13,
@@ -735,8 +751,7 @@ __global__ void __launch_bounds__(kGemmWaves * 64) gemm1_kernel(const uint8_t* _
       for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float gv = bf16_round(acc[mi][0][r]), uv = bf16_round(acc[mi][1][r]);
-          const float a = bf16_round(bf16_round(gv / (1.0f + expf(-gv))) * uv);
+          const float a = act_and_mul<ACT>(bf16_round(acc[mi][0][r]), bf16_round(acc[mi][1][r]));
           acc[mi][0][r] = a;
           float m = fabsf(a);
           m = row16_max(m);
@@ -836,6 +851,7 @@ __device__ __forceinline__ void subtile_rows(const Tile& tile, int r0, const int
 // (subtile, column block) items.
 constexpr int kSplitRound = 16;  // K blocks per round, kSplitRound / 4 per wave
 
+template <int ACT>
 __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* __restrict__ xq,
                                                                 const float* __restrict__ xs, int64_t H, int64_t I,
                                                                 int topk, const uint8_t* __restrict__ w13,
@@ -920,8 +936,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
   if (wave == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
-      const float a = bf16_round(bf16_round(g / (1.0f + expf(-g))) * u);
+      const float a = act_and_mul<ACT>(bf16_round(acc[0][r]), bf16_round(acc[1][r]));
       float m = fabsf(a);
       m = row16_max(m);
       const int row = 4 * q + r;
@@ -998,6 +1013,7 @@ __device__ __forceinline__ DecodeRoute decode_route(int p, int n, const void* id
 
 // gemm1_narrow_kernel over a decode step's pairs, with their routing and the
 // quantisation of their token rows done here. Dynamic LDS: 16 x H fp8 rows.
+template <int ACT>
 __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
     const uint16_t* __restrict__ x, int64_t H, int64_t I, const void* ids, int eb, int npairs, int topk,
     const int32_t* __restrict__ expert_map, const int32_t* __restrict__ pair_slot, int E, int slots,
@@ -1152,8 +1168,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
   if (wave == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float g = bf16_round(acc[0][r]), u = bf16_round(acc[1][r]);
-      const float a = bf16_round(bf16_round(g / (1.0f + expf(-g))) * u);
+      const float a = act_and_mul<ACT>(bf16_round(acc[0][r]), bf16_round(acc[1][r]));
       float m = fabsf(a);
       m = row16_max(m);
       const int row = 4 * q + r;
@@ -1763,7 +1778,8 @@ int check_ffn(const char* what, int64_t T, int64_t topk, const float* topk_weigh
 int check_experts(const char* what, const uint8_t* xq, const float* xs, int64_t T, int64_t topk,
                   const float* topk_weight, int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale,
                   const uint8_t* w2, const float* w2_scale, int64_t slots, const int32_t* offsets,
-                  const int32_t* pairs, const int32_t* tiles, const uint16_t* out) {
+                  const int32_t* pairs, const int32_t* tiles, const uint16_t* out, int activation) {
+  XP_REQUIRE(activation == XP_ACT_SILU || activation == XP_ACT_GELU, "%s: unknown activation %d", what, activation);
   const int rc = check_ffn(what, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
                            tiles, out);
   if (rc || T == 0) return rc;
@@ -1794,7 +1810,7 @@ int cus_per_xcd(int* out) {
 int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
                    int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
                    int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, uint8_t* work,
-                   uint16_t* out, void* stream) {
+                   uint16_t* out, int act, void* stream) {
   const int64_t npairs = T * topk;
   const int64_t bound = tile_bound(npairs, slots);
   Work w;
@@ -1818,8 +1834,14 @@ int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
     const int64_t per_xcd_tiles = (wmax + 7) / 8;  // wide tiles of one XCD, at most
     // One workgroup per CU: the operand ring takes most of its LDS.
     const int64_t n1 = std::min<int64_t>(per_xcd, per_xcd_tiles * (I / (16 * kGemmWaves)));
-    hipLaunchKernelGGL(gemm1_kernel, dim3(static_cast<unsigned>(8 * n1)), dim3(64 * kGemmWaves), 0,
-                       as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, pairs, wide, wmax, npairs, w);
+    if (act == XP_ACT_GELU)
+      hipLaunchKernelGGL(gemm1_kernel<XP_ACT_GELU>, dim3(static_cast<unsigned>(8 * n1)), dim3(64 * kGemmWaves), 0,
+                         as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, pairs, wide, wmax,
+                         npairs, w);
+    else
+      hipLaunchKernelGGL(gemm1_kernel<XP_ACT_SILU>, dim3(static_cast<unsigned>(8 * n1)), dim3(64 * kGemmWaves), 0,
+                         as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, pairs, wide, wmax,
+                         npairs, w);
     rc = check_launch("gemm1_kernel");
     if (rc) return rc;
     // 256 output columns per item where H allows, else 128.
@@ -1841,8 +1863,14 @@ int launch_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   // Few pairs: 16-row subtiles x 16 columns, the K blocks split over 4 waves.
   const int64_t g1n = tiles8 * nsub * (I / 16);
   XP_REQUIRE(g1n <= INT32_MAX && nsub * g2 <= INT32_MAX, "xp_moe_experts: grid too large");
-  hipLaunchKernelGGL(gemm1_narrow_kernel, dim3(static_cast<unsigned>(g1n)), dim3(kThreads), 0, as_stream(stream), xq,
-                     xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles, nsub, w);
+  if (act == XP_ACT_GELU)
+    hipLaunchKernelGGL(gemm1_narrow_kernel<XP_ACT_GELU>, dim3(static_cast<unsigned>(g1n)), dim3(kThreads), 0,
+                       as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles,
+                       nsub, w);
+  else
+    hipLaunchKernelGGL(gemm1_narrow_kernel<XP_ACT_SILU>, dim3(static_cast<unsigned>(g1n)), dim3(kThreads), 0,
+                       as_stream(stream), xq, xs, H, I, static_cast<int>(topk), w13, w13_scale, offsets, pairs, tiles,
+                       nsub, w);
   rc = check_launch("gemm1_narrow_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(gemm2_narrow_kernel<kNarrowChunk>, dim3(static_cast<unsigned>(nsub * g2)), dim3(kThreads), 0,
@@ -1858,9 +1886,9 @@ extern "C" {
 int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight, int64_t H,
                    int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2, const float* w2_scale,
                    int64_t slots, const int32_t* offsets, const int32_t* pairs, const int32_t* tiles, void* work,
-                   int64_t work_bytes, uint16_t* out, void* stream) {
+                   int64_t work_bytes, uint16_t* out, int activation, void* stream) {
   int rc = check_experts("xp_moe_experts", xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots,
-                         offsets, pairs, tiles, out);
+                         offsets, pairs, tiles, out, activation);
   if (rc || T == 0) return rc;
   XP_REQUIRE(work && (reinterpret_cast<uintptr_t>(work) & 255) == 0,
              "xp_moe_experts: the workspace must be non-null and 256-byte aligned");
@@ -1868,15 +1896,15 @@ int xp_moe_experts(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, 
   XP_REQUIRE(work_bytes >= need, "xp_moe_experts: workspace of %lld B, needs %lld", (long long)work_bytes,
              (long long)need);
   return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
-                        tiles, static_cast<uint8_t*>(work), out, stream);
+                        tiles, static_cast<uint8_t*>(work), out, activation, stream);
 }
 
 int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T, int64_t topk, const float* topk_weight,
                            int64_t H, int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
                            const float* w2_scale, int64_t slots, const int32_t* offsets, const int32_t* pairs,
-                           const int32_t* tiles, uint16_t* out, void* stream) {
+                           const int32_t* tiles, uint16_t* out, int activation, void* stream) {
   int rc = check_experts("xp_moe_experts_noalloc", xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2,
-                         w2_scale, slots, offsets, pairs, tiles, out);
+                         w2_scale, slots, offsets, pairs, tiles, out, activation);
   if (rc || T == 0) return rc;
   const int64_t need = xp_moe_workspace_bytes(T * topk, I);
   if (need > XP_MOE_SCRATCH_BYTES)
@@ -1888,14 +1916,14 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T, int64_
   rc = moe_scratch_address(&work);
   if (rc) return rc;
   return launch_experts(xq, xs, T, topk, topk_weight, H, I, w13, w13_scale, w2, w2_scale, slots, offsets, pairs,
-                        tiles, work, out, stream);
+                        tiles, work, out, activation, stream);
 }
 
 int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* topk_ids, int topk_elem_bytes,
                           int64_t topk, const float* topk_weight, const int32_t* expert_map,
-                          const int32_t* pair_slot, int64_t num_experts, int64_t I, const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
-                          const float* w2_scale, int64_t slots, void* work, int64_t work_bytes, uint16_t* out,
-                          void* stream) {
+                          const int32_t* pair_slot, int64_t num_experts, int64_t I, const uint8_t* w13,
+                          const float* w13_scale, const uint8_t* w2, const float* w2_scale, int64_t slots, void* work,
+                          int64_t work_bytes, uint16_t* out, int activation, void* stream) {
   const char* what = "xp_moe_decode_experts";
   XP_REQUIRE(T >= 0 && topk >= 1 && T * topk <= INT32_MAX, "%s: T=%lld, topk=%lld", what, (long long)T,
              (long long)topk);
@@ -1907,6 +1935,7 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
                 what, (long long)npairs, kDecodePairs, (long long)H, kDecodeMaxH, (long long)(topk * I),
                 kDecodeActBytes);
   XP_REQUIRE(topk_elem_bytes == 4 || topk_elem_bytes == 8, "%s: id size %d", what, topk_elem_bytes);
+  XP_REQUIRE(activation == XP_ACT_SILU || activation == XP_ACT_GELU, "%s: unknown activation %d", what, activation);
   XP_REQUIRE(num_experts >= 1 && num_experts <= INT32_MAX, "%s: %lld experts", what, (long long)num_experts);
   XP_REQUIRE(H > 0 && I > 0 && H % kBN == 0 && I % kBN == 0, "%s: H=%lld and I=%lld must be multiples of %d", what,
              (long long)H, (long long)I, kBN);
@@ -1923,11 +1952,17 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
   work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
   const int64_t tiles8 = (tile_bound(npairs, slots) + 7) / 8 * 8;
   const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(static_cast<unsigned>(tiles8 * nsub * (I / 16))), dim3(kThreads),
-                     static_cast<size_t>(16 * H), as_stream(stream), x, H, I, topk_ids, topk_elem_bytes,
-                     static_cast<int>(npairs), static_cast<int>(topk), expert_map, pair_slot,
-                     static_cast<int>(num_experts),
-                     static_cast<int>(slots), w13, w13_scale, nsub, w);
+  const dim3 g1(static_cast<unsigned>(tiles8 * nsub * (I / 16)));
+  if (activation == XP_ACT_GELU)
+    hipLaunchKernelGGL(gemm1_decode_kernel<XP_ACT_GELU>, g1, dim3(kThreads), static_cast<size_t>(16 * H),
+                       as_stream(stream), x, H, I, topk_ids, topk_elem_bytes, static_cast<int>(npairs),
+                       static_cast<int>(topk), expert_map, pair_slot, static_cast<int>(num_experts),
+                       static_cast<int>(slots), w13, w13_scale, nsub, w);
+  else
+    hipLaunchKernelGGL(gemm1_decode_kernel<XP_ACT_SILU>, g1, dim3(kThreads), static_cast<size_t>(16 * H),
+                       as_stream(stream), x, H, I, topk_ids, topk_elem_bytes, static_cast<int>(npairs),
+                       static_cast<int>(topk), expert_map, pair_slot, static_cast<int>(num_experts),
+                       static_cast<int>(slots), w13, w13_scale, nsub, w);
   int rc = check_launch("gemm1_decode_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(gemm2_decode_kernel, dim3(static_cast<unsigned>(T * (H / 16))), dim3(kThreads),

@@ -124,10 +124,11 @@ _SIGNATURES = {
     "xp_moe_route": (_I, [_P, _I, _L, _L, _P, _L, _L, _P, _P, _P, _P]),
     "xp_moe_quant_route": (_I, [_P, _L, _L, _P, _P, _P, _I, _L, _P, _L, _L, _P, _P, _P, _P]),
     "xp_moe_workspace_bytes": (_L, [_L, _L]),
-    "xp_moe_experts": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _L, _P, _P]),
+    "xp_moe_experts": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _L, _P, _I, _P]),
     "xp_ssd_read_probe": (_I, [_I, _L, _P, _L, _I, _I, _P]),
-    "xp_moe_decode_experts": (_I, [_P, _L, _L, _P, _I, _L, _P, _P, _P, _L, _L, _P, _P, _P, _P, _L, _P, _L, _P, _P]),
-    "xp_moe_experts_noalloc": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P]),
+    "xp_moe_decode_experts": (_I, [_P, _L, _L, _P, _I, _L, _P, _P, _P, _L, _L, _P, _P, _P, _P, _L, _P, _L, _P, _I,
+                                   _P]),
+    "xp_moe_experts_noalloc": (_I, [_P, _P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _I, _P]),
     "xp_encode_rows": (_I, [_P, _L, _L, _L, _L, _P, _L, _P, _L, _P, _P]),
     "xp_moe_topk_sum": (_I, [_P, _L, _L, _L, _P, _I, _L, _P, _P]),
 }

@@ -17,7 +17,8 @@ and the routed sum alone is returned, the shared output staying with the
 shared experts object (experts.py:475-477). ``apply_router_weight_on_input``
 scales the tokens by their routed weight before the experts and leaves the
 outputs unweighted, as vLLM's no-EP prepare step does (top-k must be 1).
-The kernels compute ``silu(gate) * up``, so layers that ask for another
+The kernels compute ``act(gate) * up`` for act SiLU or (erf) GELU, vLLM's
+``silu_and_mul`` and ``gelu_and_mul``; layers that ask for another
 activation are refused with ``RuntimeError``. Settings are the
 ``VLLM_EXPERT_PAGER_*`` environment variables, read at import.
 
@@ -33,6 +34,7 @@ from vllm.logger import init_logger
 from vllm.model_executor.layers.fused_moe.oracle.fp8 import Fp8MoeBackend
 from vllm.model_executor.layers.fused_moe.routed_experts import RoutedExperts
 
+from vllm_expert_pager.moe import ACTIVATIONS
 from vllm_expert_pager.pager import PARAMS, SCALES, Pager, PagedExperts, Settings
 
 logger = init_logger(f"vllm.{__name__}")
@@ -53,24 +55,39 @@ def _mode_name(value) -> str:
     return str(getattr(value, "name", value)).lower()
 
 
+def _activation(layer) -> str:
+    """The layer's expert activation name: its own ``activation``, else its
+    ``moe_config``'s, else "silu" (vLLM's default)."""
+    for owner in (layer, getattr(layer, "moe_config", None)):
+        act = getattr(owner, "activation", None) if owner is not None else None
+        if act is not None:
+            return _mode_name(act)
+    return "silu"
+
+
 def _unsupported_modes(layer) -> list[str]:
     """What the layer asks of the expert FFN that csrc/moe.hip does not compute.
 
-    The kernels compute ``silu(gate) * up`` over w13's gate rows then up
-    rows. The reference leaves the activation to vLLM's fused MoE
-    (experts.py:594-600), which reads the layer's ``activation`` (on the
-    layer or its ``moe_config``). Each activation the kernels would get
-    silently wrong is listed here so construction can refuse it.
+    The kernels compute ``act(gate) * up`` over w13's gate rows then up rows,
+    for the activations in ``moe.ACTIVATIONS``. The reference leaves the
+    activation to vLLM's fused MoE (experts.py:594-600), which reads the
+    layer's ``activation`` (on the layer or its ``moe_config``). Each
+    activation the kernels would get silently wrong is listed here so
+    construction can refuse it.
     """
     found = []
     for owner in (layer, getattr(layer, "moe_config", None)):
         if owner is None:
             continue
         act = getattr(owner, "activation", None)
-        if act is not None and _mode_name(act) != "silu":
-            found.append(f"activation {_mode_name(act)!r} (the kernels compute silu(gate) * up)")
+        if act is not None and _mode_name(act) not in ACTIVATIONS:
+            found.append(f"activation {_mode_name(act)!r} (the kernels compute {' or '.join(ACTIVATIONS)})")
         if getattr(owner, "is_act_and_mul", True) is False:
             found.append("an activation without the gate/up product")
+    names = {_mode_name(getattr(o, "activation")) for o in (layer, getattr(layer, "moe_config", None))
+             if o is not None and getattr(o, "activation", None) is not None}
+    if len(names) > 1:
+        found.append(f"different activations on the layer and its config ({', '.join(sorted(names))})")
     return list(dict.fromkeys(found))
 
 
@@ -122,7 +139,7 @@ class ExpertPagerRoutedExperts(RoutedExperts):
                 intermediate=self.intermediate_size_per_partition,
                 device=params["w13_weight"].device,
             )
-        self._expert_pager: PagedExperts = _pager.add_layer()
+        self._expert_pager: PagedExperts = _pager.add_layer(_activation(self))
 
         # Compression assumes raw fp8 rows; Marlin repacks them.
         if _pager.store.compress and getattr(self.quant_method, "fp8_backend", None) == Fp8MoeBackend.MARLIN:

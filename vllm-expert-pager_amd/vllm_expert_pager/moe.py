@@ -32,6 +32,17 @@ MAX_SLOTS = 1024  # slots one route call can address
 
 _FP8 = tuple(t for t in (getattr(torch, "float8_e4m3fn", None), torch.uint8) if t is not None)
 
+# Expert activations the kernels compute (act(gate) * up), by vLLM's names.
+ACTIVATIONS = {"silu": 0, "gelu": 1}
+
+
+def activation_code(activation: str) -> int:
+    """The kernels' code of an activation name; ValueError for others."""
+    code = ACTIVATIONS.get(activation)
+    if code is None:
+        raise ValueError(f"activation {activation!r}: the expert kernels compute {sorted(ACTIVATIONS)}")
+    return code
+
 
 def _fp8_ptr(t: torch.Tensor, what: str) -> int:
     nat.require_device(t, what)
@@ -149,13 +160,17 @@ def run_experts(
     w2_scale: torch.Tensor,
     routing: Routing,
     contrib: torch.Tensor,
+    activation: str = "silu",
 ) -> None:
     """Write ``contrib[t*topk + k]`` (bf16, ``(T*topk, H)``) for every routed pair.
 
     ``w13`` is the slab ``(S, 2I, H)`` (gate rows then up rows), ``w2``
     ``(S, H, I)``, scales ``(S, 2I/128, H/128)`` and ``(S, H/128, I/128)``
     fp32. Rows of pairs that were not routed are left as they are.
+    ``activation`` ("silu" or "gelu") is applied to the gate before the
+    product with up.
     """
+    act = activation_code(activation)
     T, H = xq.shape
     if topk_weights.dim() != 2 or topk_weights.shape[0] != T:
         raise ValueError("topk_weights must be (T, topk)")
@@ -184,7 +199,7 @@ def run_experts(
         "xp_moe_experts", _fp8_ptr(xq, "xq"), _f32(xs, "xs").data_ptr(), T, topk, tw.data_ptr(), H, I,
         _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(), _fp8_ptr(w2, "w2"),
         _f32(w2_scale, "w2_scale").data_ptr(), routing.slots, routing.offsets.data_ptr(),
-        routing.pairs.data_ptr(), routing.tiles.data_ptr(), work.data_ptr(), nbytes, contrib.data_ptr(),
+        routing.pairs.data_ptr(), routing.tiles.data_ptr(), work.data_ptr(), nbytes, contrib.data_ptr(), act,
         nat.stream(),
     )
 
@@ -231,6 +246,7 @@ def decode_experts(
     w2_scale: torch.Tensor,
     slots: int,
     pair_slot: torch.Tensor | None = None,
+    activation: str = "silu",
 ) -> torch.Tensor:
     """``quant_route`` + ``run_experts`` + ``topk_sum`` of a decode step in two launches, same bits.
 
@@ -240,6 +256,7 @@ def decode_experts(
     entries), when given, holds each pair's slot as ``AcquirePair`` writes
     it, and the routing reads it instead of ``expert_map[topk_ids]``.
     """
+    act = activation_code(activation)
     nat.require_device(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2:
         raise ValueError(f"x must be a 2-D bfloat16 tensor, got {x.dtype} {tuple(x.shape)}")
@@ -266,8 +283,9 @@ def decode_experts(
     out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
     nat.call(
         "xp_moe_decode_experts", x.data_ptr(), T, H, nat.ptr(ids), eb, topk, tw.data_ptr(), expert_map.data_ptr(),
-        None if pair_slot is None else pair_slot.data_ptr(), num_experts, I, _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(), _fp8_ptr(w2, "w2"),
-        _f32(w2_scale, "w2_scale").data_ptr(), min(slots, S), work.data_ptr(), nbytes, out.data_ptr(), nat.stream(),
+        nat.ptr(pair_slot), num_experts, I, _fp8_ptr(w13, "w13"), _f32(w13_scale, "w13_scale").data_ptr(),
+        _fp8_ptr(w2, "w2"), _f32(w2_scale, "w2_scale").data_ptr(), min(slots, S), work.data_ptr(), nbytes,
+        out.data_ptr(), act, nat.stream(),
     )
     return out
 
@@ -282,6 +300,7 @@ def fused_moe(
     w2_scale: torch.Tensor,
     expert_map: torch.Tensor | None = None,
     num_experts: int | None = None,
+    activation: str = "silu",
 ) -> torch.Tensor:
     """One-shot MoE over a slab: quantise, route, experts, combine.
 
@@ -296,5 +315,5 @@ def fused_moe(
     r = route(topk_ids, expert_map, min(S, MAX_SLOTS))
     T, topk = topk_weights.shape
     contrib = torch.zeros((T * topk, x.shape[1]), dtype=torch.bfloat16, device=x.device)
-    run_experts(xq, xs, topk_weights, w13, w13_scale, w2, w2_scale, r, contrib)
+    run_experts(xq, xs, topk_weights, w13, w13_scale, w2, w2_scale, r, contrib, activation)
     return topk_sum(contrib, topk_ids, E)

@@ -132,8 +132,9 @@ class Pager:
     def close(self) -> None:
         self.store.close()
 
-    def add_layer(self) -> "PagedExperts":
-        return PagedExperts(self)
+    def add_layer(self, activation: str = "silu") -> "PagedExperts":
+        """A new layer whose experts compute ``activation(gate) * up`` ("silu" or "gelu")."""
+        return PagedExperts(self, activation)
 
     def layer_ready(self) -> None:
         """Count a layer whose weights are in; after the last one, flush the
@@ -155,8 +156,10 @@ class Pager:
 class PagedExperts:
     """One MoE layer whose expert weights live in the tiers and are staged into slabs."""
 
-    def __init__(self, pager: Pager) -> None:
+    def __init__(self, pager: Pager, activation: str = "silu") -> None:
+        moe.activation_code(activation)
         self.pager = pager
+        self.activation = activation
         self.store = pager.store
         self.layer = self.store.add_layer()
         self.calls = 0
@@ -287,7 +290,7 @@ class PagedExperts:
                 slab = self.cache_slab
                 out = moe.decode_experts(x, topk_weights, topk_ids, self.expert_map, E, slab[PARAMS[0]],
                                          slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]], self.table.num_slots,
-                                         pair_slot=self.acquire.pair_slot)
+                                         pair_slot=self.acquire.pair_slot, activation=self.activation)
                 self._log()
                 return out
             xq, xs, routing = moe.quant_route(x, topk_ids, self.expert_map, self.table.num_slots)
@@ -378,7 +381,7 @@ class PagedExperts:
         S = slab[PARAMS[0]].shape[0]
         r = routing if routing is not None else moe.route(topk_ids, self.expert_map, S)
         moe.run_experts(xq, xs, topk_weights, slab[PARAMS[0]], slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]],
-                        r, contrib)
+                        r, contrib, self.activation)
 
     # ---- counters ----
 
