@@ -158,7 +158,10 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
 
 // One symbol of one stream, without branches: every lane reads a ring word
 // at its refill address and keeps it only if it refills. s_lut holds
-// len | (symbol << 3) << 8 per 9-bit code. offs packs the LDS byte
+// len | (symbol << 3) << 8 per 9-bit code, followed by the 64-byte position
+// table: entry p is p - 32 for a position that refills (p > 63 - LIMIT),
+// else p. Reading it replaces a select and an add per symbol by one LDS
+// read issued beside the ring read. offs packs the LDS byte
 // addresses of the next unread ring word of the groups of the lower and
 // upper half-wave (low | high << 16; both below 2^16): wave-uniform, so it
 // advances in a scalar register.
@@ -168,7 +171,9 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
 // many words and one bit-field extract picks each lane's base.
 __device__ __forceinline__ uint32_t decode_symbol(uint64_t& buf, uint32_t& pos, uint32_t& offs, uint32_t half_shift,
                                                   const uint16_t* s_lut) {
-  // pos is the next bit's index minus one (see Chain::pos).
+  // pos is the next bit's index minus one (see Chain::pos); pr is the
+  // position after this symbol's refill (pos - 32 in refilling lanes).
+  const uint32_t pr = reinterpret_cast<const uint8_t*>(s_lut)[2 * XP_LUT_BYTES + pos];
   const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 63u - kLimit);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
   const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
@@ -180,7 +185,6 @@ __device__ __forceinline__ uint32_t decode_symbol(uint64_t& buf, uint32_t& pos, 
   const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
   const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
-  const uint32_t pr = pos + lane_select(mask, 0u, ~31u);  // pos - 32 in refilling lanes
   // The window's 9 bits shifted up by one: the byte offset of its 16-bit entry.
   const uint32_t e = *reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(s_lut) +
                                                           (static_cast<uint32_t>(buf >> (pr & 63u)) & (2u * XP_LUT_BYTES - 2)));
@@ -345,7 +349,7 @@ __device__ __forceinline__ void flush16(uint4 (&ob)[8], uint8_t* chunk0, int64_t
 // staging path's code is not touched by the RAM-tier one).
 template <int F, bool kFromRam>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) decode_kernel(DecodeArgs a) {
-  __shared__ uint16_t s_lut[XP_LUT_BYTES];
+  __shared__ uint16_t s_lut[XP_LUT_BYTES + 32];  // the LUT, then the 64-byte position table
   __shared__ uint32_t s_ring[kGroupsPerBlock][kRingPad];
 
   const int j = blockIdx.x / a.blocks_per_row;
@@ -378,6 +382,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   // (exponent field << 3) << 8. Lengths are clamped to [1, LIMIT], which
   // leaves a valid table as it is and keeps the refill bound (and so every
   // ring read in range) for any table.
+  if (tid < 64)
+    reinterpret_cast<uint8_t*>(s_lut)[2 * XP_LUT_BYTES + tid] = static_cast<uint8_t>(tid > 63 - kLimit ? tid - 32 : tid);
   for (int i = tid; i < XP_LUT_BYTES; i += kThreads) {
     const uint32_t ent = lut[i];
     const uint32_t len = min(max(ent & 15u, 1u), static_cast<uint32_t>(kLimit));
