@@ -325,3 +325,34 @@ def test_requests_published_together_answer_in_order(server, which, bounce):
         np.testing.assert_array_equal(server.pinned[0][16 + rep], pattern(0, 30 + rep, 0))
         assert a == b - 1
     assert server.stats()[:2] == (8, 4 * 17) and server.error() is None
+
+
+def test_one_reader_bounced_requests_back_to_back(tmp_path):
+    """One reader with bounced reads: it alternates between its two bounce
+    buffers while the copier empties them, so requests of several records
+    published back to back still land whole and answer in order; a stop with
+    reads and copies still queued waits for the copies out of the buffers it
+    frees (the sanitizer runs repeat this test)."""
+    pitches = (258 * 4096, 515 * 4096)
+    s = Server(str(tmp_path / "one.bin"), nworkers=0, which="xp", pitches=pitches)
+    s.lib.xp_ssd_test_bounce(s.h)
+    try:
+        for rep in range(3):
+            want = {}
+            seqs = []
+            for i in range(3):
+                experts = [(11 * rep + 5 * i + k) % E for k in range(5)]
+                rows = [5 * i + k for k in range(5)]
+                layer = (rep + i) % L
+                seqs.append(s.publish(layer, experts, rows))
+                want.update({row: (layer, e) for e, row in zip(experts, rows)})
+            s.wait(seqs[-1])
+            assert int(s.done[0]) == seqs[-1]
+            for row, (layer, e) in want.items():
+                for n in range(2):
+                    np.testing.assert_array_equal(s.pinned[n][row], s.expected(layer, e, n))
+        assert s.error() is None and s.stats()[:2] == (9, 45)
+        s.publish(0, list(range(8)), list(range(8)))
+        s.publish(1, list(range(8, 16)), list(range(8, 16)))
+    finally:
+        s.close()  # stops with these two still being read and copied

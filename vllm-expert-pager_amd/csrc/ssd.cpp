@@ -22,24 +22,29 @@
 //     It goes straight back to polling, so a request published while an
 //     earlier one is still being read (prefill chunks are published one
 //     ahead) starts at once.
-//   * Reader threads take tasks from the front of the queue. A record is
-//     read whole, in one preadv: the paging file's disk serves a record in
-//     about the time it serves a third of one, so reads are never split.
-//     The read goes straight into the record's pinned rows with O_DIRECT;
-//     where the pinned memory cannot be an O_DIRECT target (preadv fails
-//     with EFAULT, seen with the GPU driver's pinned allocations) it goes
-//     into the reader's aligned bounce buffer instead, and the copy into the
-//     rows is cut into chunks that are put at the front of the queue, so
-//     idle readers copy beside the one that read (non-temporal stores).
-//   * Each request counts its records down. The reader that finishes a
-//     request's last record marks it, then answers every marked request at
-//     the head of the in-flight list in seq order.
+//   * Reader threads take read tasks from a queue. A record is read whole,
+//     in one preadv: the paging file's disk serves a record in about the
+//     time it serves a third of one, so reads are never split. The read
+//     goes straight into the record's pinned rows with O_DIRECT; where the
+//     pinned memory cannot be an O_DIRECT target (preadv fails with EFAULT,
+//     seen with the GPU driver's pinned allocations) it goes into one of the
+//     reader's two aligned bounce buffers instead, and the copy into the
+//     rows is cut into chunks on a second queue. Two copier threads take
+//     those chunks, and so do idle readers (non-temporal stores), while the
+//     reader goes on to its next read in its other bounce buffer: reads and
+//     copies overlap even with one reader. A reader whose next bounce
+//     buffer is still being copied out helps with the copies first.
+//   * Each request counts its records down. The thread that completes a
+//     record (its read, or the last chunk of its copy) counts it; the one
+//     that finishes a request's last record marks it, then answers every
+//     marked request at the head of the in-flight list in seq order.
 //   * Idle readers sleep on a condition variable, and the watcher yields
 //     the CPU between polls instead of spinning on pause instructions: on a
 //     virtual machine host, pause loops exit to the hypervisor, and a
 //     watcher that spun on them served single-record requests in about
 //     twice the time of one that yields (0.78 against 0.43 ms, measured).
-//   * Time is kept per phase (queue, read, copy), and the time with any
+//   * Time is kept per phase (queue, read, copy: summed over threads, so
+//     overlapping reads and copies both count), and the time with any
 //     request in flight, for xp_ssd_phase_stats.
 //
 // Exported with the reference's C ABI (store.py:253-308).
@@ -71,6 +76,7 @@ constexpr int kHead = 2;                  // [re-publishes, give-ups]
 constexpr long kAlign = 4096;             // O_DIRECT alignment of offsets, lengths and buffers
 constexpr long kCopyChunk = 1L << 20;     // longest run of a bounce copy one thread takes
 constexpr int kMaxInFlight = 64;          // requests picked up and not yet answered
+constexpr int kCopiers = 2;               // copier threads (one copies about 6 GB/s into pinned rows)
 
 inline void cpu_relax() {
 #if defined(__x86_64__) || defined(__i386__)
@@ -122,13 +128,15 @@ struct ssd_t {
     std::atomic<bool> finished{false};
   };
 
-  // The copy chunks of one bounced record still to be done.
+  // The copy chunks of one bounced record still to be done; one per bounce
+  // buffer of a reader, which reuses the buffer once `left` is 0.
   struct CopyGroup {
     std::atomic<long> left{0};
   };
 
   // A queued task: the read of one record (group == nullptr), or one chunk
-  // of the copy of a bounced record into its row.
+  // of the copy of a bounced record into its row (req is the record's
+  // request, counted down when the group's last chunk is copied).
   struct Task {
     Request* req = nullptr;
     long layer = 0, expert = 0, row = 0;
@@ -155,9 +163,10 @@ struct ssd_t {
   std::atomic<long long> delay_ns{0};
   std::atomic<bool> direct{true};  // O_DIRECT straight into the pinned rows works
 
-  std::mutex queue_mu;  // queue, sleepers
+  std::mutex queue_mu;  // queue, copies, sleepers
   std::condition_variable queue_cv;
-  std::deque<Task> queue;
+  std::deque<Task> queue;   // reads
+  std::deque<Task> copies;  // copy chunks of bounced records
   int sleepers = 0;
 
   std::mutex answer_mu;  // in_flight, free_requests, answered, busy time and every store to `done`
@@ -176,6 +185,7 @@ struct ssd_t {
   char err[512] = {0};
 
   std::thread watcher;
+  std::vector<std::thread> copiers;
   std::vector<std::thread> readers;
 
   void fail(const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -185,11 +195,13 @@ struct ssd_t {
   bool enqueue(int64_t seq, const int64_t* slot, int64_t picked_ns);
   void watch();
   void read_loop();
-  bool next_task(Task* out);
+  void copy_loop();
+  int next_task(Task* out);
   bool take_copy(Task* out);
   void run_copy(const Task& t);
+  void help_until_copied(const CopyGroup& g);
   long preadv_full(iovec* iov, int n, off_t off, int* error);
-  void serve(const Task& t, uint8_t** bounce);
+  bool serve(const Task& t, uint8_t* (&bounce)[2], CopyGroup (&group)[2], int* cur);
 };
 
 void ssd_t::fail(const char* fmt, ...) {
@@ -334,33 +346,55 @@ void ssd_t::watch() {
   }
 }
 
-bool ssd_t::next_task(Task* out) {
+// The next task of a reader: a read if one is queued, else a copy chunk
+// (1: read, 2: copy); 0 when stopping.
+int ssd_t::next_task(Task* out) {
   std::unique_lock<std::mutex> lock(queue_mu);
-  while (queue.empty() && !stopping.load(std::memory_order_acquire)) {
+  for (;;) {
+    if (stopping.load(std::memory_order_acquire)) return 0;
+    if (!queue.empty()) {
+      *out = queue.front();
+      queue.pop_front();
+      return 1;
+    }
+    if (!copies.empty()) {
+      *out = copies.front();
+      copies.pop_front();
+      return 2;
+    }
     ++sleepers;
     queue_cv.wait(lock);
     --sleepers;
   }
-  if (stopping.load(std::memory_order_acquire)) return false;
-  *out = queue.front();
-  queue.pop_front();
-  return true;
 }
 
-// A copy chunk from the front of the queue, if one is there.
+// A copy chunk, if one is queued.
 bool ssd_t::take_copy(Task* out) {
   std::lock_guard<std::mutex> lock(queue_mu);
-  if (queue.empty() || queue.front().group == nullptr) return false;
-  *out = queue.front();
-  queue.pop_front();
+  if (copies.empty()) return false;
+  *out = copies.front();
+  copies.pop_front();
   return true;
 }
 
+// Copy one chunk; the chunk that completes its record counts the record.
 void ssd_t::run_copy(const Task& t) {
   const int64_t t0 = now_ns();
   copy_out(t.dst, t.src, static_cast<size_t>(t.bytes));
   copy_ns.fetch_add(now_ns() - t0, std::memory_order_relaxed);
-  t.group->left.fetch_sub(1, std::memory_order_acq_rel);
+  if (t.group->left.fetch_sub(1, std::memory_order_acq_rel) == 1) finish_record(t.req);
+}
+
+// Wait until a bounce buffer's chunks are all copied, copying queued chunks
+// (of any record) meanwhile.
+void ssd_t::help_until_copied(const CopyGroup& g) {
+  Task other;
+  while (g.left.load(std::memory_order_acquire) > 0) {
+    if (take_copy(&other))
+      run_copy(other);
+    else
+      cpu_relax();  // the last chunks are being copied by other threads
+  }
 }
 
 // preadv until the iovecs are full, end of file or an error; returns the
@@ -388,7 +422,10 @@ long ssd_t::preadv_full(iovec* iov, int n, off_t off, int* error) {
   return got;
 }
 
-void ssd_t::serve(const Task& t, uint8_t** bounce) {
+// Read one record into its rows. Returns true when the record is complete
+// (read straight into the rows, or failed); false when its copy out of a
+// bounce buffer was queued, whose last chunk counts the record.
+bool ssd_t::serve(const Task& t, uint8_t* (&bounce)[2], CopyGroup (&group)[2], int* cur) {
   const int64_t t0 = now_ns();
   queue_ns.fetch_add(t0 - t.queued_ns, std::memory_order_relaxed);
   const off_t off = static_cast<off_t>(t.layer * E + t.expert) * record_bytes;
@@ -404,86 +441,107 @@ void ssd_t::serve(const Task& t, uint8_t** bounce) {
       via_bounce = true;
     }
   }
+  const int b = *cur;
+  int64_t t1 = now_ns();
   if (via_bounce) {
-    if (!*bounce) {
+    help_until_copied(group[b]);  // the buffer's previous record is out
+    if (!bounce[b]) {
       void* mem = nullptr;
       if (posix_memalign(&mem, kAlign, static_cast<size_t>(record_bytes)) != 0) {
         fail("cannot allocate a %ld B read buffer", record_bytes);
-        return;
+        return true;
       }
-      *bounce = static_cast<uint8_t*>(mem);
+      bounce[b] = static_cast<uint8_t*>(mem);
     }
-    iovec one{*bounce, static_cast<size_t>(record_bytes)};
+    t1 = now_ns();
+    iovec one{bounce[b], static_cast<size_t>(record_bytes)};
     got = preadv_full(&one, 1, off, &error);
   }
-  const int64_t t1 = now_ns();
-  read_ns.fetch_add(t1 - t0, std::memory_order_relaxed);
+  read_ns.fetch_add(now_ns() - (via_bounce ? t1 : t0), std::memory_order_relaxed);
   preads.fetch_add(1, std::memory_order_relaxed);
   if (error) {
     fail("reading expert %ld of layer %ld from the paging file failed: %s", t.expert, t.layer, strerror(error));
-    return;
+    return true;
   }
   if (got != record_bytes) {
     fail("short read: %ld of %ld B of expert %ld of layer %ld", got, record_bytes, t.expert, t.layer);
-    return;
+    return true;
   }
-  if (!via_bounce) return;
+  if (!via_bounce) return true;
 
-  // Copy out of the bounce buffer: chunk 0 here, the rest at the front of
-  // the queue for idle readers (and for this one, while it waits).
+  // Queue the copy out of the bounce buffer and go on with the other one.
   std::vector<Task> chunks;
-  CopyGroup group;
   long pos = 0;
   for (int n = 0; n < names; ++n) {
     uint8_t* dst = pinned[n] + t.row * pitch[n];
     for (long at = 0; at < pitch[n]; at += kCopyChunk) {
       Task c;
-      c.group = &group;
+      c.req = t.req;
+      c.group = &group[b];
       c.dst = dst + at;
-      c.src = *bounce + pos + at;
+      c.src = bounce[b] + pos + at;
       c.bytes = pitch[n] - at < kCopyChunk ? pitch[n] - at : kCopyChunk;
       chunks.push_back(c);
     }
     pos += pitch[n];
   }
-  group.left.store(static_cast<long>(chunks.size()), std::memory_order_relaxed);
-  if (chunks.size() > 1) {
-    bool wake;
-    {
-      std::lock_guard<std::mutex> lock(queue_mu);
-      for (size_t i = chunks.size() - 1; i >= 1; --i) queue.push_front(chunks[i]);
-      wake = sleepers > 0;
-    }
-    if (wake) queue_cv.notify_all();
+  group[b].left.store(static_cast<long>(chunks.size()), std::memory_order_relaxed);
+  bool wake;
+  {
+    std::lock_guard<std::mutex> lock(queue_mu);
+    for (const Task& c : chunks) copies.push_back(c);
+    wake = sleepers > 0;
   }
-  run_copy(chunks[0]);
-  Task other;
-  while (group.left.load(std::memory_order_acquire) > 0) {
-    if (take_copy(&other))
-      run_copy(other);  // ours, or another record's
-    else
-      cpu_relax();  // the rest of ours are being copied by other readers
-  }
+  if (wake) queue_cv.notify_all();
+  *cur = b ^ 1;
+  return false;
 }
 
 void ssd_t::read_loop() {
-  uint8_t* bounce = nullptr;
+  uint8_t* bounce[2] = {nullptr, nullptr};
+  CopyGroup group[2];
+  int cur = 0;
   Task t;
-  while (next_task(&t)) {
-    if (t.group) {
+  for (;;) {
+    const int kind = next_task(&t);
+    if (kind == 0) break;
+    if (kind == 2) {
       run_copy(t);
       continue;
     }
-    serve(t, &bounce);
-    finish_record(t.req);
+    if (serve(t, bounce, group, &cur)) finish_record(t.req);
   }
-  std::free(bounce);
+  // Chunks still queued point into this reader's buffers: see them copied
+  // before the buffers go.
+  for (const CopyGroup& g : group) help_until_copied(g);
+  std::free(bounce[0]);
+  std::free(bounce[1]);
+}
+
+// A copier: copy chunks as they are queued; at stop, the ones left first.
+void ssd_t::copy_loop() {
+  std::unique_lock<std::mutex> lock(queue_mu);
+  for (;;) {
+    if (!copies.empty()) {
+      const Task c = copies.front();
+      copies.pop_front();
+      lock.unlock();
+      run_copy(c);
+      lock.lock();
+      continue;
+    }
+    if (stopping.load(std::memory_order_acquire)) return;
+    ++sleepers;
+    queue_cv.wait(lock);
+    --sleepers;
+  }
 }
 
 extern "C" {
 
 // `nworkers` + 1 reader threads serve the records (the reference's server
-// reads with itself and `nworkers` workers).
+// reads with itself and `nworkers` workers), beside the watcher and the
+// copiers.
 ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L, long E, long rows, long record_bytes,
                  int names, void** pinned, long* pitch, int nworkers) {
   if (names < 1 || names > kMaxNames || !req || !done || ring < 1 || block < 1 || nworkers < 0 || nworkers > 255 ||
@@ -518,6 +576,7 @@ ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L, l
       s->pool.emplace_back(new ssd_t::Request);
       s->free_requests.push_back(s->pool.back().get());
     }
+    for (int i = 0; i < kCopiers; ++i) s->copiers.emplace_back([s] { s->copy_loop(); });
     for (int i = 0; i < s->nreaders; ++i) s->readers.emplace_back([s] { s->read_loop(); });
     s->watcher = std::thread([s] { s->watch(); });
   } catch (...) {
@@ -527,6 +586,8 @@ ssd_t* ssd_start(int fd, void* req, void* done, long ring, long block, long L, l
     }
     s->queue_cv.notify_all();
     for (auto& t : s->readers)
+      if (t.joinable()) t.join();
+    for (auto& t : s->copiers)
       if (t.joinable()) t.join();
     delete s;
     return nullptr;
@@ -545,6 +606,8 @@ void ssd_stop(ssd_t* s) {
   s->slot_cv.notify_all();
   if (s->watcher.joinable()) s->watcher.join();
   for (auto& t : s->readers)
+    if (t.joinable()) t.join();
+  for (auto& t : s->copiers)
     if (t.joinable()) t.join();
   delete s;
 }

@@ -286,7 +286,8 @@ class Store:
         """Probe the paging file with record-sized O_DIRECT reads of random
         records from 1, 2, 4 and 8 threads (two passes in opposite orders,
         each about ``seconds`` long at 3 GB/s, the better kept), and restart
-        the server with the smallest depth within 5% of the fastest. Only
+        the server with the smallest depth within 10% of the fastest (fewer
+        reads in flight serve a decode step's single records sooner). Only
         while no request has been made: a new server starts from seq 1.
         Returns the rates (GB/s by depth), or None when nothing was done."""
         if not self._handle or self.fd_r is None:
@@ -310,7 +311,7 @@ class Store:
                     return None
                 rates[depth] = max(rates.get(depth, 0.0), count * self.record_bytes / sec.value / 1e9)
         best = max(rates.values())
-        readers = min(d for d, r in rates.items() if r >= 0.95 * best)
+        readers = min(d for d, r in rates.items() if r >= 0.9 * best)
         self.reader_probe = {str(d): round(r, 3) for d, r in sorted(rates.items())}
         if readers != self.readers:
             self._so.ssd_stop(ctypes.c_void_p(self._handle))
