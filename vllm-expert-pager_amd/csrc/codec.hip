@@ -21,6 +21,8 @@
 // to 64 VGPRs, so that 8 waves share each SIMD.
 #include "common.h"
 
+#include <type_traits>
+
 namespace xp {
 namespace {
 
@@ -97,6 +99,7 @@ struct Chain {
   uint32_t b_base, b_n, b_val0, b_val1;  // request in flight, issued at this half's start
   uint32_t ab0;      // byte address of word rp in LDS at the half's start
   uint32_t x_next;   // nibble word of the next iteration
+  uint32_t x_next1;  // and the one after it, when both are fetched an iteration ahead
   uint32_t count;    // Huffman words of the group
   uint32_t wsrc;     // byte offset in the record of the group's word li (this lane's column)
   uint32_t nib;      // byte offset in the record of this lane's first nibble word
@@ -370,6 +373,22 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   if (drow < 0 || drow >= nm.dst_rows || srow < 0 || srow >= nm.stg_rows) return;
 
   const int tid = threadIdx.x;
+  // Read from the RAM tier, a launch that expands a single row is bound by
+  // the latency of its loads over the host link, so both nibble words of an
+  // iteration are fetched an iteration ahead; with more rows the link's
+  // bandwidth is the bound, and the second word fetched at its iteration
+  // paces the requests (fetching both early made 2-8 rows 13-20% slower).
+  // The count looks at the first 256 entries of todo at most.
+  bool early = false;
+  if constexpr (kFromRam) {
+    int rows = 0;
+    const int scan = a.K < 256 ? a.K : 256;
+    for (int k = 0; k < scan && rows < 2; ++k) {
+      const int64_t ek = a.todo[k];
+      rows += ek >= 0 && ek < a.E && a.cache_row[ek] < 0;
+    }
+    early = rows <= 1 && a.K <= 256;
+  }
   // Read from the RAM tier, the name's first workgroup of the row also
   // copies the expert's scale row, which a staging gather would have moved.
   if constexpr (kFromRam) {
@@ -449,6 +468,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
     }
     ch.fe = ch.q = fill;
     ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 0, 0);
+    ch.x_next1 = early ? __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128, 0) : 0u;
   }
   __syncthreads();
 
@@ -456,34 +476,49 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   // F iterations (8F bytes) are gathered in registers and stored together
   // (see flush): lines written in 16-byte pieces far apart in time leave the
   // caches as partial writes, which cost more than the decode itself.
-  uint4 ob[F / 2];
+  // The main loop, instantiated for each nibble fetch policy (a branch
+  // inside it changed how the compiler scheduled the loads of the other).
+  auto run = [&](auto early_c) __attribute__((always_inline)) {
+    constexpr bool kEarly = decltype(early_c)::value;
+    uint4 ob[F / 2];
 #pragma unroll
-  for (int i = 0; i < F / 2; ++i) ob[i] = make_uint4(0, 0, 0, 0);
-  for (int m0 = 0; m0 < msteps; m0 += F) {
+    for (int i = 0; i < F / 2; ++i) ob[i] = make_uint4(0, 0, 0, 0);
+    for (int m0 = 0; m0 < msteps; m0 += F) {
 #pragma unroll
-    for (int u = 0; u < F; u += 2) {
-      const int m = m0 + u;
-      const uint32_t x0 = ch.x_next;
-      const uint32_t x1 = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 1), 0);
-      ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 2 < msteps ? m + 2 : m), 0);
-      uint2 o0 = nibble_template(x0), o1 = nibble_template(x1);
-      half_begin(ch, li, rrec);
-      // The next unread ring word of each half's group, packed in a scalar register.
-      uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
-      __builtin_amdgcn_wave_barrier();
-      o0.x = quad(ch, offs, half_shift, s_lut, o0.x);
-      o0.y = quad(ch, offs, half_shift, s_lut, o0.y);
-      o1.x = quad(ch, offs, half_shift, s_lut, o1.x);
-      o1.y = quad(ch, offs, half_shift, s_lut, o1.y);
-      __builtin_amdgcn_wave_barrier();
-      half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
-      ob[u >> 1] = make_uint4(o0.x, o0.y, o1.x, o1.y);
+      for (int u = 0; u < F; u += 2) {
+        const int m = m0 + u;
+        const uint32_t x0 = ch.x_next;
+        uint32_t x1;
+        if constexpr (kEarly) {
+          x1 = ch.x_next1;
+          ch.x_next1 = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 3 < msteps ? m + 3 : m + 1), 0);
+        } else {
+          x1 = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 1), 0);
+        }
+        ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 2 < msteps ? m + 2 : m), 0);
+        uint2 o0 = nibble_template(x0), o1 = nibble_template(x1);
+        half_begin(ch, li, rrec);
+        // The next unread ring word of each half's group, packed in a scalar register.
+        uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
+        __builtin_amdgcn_wave_barrier();
+        o0.x = quad(ch, offs, half_shift, s_lut, o0.x);
+        o0.y = quad(ch, offs, half_shift, s_lut, o0.y);
+        o1.x = quad(ch, offs, half_shift, s_lut, o1.x);
+        o1.y = quad(ch, offs, half_shift, s_lut, o1.y);
+        __builtin_amdgcn_wave_barrier();
+        half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
+        ob[u >> 1] = make_uint4(o0.x, o0.y, o1.x, o1.y);
+      }
+      if constexpr (F == 16)
+        flush16(ob, out_wave, a.chunk, static_cast<uint32_t>(lane), 8 * m0, valid_lo, valid_hi);
+      else
+        flush<F>(ob, out, a.chunk, li, 8 * m0, valid);
     }
-    if constexpr (F == 16)
-      flush16(ob, out_wave, a.chunk, static_cast<uint32_t>(lane), 8 * m0, valid_lo, valid_hi);
-    else
-      flush<F>(ob, out, a.chunk, li, 8 * m0, valid);
-  }
+  };
+  if (kFromRam && early)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 }
 
 }  // namespace
