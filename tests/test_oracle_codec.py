@@ -149,3 +149,26 @@ def test_host_encoder_errors():
     r2 = rows(3, n=N + 8)
     with pytest.raises(ValueError, match="not a multiple"):
         codec.encode_into(r2, np.empty(8 * N, np.uint8), np.empty(512, np.uint8), CHUNK)
+
+
+def test_host_code_matches_oracle_on_random_histograms():
+    """The native code construction (lengths by merging, length limiting,
+    canonical codes, LUT) against the oracle's on 400 random histograms:
+    ties of equal counts, zero counts, skewed ones that need the length
+    limit, and near-uniform ones."""
+    codec = _native_codec()
+    rng = np.random.default_rng(41)
+    for i in range(400):
+        kind = i % 4
+        if kind == 0:  # many ties
+            h = rng.integers(0, 4, 16) * 1000
+        elif kind == 1:  # geometric: lengths beyond the limit before limiting
+            h = (2.0 ** rng.permutation(16) * rng.integers(1, 4)).astype(np.int64)
+        elif kind == 2:  # sparse, with zeros
+            h = rng.integers(0, 10**6, 16) * (rng.random(16) < 0.4)
+        else:
+            h = rng.integers(10**5, 2 * 10**5, 16)
+        c = codec.Code([int(x) for x in h])
+        r = codec_ref.Code([int(x) for x in h])
+        assert c.lengths == list(r.lengths) and c.codes == list(r.codes) and c.lut == list(r.lut), h.tolist()
+        assert max(c.lengths) <= 9

@@ -23,39 +23,70 @@ namespace code {
 
 constexpr int kSyms = 16;
 
-// Huffman lengths of 16 weighted symbols (ties broken by node id).
+// Huffman lengths of 16 weighted symbols (ties broken by node id). Every
+// array is indexed by loop constants only (selects instead of dynamic
+// indexing), so on the GPU it stays in registers rather than scratch memory.
 __host__ __device__ inline void huffman_lengths(const double* counts, int32_t* lengths) {
   double c[kSyms];
   int id[kSyms];
   uint32_t members[kSyms];  // bit s set: symbol s is under the node
-  int n = kSyms;
+#pragma unroll
   for (int i = 0; i < kSyms; ++i) {
     c[i] = counts[i];
     id[i] = i;
     members[i] = 1u << i;
     lengths[i] = 0;
   }
-  int next_id = kSyms;
-  while (n > 1) {
+  int n = kSyms, next_id = kSyms;
+  for (int step = 0; step < kSyms - 1; ++step) {  // 16 nodes merge into one
     double pc[2];
     uint32_t pm[2];
+#pragma unroll
     for (int t = 0; t < 2; ++t) {
-      int best = 0;
-      for (int i = 1; i < n; ++i)
-        if (c[i] < c[best] || (c[i] == c[best] && id[i] < id[best])) best = i;
-      pc[t] = c[best];
-      pm[t] = members[best];
+      // The lightest of the n live nodes, the lower id on a tie.
+      int best = 0, bid = id[0];
+      double bc = c[0];
+      uint32_t bm = members[0];
+#pragma unroll
+      for (int i = 1; i < kSyms; ++i) {
+        const bool take = i < n && (c[i] < bc || (c[i] == bc && id[i] < bid));
+        best = take ? i : best;
+        bc = take ? c[i] : bc;
+        bid = take ? id[i] : bid;
+        bm = take ? members[i] : bm;
+      }
+      pc[t] = bc;
+      pm[t] = bm;
       --n;  // the last node moves into the picked one's place
-      c[best] = c[n];
-      id[best] = id[n];
-      members[best] = members[n];
+      double lc = 0.0;
+      int lid = 0;
+      uint32_t lm = 0;
+#pragma unroll
+      for (int i = 0; i < kSyms; ++i)
+        if (i == n) {
+          lc = c[i];
+          lid = id[i];
+          lm = members[i];
+        }
+#pragma unroll
+      for (int i = 0; i < kSyms; ++i)
+        if (i == best) {
+          c[i] = lc;
+          id[i] = lid;
+          members[i] = lm;
+        }
     }
     const uint32_t m = pm[0] | pm[1];
-    for (int s = 0; s < kSyms; ++s)
-      if (m & (1u << s)) ++lengths[s];
-    c[n] = pc[0] + pc[1];
-    id[n] = next_id++;
-    members[n] = m;
+#pragma unroll
+    for (int s = 0; s < kSyms; ++s) lengths[s] += static_cast<int32_t>((m >> s) & 1u);
+#pragma unroll
+    for (int i = 0; i < kSyms; ++i)
+      if (i == n) {
+        c[i] = pc[0] + pc[1];
+        id[i] = next_id;
+        members[i] = m;
+      }
+    ++next_id;
     ++n;
   }
 }
@@ -80,29 +111,34 @@ __host__ __device__ inline void code_lengths(const int64_t* hist, int32_t* lengt
   }
 }
 
-// Canonical codes in (length, symbol) order, bit-reversed.
+// Canonical codes in (length, symbol) order, bit-reversed: the first code
+// of length L is (first code of L - 1 + count of length L - 1) << 1, and
+// symbols of one length take consecutive codes in symbol order. Loop
+// constants index every array (see huffman_lengths).
 __host__ __device__ inline void canonical_codes(const int32_t* lengths, int32_t* codes) {
-  int order[kSyms];
-  for (int i = 0; i < kSyms; ++i) order[i] = i;
-  for (int i = 1; i < kSyms; ++i)  // insertion sort by (length, symbol)
-    for (int k = i; k > 0 && (lengths[order[k]] < lengths[order[k - 1]] ||
-                              (lengths[order[k]] == lengths[order[k - 1]] && order[k] < order[k - 1]));
-         --k) {
-      const int t = order[k];
-      order[k] = order[k - 1];
-      order[k - 1] = t;
-    }
-  uint32_t canon[kSyms] = {0};
-  uint32_t code = 0;
-  for (int i = 0; i < kSyms; ++i) {
-    const int s = order[i];
-    if (i) code = (code + 1) << (lengths[s] - lengths[order[i - 1]]);
-    canon[s] = code;
+  uint32_t first[XP_LIMIT + 1];
+  uint32_t code = 0, prev = 0;
+#pragma unroll
+  for (int L = 1; L <= XP_LIMIT; ++L) {
+    code = (code + prev) << 1;
+    first[L] = code;
+    prev = 0;
+#pragma unroll
+    for (int s = 0; s < kSyms; ++s) prev += lengths[s] == L ? 1u : 0u;
   }
+  first[0] = 0;
+#pragma unroll
   for (int s = 0; s < kSyms; ++s) {
+    const int L = lengths[s];
+    uint32_t canon = 0;
+#pragma unroll
+    for (int k = 1; k <= XP_LIMIT; ++k) canon = k == L ? first[k] : canon;
+#pragma unroll
+    for (int t = 0; t < s; ++t) canon += lengths[t] == L ? 1u : 0u;
     uint32_t rev = 0;
-    for (int b = 0; b < lengths[s]; ++b)
-      if (canon[s] & (1u << b)) rev |= 1u << (lengths[s] - 1 - b);
+#pragma unroll
+    for (int b = 0; b < XP_LIMIT; ++b)
+      if (b < L && (canon & (1u << b))) rev |= 1u << (L - 1 - b);
     codes[s] = static_cast<int32_t>(rev);
   }
 }

@@ -52,13 +52,18 @@ struct EncodeArgs {
   int64_t* needed;     // record bytes each row needs
 };
 
-// Lengths of the four bytes of w as a sum, from 16 4-bit lengths packed
-// in lens (symbol s in bits 4s..4s+3).
-__device__ __forceinline__ uint32_t sum_lengths4(uint32_t w, uint64_t lens) {
-  uint32_t t = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) t += static_cast<uint32_t>(lens >> (4 * ((w >> (8 * b + 3)) & 15u))) & 15u;
-  return t;
+// Lengths of the four bytes of w as a sum. lb[k] holds the code lengths of
+// symbols 4k..4k+3 as bytes. Each byte's symbol (its exponent field) selects
+// its length with byte permutes: one over symbols 0-7, one over 8-15, and a
+// third that takes each byte from the one its symbol's bit 3 names; a sum
+// of absolute byte differences against zero adds the four lengths.
+__device__ __forceinline__ uint32_t sum_lengths4(uint32_t w, const uint32_t (&lb)[4]) {
+  const uint32_t sym = (w >> 3) & 0x0f0f0f0fu;
+  const uint32_t low = sym & 0x07070707u;
+  const uint32_t a = __builtin_amdgcn_perm(lb[1], lb[0], low);  // symbols 0-7
+  const uint32_t b = __builtin_amdgcn_perm(lb[3], lb[2], low);  // symbols 8-15
+  const uint32_t pick = ((sym >> 1) & 0x04040404u) | 0x03020100u;  // byte i of a, or of b for symbols 8-15
+  return __builtin_amdgcn_sad_u8(__builtin_amdgcn_perm(b, a, pick), 0u, 0u);
 }
 
 __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a) {
@@ -75,7 +80,10 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
   const int64_t n = a.n;
   const int chunk = a.chunk, G = a.G;
 
-  // 1. Histogram of the exponent fields.
+  // 1. Histogram of the exponent fields. Each thread counts into its own
+  // LDS counters with atomic adds whose result is not returned: a plain
+  // increment is a read and a write that the next increment of the same
+  // counter must wait for, a chain of LDS round trips per byte.
   for (int s = 0; s < code::kSyms; ++s) s_hist[s][tid] = 0;
   constexpr int64_t kStep = int64_t(kPlanThreads) * 16;
   for (int64_t off0 = int64_t(tid) * 16; off0 < n; off0 += kStep * kPlanUnroll) {
@@ -90,7 +98,7 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
 #pragma unroll
       for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) ++s_hist[(w[k] >> (8 * b + 3)) & 15u][tid];
+        for (int b = 0; b < 4; ++b) atomicAdd(&s_hist[(w[k] >> (8 * b + 3)) & 15u][tid], 1u);
     }
   }
   __syncthreads();
@@ -127,8 +135,9 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
     for (int x = tid; x < XP_LUT_BYTES; x += kPlanThreads)
       lut[x] = static_cast<uint8_t>(code::lut_entry(lengths, codes, x));
   }
-  uint64_t lens = 0;
-  for (int s = 0; s < code::kSyms; ++s) lens |= static_cast<uint64_t>(s_len[s]) << (4 * s);
+  uint32_t lb[4] = {0u, 0u, 0u, 0u};  // the lengths as bytes, symbol s in byte s % 4 of lb[s / 4]
+#pragma unroll
+  for (int s = 0; s < code::kSyms; ++s) lb[s / 4] |= static_cast<uint32_t>(s_len[s]) << (8 * (s % 4));
 
   // 3. Words per chunk: (start bit of its last symbol + LIMIT - 1) / 32 + 1.
   // The chunk's 16-byte pieces are spread over consecutive threads, so each
@@ -147,10 +156,14 @@ __global__ void __launch_bounds__(kPlanThreads) encode_plan_kernel(EncodeArgs a)
     for (int u = 0; u < kPlanUnroll; ++u) {
       const int64_t off = off0 + u * kStep;
       if (off >= n) continue;
-      uint32_t bits = sum_lengths4(v[u].x, lens) + sum_lengths4(v[u].y, lens) + sum_lengths4(v[u].z, lens) +
-                      sum_lengths4(v[u].w, lens);
+      uint32_t bits = sum_lengths4(v[u].x, lb) + sum_lengths4(v[u].y, lb) + sum_lengths4(v[u].z, lb) +
+                      sum_lengths4(v[u].w, lb);
       const bool last = ((off + 16) % chunk) == 0;
-      if (last) bits -= static_cast<uint32_t>(lens >> (4 * ((v[u].w >> 27) & 15u))) & 15u;  // not the last symbol
+      if (last) {  // not the last symbol
+        const uint32_t s3 = v[u].w >> 27 & 15u;
+        const bool hi = s3 >= 8u;
+        bits -= __builtin_amdgcn_perm(hi ? lb[3] : lb[1], hi ? lb[2] : lb[0], (s3 & 7u) | 0x0c0c0c00u);
+      }
       for (int d = 1; d < per; d <<= 1) bits += __shfl_xor(bits, d, per);
       if (last)
         atomicAdd(&s_words[off / (int64_t(chunk) * XP_LANES)], static_cast<int32_t>((bits + XP_LIMIT - 1) / 32 + 1));
@@ -273,13 +286,12 @@ __global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, i
           }
         }
         if (k & 1) {  // 8 values: one nibble word, value j in bits 4j..4j+3
+          // Per byte, sign (bit 7) to bit 3 beside the mantissa (bits 0-2);
+          // then two bytes' nibbles joined and the four pairs picked.
           const uint32_t x0 = w[k - 1], x1 = w[k];
-          uint32_t nib = 0;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t byte = ((j < 4 ? x0 : x1) >> (8 * (j & 3))) & 0xffu;
-            nib |= (((byte >> 7) << 3) | (byte & 7u)) << (4 * j);
-          }
+          const uint32_t t0 = (x0 & 0x07070707u) | ((x0 >> 4) & 0x08080808u);
+          const uint32_t t1 = (x1 & 0x07070707u) | ((x1 >> 4) & 0x08080808u);
+          const uint32_t nib = __builtin_amdgcn_perm(t1 | (t1 >> 4), t0 | (t0 >> 4), 0x06040200u);
           if (live) fx[int64_t((i0 + 8 * (k >> 1)) / 8) * XP_LANES] = nib;
         }
       }
