@@ -121,6 +121,27 @@ int xp_plan_chunks(const xp_table* ram, const int64_t* before,
                    int64_t* src_row, int64_t* maps, int64_t* todo,
                    int64_t* ssd, int64_t* late, void* stream);
 
+/* The same five table operations on host memory, for tables kept in CPU
+ * tensors: the reference's ExpertTable is device-agnostic torch code whose
+ * tables also run on CPU tensors (table.py:1-9). Same arguments (minus the
+ * stream), checks and results as the entry points above, computed by
+ * sequential host code; every pointer is host memory. */
+int xp_table_acquire_host(const void* topk, int topk_elem_bytes, int64_t K,
+                          const xp_table* t, int64_t* expert_map_i64,
+                          int32_t* expert_map_i32, int64_t* slot_out,
+                          int64_t* todo);
+int xp_need_mask_host(const void* topk, int topk_elem_bytes, int64_t n,
+                      int64_t num_experts, uint8_t* need);
+int xp_pack_host(const uint8_t* mask, int64_t num_experts, int64_t* out);
+int xp_table_seed_host(const xp_table* ram, const xp_table* vram,
+                       const void* topk, int topk_elem_bytes, int64_t n,
+                       const uint8_t* need);
+int xp_plan_chunks_host(const xp_table* ram, const int64_t* before,
+                        const uint8_t* need, const int64_t* cached_row,
+                        int64_t W, int64_t ram_base, int64_t working_base,
+                        int64_t* dst_row, int64_t* src_row, int64_t* maps,
+                        int64_t* todo, int64_t* ssd, int64_t* late);
+
 /* ---- Gather (RAM tier / cache slab -> slab or staging) ---- */
 
 /* One weight name (w13 or w2) of a gather. Sizes in bytes, multiples of 16;

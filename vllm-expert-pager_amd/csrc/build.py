@@ -41,7 +41,7 @@ HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 GPU_SOURCES = ["table.hip", "gather.hip", "codec.hip", "encode.hip", "moe.hip", "scratch.hip"]
 HIP_HOST_SOURCES = ["host.cpp", "codec_host.cpp"]  # HIP runtime API or headers
-HOST_SOURCES = ["error.cpp", "ssd.cpp", "ssd_probe.cpp"]
+HOST_SOURCES = ["error.cpp", "ssd.cpp", "ssd_probe.cpp", "table_host.cpp"]
 
 
 def _run(cmd: list[str], verbose: bool) -> None:

@@ -98,6 +98,11 @@ _SIGNATURES = {
     "xp_pack": (_I, [_P, _L, _P, _P]),
     "xp_table_seed": (_I, [_P, _P, _P, _I, _L, _P, _P]),
     "xp_plan_chunks": (_I, [_P, _P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P]),
+    "xp_table_acquire_host": (_I, [_P, _I, _L, _P, _P, _P, _P, _P]),
+    "xp_need_mask_host": (_I, [_P, _I, _L, _L, _P]),
+    "xp_pack_host": (_I, [_P, _L, _P]),
+    "xp_table_seed_host": (_I, [_P, _P, _P, _I, _L, _P]),
+    "xp_plan_chunks_host": (_I, [_P, _P, _P, _P, _L, _L, _L, _P, _P, _P, _P, _P, _P]),
     "xp_gather_rows": (_I, [_P, _L, _L, _P, _P, _P, _L, _P, _I, _P, _L, _P, _P]),
     "xp_gather_set_blocks": (_I, [_I]),
     "xp_fetch_rows": (_I, [_P, _L, _L, _P, _L, _L, _P, _P]),
