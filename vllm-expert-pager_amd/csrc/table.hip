@@ -42,6 +42,7 @@ struct AcquireLds {
   int16_t occ[XP_MAX_SLOTS];      // expert_in before the update
   int16_t order[XP_MAX_SLOTS];    // order[r] = slot taken by the r-th miss
   int16_t miss_e[XP_MAX_SLOTS];   // miss_e[r] = the r-th missed expert
+  int16_t ids[XP_MAX_SLOTS];      // the step's ids, -1 where not an expert
   int wave_a[kWaves];
   int wave_b[kWaves];
 };
@@ -129,8 +130,9 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
   constexpr int kPerE = XP_MAX_EXPERTS / kThreads;
   constexpr int kPerS = XP_MAX_SLOTS / kThreads;
 
-  // Every read of the table is issued first, so the latencies overlap.
-  int64_t cur_r[kPerE], occ_r[kPerS], lu_r[kPerS];
+  // Every read of the table and of the ids is issued first, so the
+  // latencies overlap (K <= S <= XP_MAX_SLOTS: kPerS ids per thread).
+  int64_t cur_r[kPerE], occ_r[kPerS], lu_r[kPerS], id_r[kPerS];
 #pragma unroll
   for (int i = 0; i < kPerE; ++i) {
     const int e = tid + kThreads * i;
@@ -142,13 +144,24 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
     occ_r[i] = s < S ? t.expert_in[s] : -1;
     lu_r[i] = s < S ? t.last_used[s] : 0;
   }
+#pragma unroll
+  for (int i = 0; i < kPerS; ++i) {
+    const int k = tid + kThreads * i;
+    id_r[i] = k < K ? ids(k) : -1;
+  }
   const int64_t step = *t.step;
 
   for (int e = tid; e < E; e += kThreads) lds.need[e] = 0;
   __syncthreads();
-  for (int k = tid; k < K; k += kThreads) {
-    int64_t id = ids(k);
-    if (id >= 0 && id < E) lds.need[id] = 1;  // same value for duplicates
+#pragma unroll
+  for (int i = 0; i < kPerS; ++i) {
+    const int k = tid + kThreads * i;
+    if (k < K) {
+      const int64_t id = id_r[i];
+      const bool ok = id >= 0 && id < E;
+      if (ok) lds.need[id] = 1;  // same value for duplicates
+      lds.ids[k] = static_cast<int16_t>(ok ? id : -1);
+    }
   }
   __syncthreads();
 
@@ -190,15 +203,21 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
   const int M = miss_base;  // <= K <= S (checked on the host)
   __syncthreads();
 
-  // order[r] for r < M: the slot with the r-th smallest key.
-  if (M <= 32) {
-    if (tid < 64) smallest_keys_wave(lds.key, S, M, lds.order);
-  } else {
-    for (int s = tid; s < S; s += kThreads) {
-      const uint64_t mine = lds.key[s];
-      int c = 0;
-      for (int s2 = 0; s2 < S; ++s2) c += lds.key[s2] < mine ? 1 : 0;
-      if (c < M) lds.order[c] = static_cast<int16_t>(s);
+  // order[r] for r < M: the slot with the r-th smallest key. Either each
+  // slot counts the keys below its own (S broadcast LDS reads per slot, S/256
+  // slots per thread), or one wave takes M rounds of a wave-wide minimum
+  // (about 1000 clocks a round): whichever is cheaper for this S and M.
+  if (M > 0) {
+    const int per = (S + kThreads - 1) / kThreads;
+    if (M > 32 || S * per < 83 * M) {
+      for (int s = tid; s < S; s += kThreads) {
+        const uint64_t mine = lds.key[s];
+        int c = 0;
+        for (int s2 = 0; s2 < S; ++s2) c += lds.key[s2] < mine ? 1 : 0;
+        if (c < M) lds.order[c] = static_cast<int16_t>(s);
+      }
+    } else if (tid < 64) {
+      smallest_keys_wave(lds.key, S, M, lds.order);
     }
   }
   __syncthreads();
@@ -263,8 +282,8 @@ __global__ void __launch_bounds__(kThreads) acquire_pair_kernel(GlobalIds ids, i
     // one load instead of id then expert_map.
     if (pair_slot)
       for (int k = threadIdx.x; k < K; k += kThreads) {
-        const int64_t id = ids(k);
-        pair_slot[k] = id >= 0 && id < a.E ? static_cast<int32_t>(lds.fin[id]) : -1;
+        const int id = lds.ids[k];
+        pair_slot[k] = id >= 0 ? static_cast<int32_t>(lds.fin[id]) : -1;
       }
   } else {
     acquire_block(ids, K, b, nullptr, nullptr, b_slot, b_todo, true, false, lds);
