@@ -979,51 +979,56 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
 constexpr int kDecodePairs = 64;
 constexpr int kDecodeMaxH = 4096;       // 16 quantised token rows of H bytes fit in LDS
 constexpr int kDecodeActBytes = 32768;  // a token's quantised activations (topk x I) in LDS
+constexpr int kDecodeCols2 = 8;         // output columns per gemm2_decode_kernel workgroup
 
-// Pair p's routing, the lists route_kernel writes (pairs by slot, then by
-// pair index; one tile per occupied slot, since a slot holds at most 64 of
-// these pairs): its slot (-1: not routed), its position in the pair list,
-// its slot's tile index, and whether it is its slot's first pair.
+// Pair p's slot (-1: an id outside [0, E) or an expert without a slot):
+// from the acquire's per-pair slots when given, else ids then expert_map.
+__device__ __forceinline__ int decode_slot(int p, int n, const void* ids, int eb, const int32_t* __restrict__ expert_map,
+                                           const int32_t* __restrict__ pair_slot, int E, int slots) {
+  const int pc = p < n ? p : 0;  // unconditional loads; lanes past n are not routed
+  int sl;
+  if (pair_slot) {
+    sl = pair_slot[pc];
+  } else {
+    const int64_t e = load_id(ids, eb, pc);
+    sl = e >= 0 && e < E ? expert_map[e] : -1;
+  }
+  return p < n && sl >= 0 && sl < slots ? sl : -1;
+}
+
+// The step's routing as route_kernel lists it (pairs by slot, then by pair
+// index; one tile per occupied slot, since a slot holds at most 64 of these
+// pairs), computed by one wave from the pairs' slots (lane p: pair p):
+// whether lane p's pair is its slot's first, and that slot's tile index (the
+// number of occupied slots below it). The loops run over uniform pair
+// indices, so each read of another lane's slot is a readlane.
 struct DecodeRoute {
-  int slot, pos, tile;
+  int slot, tile;
   bool first;
 };
 
-__device__ __forceinline__ DecodeRoute decode_route(int p, int n, const void* ids, int eb,
-                                                    const int32_t* __restrict__ expert_map,
-                                                    const int32_t* __restrict__ pair_slot, int E, int slots) {
-  int slot = -1;
-  if (p < n) {
-    if (pair_slot) {  // each pair's slot, as the acquire wrote it: one load
-      const int sl = pair_slot[p];
-      slot = sl >= 0 && sl < slots ? sl : -1;
-    } else {
-      const int64_t e = load_id(ids, eb, p);
-      if (e >= 0 && e < E) {
-        const int sl = expert_map[e];
-        slot = sl >= 0 && sl < slots ? sl : -1;
-      }
-    }
-  }
-  int before = 0;
+__device__ __forceinline__ DecodeRoute decode_route(int slot, int n) {
+  const int lane = threadIdx.x & 63;
   bool first = slot >= 0;
   for (int q = 0; q < n; ++q) {
-    const int sq = __shfl(slot, q, 64);
-    if (slot < 0 || sq < 0) continue;
-    if (sq < slot || (sq == slot && q < p)) ++before;
-    if (sq == slot && q < p) first = false;
+    const int sq = __builtin_amdgcn_readlane(slot, q);
+    if (q < lane && sq == slot) first = false;
   }
+  const unsigned long long firsts = __ballot(first);
   int tile = 0;
   for (int q = 0; q < n; ++q) {
-    const int sq = __shfl(slot, q, 64);
-    const bool fq = __shfl(static_cast<int>(first), q, 64) != 0;
-    if (fq && sq < slot) ++tile;
+    const int sq = __builtin_amdgcn_readlane(slot, q);
+    if (((firsts >> q) & 1ull) && sq < slot) ++tile;
   }
-  return DecodeRoute{slot, before, tile, first};
+  return DecodeRoute{slot, tile, first};
 }
 
 // gemm1_narrow_kernel over a decode step's pairs, with their routing and the
 // quantisation of their token rows done here. Dynamic LDS: 16 x H fp8 rows.
+// Every wave routes the step itself (a pair per lane), so the weight rows of
+// the workgroup's slot are requested as soon as the pairs' slots arrive; the
+// token rows, requested before the slots, are quantised while the weights
+// are in flight.
 template <int ACT>
 __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
     const uint16_t* __restrict__ x, int64_t H, int64_t I, const void* ids, int eb, int npairs, int topk,
@@ -1031,89 +1036,85 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
     const uint8_t* __restrict__ w13,
     const float* __restrict__ w13_scale, int nsub, Work work) {
   constexpr int kPerWave = kSplitRound / (kThreads / 64);
+  constexpr int kPre = 4;  // token pieces per thread requested before the routing
   extern __shared__ __attribute__((aligned(16))) uint8_t s_aq[];  // [16][H] fp8 token rows
-  __shared__ int s_slot[kDecodePairs], s_pos[kDecodePairs], s_tile[kDecodePairs], s_first[kDecodePairs];
-  __shared__ int s_pairat[kDecodePairs];  // pair at each list position
-  __shared__ int s_ntiles;
   __shared__ int s_pair[16];
   __shared__ int s_arow[16];            // LDS row of each subtile row's activations
   __shared__ float s_xs[16 * kMaxKB];   // their scales [LDS row][K block]
   __shared__ float s_sw[2][kMaxKB];
   __shared__ float s_m[16];
-  __shared__ f32x4 s_part[kSplitRound][2][64];
+  // Raw products of a round: [K block][gate, up][row within the lane's
+  // 4-row group][lane], so that a wave reads its own row's values in lane
+  // order.
+  __shared__ float s_part[kSplitRound][2][4][64];
   __shared__ __attribute__((aligned(16))) uint16_t s_o[16 * 16];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(H / kKB);
 
-  // Token rows quantised as quant_tokens_kernel does (16 lanes per
-  // 128-column group, 8 values per lane) into LDS row r, by `nthreads`
-  // threads from thread `t0` (whole waves).
-  auto quant_row = [&](int r, int64_t t, int t0, int nthreads) {
-    const uint16_t* row = x + t * H;
-    for (int64_t c8 = (tid - t0) * 8; c8 < H; c8 += nthreads * 8) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(row + c8);
-      float v[8];
-      float amax = 0.f;
+  // A token piece (8 columns of token t from column c8) quantised as
+  // quant_tokens_kernel does (16 lanes per 128-column group) into LDS row r.
+  auto quant_piece = [&](const u32x4& raw, int r, int c8) {
+    float v[8];
+    float amax = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = bf16_value(raw[i] & 0xffffu);
-        v[2 * i + 1] = bf16_value(raw[i] >> 16);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = row16_max(amax);
-      const float sc = quant_scale(amax);
-      uint32_t q0 = 0, q1 = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        q0 |= to_fp8(clamp_fp8(v[i] / sc)) << (8 * i);
-        q1 |= to_fp8(clamp_fp8(v[4 + i] / sc)) << (8 * i);
-      }
-      *reinterpret_cast<uint2*>(s_aq + r * H + c8) = make_uint2(q0, q1);
-      if ((tid & 15) == 0) s_xs[r * KB + c8 / kKB] = sc;
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_value(raw[i] & 0xffffu);
+      v[2 * i + 1] = bf16_value(raw[i] >> 16);
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = row16_max(amax);
+    const float sc = quant_scale(amax);
+    uint32_t q0 = 0, q1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      q0 |= to_fp8(clamp_fp8(v[i] / sc)) << (8 * i);
+      q1 |= to_fp8(clamp_fp8(v[4 + i] / sc)) << (8 * i);
+    }
+    *reinterpret_cast<uint2*>(s_aq + r * H + c8) = make_uint2(q0, q1);
+    if ((tid & 15) == 0) s_xs[r * KB + c8 / kKB] = sc;
   };
-  // With at most 16 tokens, all their rows are quantised (by waves 1-3)
-  // while wave 0 routes; otherwise each workgroup quantises its subtile's.
+  // With at most 16 tokens, all their rows are quantised (piece i of the
+  // step: token i / (H / 8)); otherwise each workgroup quantises its
+  // subtile's rows once they are known.
   const int ntok = npairs / topk;
   const bool by_token = ntok <= 16;
-  if (wave == 0) {
-    const DecodeRoute r = decode_route(lane, npairs, ids, eb, expert_map, pair_slot, E, slots);
-    // gemm2_decode_kernel reads the pairs' slots from the workspace (the
-    // activation-scale region, which the decode path does not use).
-    if (blockIdx.x == 0 && lane < npairs) reinterpret_cast<int32_t*>(work.acts)[lane] = r.slot;
-    s_slot[lane] = r.slot;
-    s_pos[lane] = r.pos;
-    s_tile[lane] = r.tile;
-    s_first[lane] = r.first;
-    if (r.slot >= 0) s_pairat[r.pos] = lane;
-    const int nt = __popcll(__ballot(r.first));
-    if (lane == 0) s_ntiles = nt;
-  } else if (by_token) {
-    for (int t = 0; t < ntok; ++t) quant_row(t, t, 64, kThreads - 64);
+  const int nc8 = static_cast<int>(H / 8), npiece = by_token ? ntok * nc8 : 0;
+  auto piece_ptr = [&](int i) { return x + static_cast<int64_t>(i / nc8) * H + (i % nc8) * 8; };
+  u32x4 xr[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int it = tid + kThreads * i;
+    xr[i] = *reinterpret_cast<const u32x4*>(piece_ptr(it < npiece ? it : 0));
   }
-  __syncthreads();
+
+  const int slot_l = decode_slot(lane, npairs, ids, eb, expert_map, pair_slot, E, slots);
+  // gemm2_decode_kernel reads the pairs' slots from the workspace (the
+  // activation-scale region, which the decode path does not use).
+  if (blockIdx.x == 0 && wave == 0 && lane < npairs) reinterpret_cast<int32_t*>(work.acts)[lane] = slot_l;
+  const DecodeRoute rt = decode_route(slot_l, npairs);
+  const int ntiles = __popcll(__ballot(rt.first));
 
   const int ncb = static_cast<int>(I / 16);
   int ti, item;
   xcd_item(nsub * ncb, ti, item);
-  if (ti >= s_ntiles) return;
-  int slot = -1, first = 0, count = 0;
-  for (int p = 0; p < npairs; ++p) {
-    if (s_first[p] && s_tile[p] == ti) {
-      slot = s_slot[p];
-      first = s_pos[p];
-    }
-  }
-  for (int p = 0; p < npairs; ++p) count += s_slot[p] == slot;
+  if (ti >= ntiles) return;  // the same in every wave
+  const unsigned long long lead = __ballot(rt.first && rt.tile == ti);
+  const int slot = __builtin_amdgcn_readlane(slot_l, __ffsll(static_cast<long long>(lead)) - 1);
+  const unsigned long long mine = __ballot(slot_l == slot);
+  const int count = __popcll(mine);
   const int sub = item / ncb, r0 = 16 * sub;
   if (r0 >= count) return;
   const int c0 = (item - sub * ncb) * 16;
   const int nrow = count - r0 < 16 ? count - r0 : 16;
 
-  // The first round's weight rows depend on the slot alone.
+  // The slot's gate and up scales, then its weight rows, requested at once.
+  const float* sg = w13_scale + (static_cast<int64_t>(slot) * (2 * I / kKB) + c0 / kKB) * KB;
+  const float* su = w13_scale + (static_cast<int64_t>(slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
+  const int si = tid < 2 * KB ? tid : 0;
+  const float sw = (si < KB ? sg : su)[si < KB ? si : si - KB];
   const uint8_t* wslot = w13 + static_cast<int64_t>(slot) * 2 * I * H;
   const int64_t n = c0 + j;
   const uint8_t* const brow[2] = {wslot + n * H + 32 * q, wslot + (I + n) * H + 32 * q};
@@ -1121,22 +1122,41 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
   KBlock c[kPerWave];
   load_chunk_b<kPerWave>(c, brow, kw0, KB);
 
-  if (tid < 16) s_pair[tid] = tid < nrow ? s_pairat[first + r0 + tid] : -1;
-  {
-    const float* sg = w13_scale + (static_cast<int64_t>(slot) * (2 * I / kKB) + c0 / kKB) * KB;
-    const float* su = w13_scale + (static_cast<int64_t>(slot) * (2 * I / kKB) + (I + c0) / kKB) * KB;
-    for (int i = tid; i < 2 * KB; i += kThreads) s_sw[i / KB][i % KB] = (i < KB ? sg : su)[i % KB];
+  // Token rows into LDS while the weights are in flight.
+  if (by_token) {
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) {
+      const int it = tid + kThreads * i;
+      if (it < npiece) quant_piece(xr[i], it / nc8, (it % nc8) * 8);  // whole 16-lane groups
+    }
+    for (int it = tid + kThreads * kPre; it < npiece; it += kThreads)
+      quant_piece(*reinterpret_cast<const u32x4*>(piece_ptr(it)), it / nc8, (it % nc8) * 8);
   }
-  __syncthreads();  // s_pair
-  if (!by_token)
-    for (int r = 0; r < nrow; ++r) quant_row(r, s_pair[r] / topk, 0, kThreads);
-  // The LDS row each subtile row reads (rows past nrow, whose outputs are
-  // not stored, read the first row's).
-  if (tid < 16) {
-    const int rr = tid < nrow ? tid : 0;
-    s_arow[tid] = by_token ? s_pair[rr] / topk : rr;
+  if (tid < 2 * KB) s_sw[tid / KB][tid % KB] = sw;
+  // The subtile's rows: the slot's pairs in pair order, rows r0 .. r0 + 15;
+  // rows past nrow (outputs not stored) read the subtile's first row.
+  if (wave == 0) {
+    const int rk = static_cast<int>(lane_prefix(mine));
+    const bool in_sub = slot_l == slot && rk >= r0 && rk < r0 + 16;
+    const int lead_row = __ffsll(static_cast<long long>(__ballot(slot_l == slot && rk == r0))) - 1;
+    if (lane < 16) {
+      s_pair[lane] = -1;
+      s_arow[lane] = by_token ? lead_row / topk : 0;
+    }
+    if (in_sub) {
+      s_pair[rk - r0] = lane;
+      s_arow[rk - r0] = by_token ? lane / topk : rk - r0;
+    }
   }
-  __syncthreads();  // s_aq, s_xs, s_arow, s_pair, s_sw
+  __syncthreads();  // s_aq, s_xs, s_sw, s_pair, s_arow
+  if (!by_token) {
+    for (int r = 0; r < nrow; ++r) {
+      const uint16_t* row = x + static_cast<int64_t>(s_pair[r] / topk) * H;
+      for (int c8 = tid * 8; c8 < H; c8 += kThreads * 8)
+        quant_piece(*reinterpret_cast<const u32x4*>(row + c8), r, c8);
+    }
+    __syncthreads();
+  }
 
   const uint8_t* arow = s_aq + s_arow[j] * H + 32 * q;
   auto load_a = [&](int kb0) {
@@ -1147,7 +1167,11 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
       c[i].a[1] = *reinterpret_cast<const u32x4*>(arow + kb * kKB + 16);
     }
   };
-  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // wave 0's sums
+  // Wave w scales and sums row 4q + w of the lane's 4-row group (gate and
+  // up) in K order, one FMA per block, as gemm1_kernel does.
+  const int row = 4 * q + wave;
+  const int ar = s_arow[row];
+  float acc_g = 0.f, acc_u = 0.f;
   for (int k0 = 0; k0 < KB; k0 += kSplitRound) {
     const int kw = k0 + kw0;
     if (k0 > 0) load_chunk_b<kPerWave>(c, brow, kw, KB);
@@ -1155,53 +1179,56 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
 #pragma unroll
     for (int i = 0; i < kPerWave; ++i) {
       if (kw + i >= KB) continue;
-      s_part[wave * kPerWave + i][0][lane] = mfma_k128(c[i].a, c[i].b[0]);
-      s_part[wave * kPerWave + i][1][lane] = mfma_k128(c[i].a, c[i].b[1]);
+      const f32x4 pg = mfma_k128(c[i].a, c[i].b[0]), pu = mfma_k128(c[i].a, c[i].b[1]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s_part[wave * kPerWave + i][0][r][lane] = pg[r];
+        s_part[wave * kPerWave + i][1][r][lane] = pu[r];
+      }
     }
     __syncthreads();
-    if (wave == 0) {
-      const int nk = KB - k0 < kSplitRound ? KB - k0 : kSplitRound;
-      for (int t = 0; t < nk; ++t) {
-        const int kb = k0 + t;
-        const float g = s_sw[0][kb], u = s_sw[1][kb];
-        const f32x4 pg = s_part[t][0][lane], pu = s_part[t][1][lane];
+    // Row `wave` of the lane's group: fixed offsets from one address, and
+    // the whole round unrolled, so every LDS read of the sum is in flight
+    // before the FMAs that consume it.
+    const float* sp = &s_part[0][0][wave][lane];
+    const float* sx = s_xs + ar * KB + k0;
+    auto sum_block = [&](int t) {
+      const float sa = sx[t];
+      acc_g = fmaf(sp[(2 * t) * 256], sa * s_sw[0][k0 + t], acc_g);
+      acc_u = fmaf(sp[(2 * t + 1) * 256], sa * s_sw[1][k0 + t], acc_u);
+    };
+    if (KB - k0 >= kSplitRound) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float sa = s_xs[s_arow[4 * q + r] * KB + kb];
-          acc[0][r] = fmaf(pg[r], sa * g, acc[0][r]);
-          acc[1][r] = fmaf(pu[r], sa * u, acc[1][r]);
-        }
-      }
+      for (int t = 0; t < kSplitRound; ++t) sum_block(t);
+    } else {
+      for (int t = 0; t < KB - k0; ++t) sum_block(t);
     }
     __syncthreads();  // s_part is rewritten by the next round
   }
 
-  if (wave == 0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float a = act_and_mul<ACT>(bf16_round(acc[0][r]), bf16_round(acc[1][r]));
-      float m = fabsf(a);
-      m = row16_max(m);
-      const int row = 4 * q + r;
-      if (j == 0) s_m[row] = m;
-      s_o[row * 16 + j] = static_cast<uint16_t>(bf16_bits(a));
-    }
+  {
+    const float a = act_and_mul<ACT>(bf16_round(acc_g), bf16_round(acc_u));
+    const float m = row16_max(fabsf(a));
+    if (j == 0) s_m[row] = m;
+    s_o[row * 16 + j] = static_cast<uint16_t>(bf16_bits(a));
   }
   __syncthreads();
   if (tid < 16) {
     const int p = s_pair[tid];
     if (p >= 0) work.amax16[static_cast<int64_t>(p) * (I / 16) + c0 / 16] = s_m[tid];
   } else if (tid < 48) {  // 16 rows x 2 pieces of 16 bytes
-    const int row = (tid - 16) >> 1, piece = tid & 1;
-    const int p = s_pair[row];
+    const int rr = (tid - 16) >> 1, piece = tid & 1;
+    const int p = s_pair[rr];
     if (p >= 0)
       *reinterpret_cast<u32x4*>(work.a16 + static_cast<int64_t>(p) * I + c0 + piece * 8) =
-          *reinterpret_cast<const u32x4*>(s_o + row * 16 + piece * 8);
+          *reinterpret_cast<const u32x4*>(s_o + rr * 16 + piece * 8);
   }
 }
 
-// gemm2 of a decode step with the top-k sum: one workgroup per (token, 16
-// output columns). Its waves take the token's pairs two at a time (wave w:
+// gemm2 of a decode step with the top-k sum: one workgroup per (token, 8
+// output columns), so that a single token spreads its weight rows over 256
+// workgroups; lanes j and j + 8 of the MFMA operand read the same row (one
+// request), and columns 8-15 of the product are not used. Its waves take the token's pairs two at a time (wave w:
 // pairs w and w + 4, then w + 8 and w + 12, ...); each pair's 16 contributions are computed as
 // gemm2_narrow_kernel computes them (the token's quantised activation row as
 // every row of the MFMA operand, kNarrowChunk K blocks of weight rows per
@@ -1211,36 +1238,101 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
 // gemm1_decode_kernel's routing through the workspace, one load instead of
 // the ids and expert_map lookups. Pairs whose id is outside [0, E) add
 // nothing; so do pairs without a slot (the separate calls would read a
-// contribution never written).
+// contribution never written). The slots, the routed weights and the first
+// activation pieces are requested first, then each wave's first two pairs'
+// weight rows, and the activations are quantised while those are in flight.
 __global__ void __launch_bounds__(kThreads) gemm2_decode_kernel(
     int64_t H, int64_t I, int topk, const float* __restrict__ topk_weight, const uint8_t* __restrict__ w2,
     const float* __restrict__ w2_scale, Work work, uint16_t* __restrict__ out) {
+  constexpr int NWAVE = kThreads / 64;
+  constexpr int kPre = 2;  // activation pieces per thread requested before the weights
   extern __shared__ __attribute__((aligned(16))) uint8_t s_act[];  // [topk][I] fp8 activations
   __shared__ int s_slot[kDecodePairs];
   __shared__ float s_as[kDecodePairs * 4];  // activation scales [pair][K block], K blocks of a round
-  __shared__ uint16_t s_c[kDecodePairs][16];
+  __shared__ uint16_t s_c[kDecodePairs][kDecodeCols2];
 
-  const int ncol = static_cast<int>(H / 16);
-  const int t = static_cast<int>(blockIdx.x) / ncol, n0 = (static_cast<int>(blockIdx.x) - t * ncol) * 16;
+  const int ncol = static_cast<int>(H / kDecodeCols2);
+  const int t = static_cast<int>(blockIdx.x) / ncol;
+  const int n0 = (static_cast<int>(blockIdx.x) - t * ncol) * kDecodeCols2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const int KB = static_cast<int>(I / kKB);
   const int64_t p0 = static_cast<int64_t>(t) * topk;
+  const int nc8 = static_cast<int>(I / 8), npiece = topk * nc8;
 
-  // The pairs' slots as gemm1_decode_kernel routed them (-1: an invalid id
-  // or an expert without a slot, which adds nothing).
-  if (tid < topk) s_slot[tid] = reinterpret_cast<const int32_t*>(work.acts)[p0 + tid];
-  // The pairs' activations quantised into LDS, 8 columns per item, as
-  // gemm2_narrow_kernel quantises them (a 128-column group's scale from its
-  // eight 16-column maxima).
-  for (int i = tid; i < topk * static_cast<int>(I / 8); i += kThreads) {
-    const int k = i / static_cast<int>(I / 8), c8 = (i - k * static_cast<int>(I / 8)) * 8, g = c8 / kKB;
-    const int64_t p = p0 + k;
-    const float* m = work.amax16 + p * (I / 16) + 8 * g;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c8);
-    float mx = m[0];
+  // Requests: the pairs' slots as gemm1_decode_kernel routed them (-1: an
+  // invalid id or an expert without a slot), the wave's first two pairs'
+  // slots and routed weights, and the first activation pieces (8 columns of
+  // pair k's bf16 row with the eight 16-column maxima of its group).
+  const int32_t* pslot = reinterpret_cast<const int32_t*>(work.acts) + p0;
+  const int my_slot = pslot[tid < topk ? tid : 0];
+  int kk0[2] = {wave, wave + NWAVE};
+  int slot0[2];
+  float tw0[2];
 #pragma unroll
-    for (int u = 1; u < 8; ++u) mx = fmaxf(mx, m[u]);
+  for (int h = 0; h < 2; ++h) {
+    const int kc = kk0[h] < topk ? kk0[h] : 0;
+    slot0[h] = pslot[kc];
+    tw0[h] = topk_weight[p0 + kc];
+  }
+  auto piece_at = [&](int it, int& k, int& c8) {
+    k = it / nc8;
+    c8 = (it - k * nc8) * 8;
+  };
+  u32x4 av[kPre], am[kPre][2];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int it = tid + kThreads * i;
+    int k, c8;
+    piece_at(it < npiece ? it : 0, k, c8);
+    const int64_t p = p0 + k;
+    av[i] = *reinterpret_cast<const u32x4*>(work.a16 + p * I + c8);
+    const float* m = work.amax16 + p * (I / 16) + 8 * (c8 / kKB);
+    am[i][0] = *reinterpret_cast<const u32x4*>(m);
+    am[i][1] = *reinterpret_cast<const u32x4*>(m + 4);
+  }
+
+  // A pair's weight rows for output columns n0 .. n0 + 7 and their scales.
+  auto pair_rows = [&](int slot, const uint8_t*& brow, const float*& sw) {
+    const int sl = slot < 0 ? 0 : slot;
+    brow = w2 + static_cast<int64_t>(sl) * H * I + static_cast<int64_t>(n0 + (j & (kDecodeCols2 - 1))) * I + 32 * q;
+    sw = w2_scale + (static_cast<int64_t>(sl) * (H / kKB) + n0 / kKB) * KB;
+  };
+  // A chunk's weight rows of two pairs, with their K blocks' scales.
+  auto load_rows = [&](const int (&slot)[2], const uint8_t* const (&brow)[2], const float* const (&sw)[2], int k0,
+                       u32x4 (&b)[2][kNarrowChunk][2], float (&wsc)[2][kNarrowChunk]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (slot[h] < 0) continue;  // uniform
+#pragma unroll
+      for (int i = 0; i < kNarrowChunk; ++i) {
+        const int kb = k0 + i < KB ? k0 + i : KB - 1;
+        wsc[h][i] = sw[h][kb];
+        load32(brow[h] + kb * kKB, b[h][i]);
+      }
+    }
+  };
+#pragma unroll
+  for (int h = 0; h < 2; ++h) slot0[h] = kk0[h] < topk ? slot0[h] : -1;
+  const uint8_t* brow0[2];
+  const float* sw0[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) pair_rows(slot0[h], brow0[h], sw0[h]);
+  u32x4 b0[2][kNarrowChunk][2];
+  float wsc0[2][kNarrowChunk];
+  load_rows(slot0, brow0, sw0, 0, b0, wsc0);
+
+  // The activations quantised into LDS as gemm2_narrow_kernel quantises them
+  // (a 128-column group's scale from its eight 16-column maxima).
+  auto quant_piece = [&](const u32x4& v, const u32x4 (&mm)[2], int it) {
+    int k, c8;
+    piece_at(it, k, c8);
+    const int g = c8 / kKB;
+    float mx = __uint_as_float(mm[0][0]);
+#pragma unroll
+    for (int u = 1; u < 4; ++u) mx = fmaxf(mx, __uint_as_float(mm[0][u]));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mx = fmaxf(mx, __uint_as_float(mm[1][u]));
     const float sc = quant_scale(mx);
     if (c8 % kKB == 0 && g < 4) s_as[k * 4 + g] = sc;
     uint32_t q0 = 0, q1 = 0;
@@ -1252,73 +1344,135 @@ __global__ void __launch_bounds__(kThreads) gemm2_decode_kernel(
       q1 |= to_fp8(clamp_fp8(bf16_value(v[2 + u] >> 16) / sc)) << (16 * u + 8);
     }
     *reinterpret_cast<uint2*>(s_act + k * I + c8) = make_uint2(q0, q1);
+  };
+  if (tid < topk) s_slot[tid] = my_slot;
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int it = tid + kThreads * i;
+    if (it < npiece) quant_piece(av[i], am[i], it);
+  }
+  for (int it = tid + kThreads * kPre; it < npiece; it += kThreads) {
+    int k, c8;
+    piece_at(it, k, c8);
+    const int64_t p = p0 + k;
+    const float* m = work.amax16 + p * (I / 16) + 8 * (c8 / kKB);
+    const u32x4 mm[2] = {*reinterpret_cast<const u32x4*>(m), *reinterpret_cast<const u32x4*>(m + 4)};
+    quant_piece(*reinterpret_cast<const u32x4*>(work.a16 + p * I + c8), mm, it);
   }
   __syncthreads();
 
-  // Two pairs per wave at a time (k and k + 4), their weight rows requested
-  // together.
-  constexpr int NWAVE = kThreads / 64;
-  for (int k = wave; k < topk; k += 2 * NWAVE) {
+  // One chunk of K blocks of two pairs: their 16 columns scaled and summed
+  // in K order in fp32 (row 0 of the product, lanes q = 0, is the pair's
+  // value).
+  auto mul_chunk = [&](const u32x4 (&b)[2][kNarrowChunk][2], const float (&wsc)[2][kNarrowChunk],
+                       const int (&kk)[2], const int (&slot)[2], int k0, float (&acc)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (slot[h] < 0) continue;
+      const int64_t p = p0 + kk[h];
+      const uint8_t* arow = s_act + kk[h] * I + 32 * q;
+      if (k0 + kNarrowChunk <= KB && k0 + kNarrowChunk <= 4) {
+        // A whole chunk whose activation scales are all in LDS: every LDS
+        // read first, then the products, in K order.
+        u32x4 a[kNarrowChunk][2];
+        float sa[kNarrowChunk];
+#pragma unroll
+        for (int i = 0; i < kNarrowChunk; ++i) {
+          a[i][0] = *reinterpret_cast<const u32x4*>(arow + (k0 + i) * kKB);
+          a[i][1] = *reinterpret_cast<const u32x4*>(arow + (k0 + i) * kKB + 16);
+          sa[i] = s_as[kk[h] * 4 + k0 + i];
+        }
+#pragma unroll
+        for (int i = 0; i < kNarrowChunk; ++i) {
+          const f32x4 part = mfma_k128(a[i], b[h][i]);
+          acc[h] = fmaf(part[0], sa[i] * wsc[h][i], acc[h]);
+        }
+        continue;
+      }
+#pragma unroll
+      for (int i = 0; i < kNarrowChunk; ++i) {
+        const int kb = k0 + i;
+        if (kb >= KB) continue;
+        u32x4 a[2];
+        a[0] = *reinterpret_cast<const u32x4*>(arow + kb * kKB);
+        a[1] = *reinterpret_cast<const u32x4*>(arow + kb * kKB + 16);
+        // the pair's activation scale for this K block: from LDS for the
+        // first four blocks, else recomputed from the maxima
+        float sa;
+        if (kb < 4) {
+          sa = s_as[kk[h] * 4 + kb];
+        } else {
+          const float* m = work.amax16 + p * (I / 16) + 8 * kb;
+          float mx = m[0];
+#pragma unroll
+          for (int u = 1; u < 8; ++u) mx = fmaxf(mx, m[u]);
+          sa = quant_scale(mx);
+        }
+        const f32x4 part = mfma_k128(a, b[h][i]);
+        acc[h] = fmaf(part[0], sa * wsc[h][i], acc[h]);
+      }
+    }
+  };
+  auto finish = [&](const int (&kk)[2], const int (&slot)[2], const float (&acc)[2], const float (&tw)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (kk[h] >= topk || q != 0 || j >= kDecodeCols2) continue;
+      s_c[kk[h]][j] = slot[h] < 0 ? 0 : static_cast<uint16_t>(bf16_bits(acc[h] * tw[h]));
+    }
+  };
+
+  // The wave's first two pairs, their first chunk already loaded.
+  {
+    float acc[2] = {0.f, 0.f};
+    mul_chunk(b0, wsc0, kk0, slot0, 0, acc);
+    for (int k0 = kNarrowChunk; k0 < KB; k0 += kNarrowChunk) {
+      u32x4 b[2][kNarrowChunk][2];
+      float wsc[2][kNarrowChunk];
+      load_rows(slot0, brow0, sw0, k0, b, wsc);
+      mul_chunk(b, wsc, kk0, slot0, k0, acc);
+    }
+    finish(kk0, slot0, acc, tw0);
+  }
+  // Further pairs (top-k above 2 x 4 waves), two at a time.
+  for (int k = wave + 2 * NWAVE; k < topk; k += 2 * NWAVE) {
     const int kk[2] = {k, k + NWAVE};
     int slot[2];
+    float tw[2];
     const uint8_t* brow[2];
     const float* sw[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       slot[h] = kk[h] < topk ? s_slot[kk[h]] : -1;
-      const int sl = slot[h] < 0 ? 0 : slot[h];
-      brow[h] = w2 + static_cast<int64_t>(sl) * H * I + static_cast<int64_t>(n0 + j) * I + 32 * q;
-      sw[h] = w2_scale + (static_cast<int64_t>(sl) * (H / kKB) + n0 / kKB) * KB;
+      tw[h] = kk[h] < topk ? topk_weight[p0 + kk[h]] : 0.f;
+      pair_rows(slot[h], brow[h], sw[h]);
     }
-    float acc[2] = {0.f, 0.f};  // row 0 (lanes q = 0, r = 0) is the pair's value
+    float acc[2] = {0.f, 0.f};
     for (int k0 = 0; k0 < KB; k0 += kNarrowChunk) {
       u32x4 b[2][kNarrowChunk][2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (slot[h] < 0) continue;
-#pragma unroll
-        for (int i = 0; i < kNarrowChunk; ++i) load32(brow[h] + (k0 + i < KB ? k0 + i : KB - 1) * kKB, b[h][i]);
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (slot[h] < 0) continue;
-        const int64_t p = p0 + kk[h];
-        const uint8_t* arow = s_act + kk[h] * I + 32 * q;
-#pragma unroll
-        for (int i = 0; i < kNarrowChunk; ++i) {
-          const int kb = k0 + i;
-          if (kb >= KB) continue;
-          u32x4 a[2];
-          a[0] = *reinterpret_cast<const u32x4*>(arow + kb * kKB);
-          a[1] = *reinterpret_cast<const u32x4*>(arow + kb * kKB + 16);
-          // the pair's activation scale for this K block: from LDS for the
-          // first four blocks, else recomputed from the maxima
-          float sa;
-          if (kb < 4) {
-            sa = s_as[kk[h] * 4 + kb];
-          } else {
-            const float* m = work.amax16 + p * (I / 16) + 8 * kb;
-            float mx = m[0];
-#pragma unroll
-            for (int u = 1; u < 8; ++u) mx = fmaxf(mx, m[u]);
-            sa = quant_scale(mx);
-          }
-          const f32x4 part = mfma_k128(a, b[h][i]);
-          acc[h] = fmaf(part[0], sa * sw[h][kb], acc[h]);
-        }
-      }
+      float wsc[2][kNarrowChunk];
+      load_rows(slot, brow, sw, k0, b, wsc);
+      mul_chunk(b, wsc, kk, slot, k0, acc);
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (kk[h] >= topk || q != 0) continue;
-      s_c[kk[h]][j] = slot[h] < 0 ? 0 : static_cast<uint16_t>(bf16_bits(acc[h] * topk_weight[p0 + kk[h]]));
-    }
+    finish(kk, slot, acc, tw);
   }
   __syncthreads();
-  if (tid < 16) {
+  if (tid < kDecodeCols2) {
+    // The token's contributions in k order, eight LDS reads in flight at a
+    // time.
     float sum = 0.f;
-    for (int k = 0; k < topk; ++k)
-      if (s_slot[k] >= 0) sum += bf16_value(s_c[k][tid]);
+    for (int k0 = 0; k0 < topk; k0 += 8) {
+      int sl[8];
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + u < topk ? k0 + u : topk - 1;
+        sl[u] = s_slot[k];
+        v[u] = bf16_value(s_c[k][tid]);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < topk && sl[u] >= 0) sum += v[u];
+    }
     out[static_cast<int64_t>(t) * H + n0 + tid] = static_cast<uint16_t>(bf16_bits(sum));
   }
 }
@@ -1961,7 +2115,8 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
   XP_REQUIRE(work_bytes >= need, "%s: workspace of %lld B, needs %lld", what, (long long)work_bytes, (long long)need);
   Work w;
   work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
-  const int64_t tiles8 = (tile_bound(npairs, slots) + 7) / 8 * 8;
+  // A tile per occupied slot: at most min(npairs, slots) of them.
+  const int64_t tiles8 = ((npairs < slots ? npairs : slots) + 7) / 8 * 8;
   const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
   const dim3 g1(static_cast<unsigned>(tiles8 * nsub * (I / 16)));
   if (activation == XP_ACT_GELU)
@@ -1976,7 +2131,7 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
                        static_cast<int>(slots), w13, w13_scale, nsub, w);
   int rc = check_launch("gemm1_decode_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(static_cast<unsigned>(T * (H / 16))), dim3(kThreads),
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(static_cast<unsigned>(T * (H / kDecodeCols2))), dim3(kThreads),
                      static_cast<size_t>(topk * I), as_stream(stream), H, I, static_cast<int>(topk), topk_weight,
                      w2, w2_scale, w, out);
   return check_launch("gemm2_decode_kernel");
