@@ -330,7 +330,9 @@ def _separate(moe, xb, tw_t, ids_t, emap, E, slots, w, act="silu"):
     [(1, 8, 256, 32, 2048, 512, 64), (5, 8, 64, 64, 2048, 512, 32), (8, 8, 256, 200, 2048, 512, 64),
      (3, 4, 12, 12, 256, 128, 32), (16, 4, 32, 32, 640, 1024, 64),
      # more than 16 tokens: each workgroup quantises its own subtile's rows
-     (32, 2, 40, 40, 384, 256, 64)],
+     (32, 2, 40, 40, 384, 256, 64),
+     # H = 4096: two rounds of 16 K blocks in the gate/up launch
+     (2, 8, 16, 16, 4096, 256, 32)],
 )
 def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits):
     """The two-launch decode FFN (routing and quantisation inside gate/up, each
