@@ -150,6 +150,13 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
     id_r[i] = k < K ? ids(k) : -1;
   }
   const int64_t step = *t.step;
+  // The counters too, so that their update at the end is not a global
+  // round trip of its own.
+  int64_t hits0 = 0, misses0 = 0;
+  if (count_refs && tid == 0) {
+    hits0 = *t.hits;
+    misses0 = *t.misses;
+  }
 
   for (int e = tid; e < E; e += kThreads) lds.need[e] = 0;
   __syncthreads();
@@ -212,8 +219,15 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
     if (M > 32 || S * per < 83 * M) {
       for (int s = tid; s < S; s += kThreads) {
         const uint64_t mine = lds.key[s];
-        int c = 0;
-        for (int s2 = 0; s2 < S; ++s2) c += lds.key[s2] < mine ? 1 : 0;
+        int c = 0, s2 = 0;
+        for (; s2 + 8 <= S; s2 += 8) {  // eight reads in flight at a time
+          uint64_t k8[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) k8[u] = lds.key[s2 + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) c += k8[u] < mine ? 1 : 0;
+        }
+        for (; s2 < S; ++s2) c += lds.key[s2] < mine ? 1 : 0;
         if (c < M) lds.order[c] = static_cast<int16_t>(s);
       }
     } else if (tid < 64) {
@@ -258,8 +272,8 @@ __device__ void acquire_block(Ids ids, int K, TableDev t, int64_t* map64, int32_
   if (tid == 0) {
     *t.step = step + 1;
     if (count_refs) {
-      *t.hits += hit_total;
-      *t.misses += M;
+      *t.hits = hits0 + hit_total;
+      *t.misses = misses0 + M;
     }
   }
   __syncthreads();
