@@ -212,3 +212,21 @@ def test_cpu_table_argument_errors_surface():
         z = torch.zeros(16, dtype=torch.int64)
         nat.call("xp_plan_chunks_host", nat.ctypes.byref(st), z.data_ptr(), z.data_ptr(), z.data_ptr(), 0, 0, 0,
                  z.data_ptr(), z.data_ptr(), z.data_ptr(), z.data_ptr(), z.data_ptr(), z.data_ptr())
+
+
+@pytest.mark.gpu
+def test_gpu_table_refuses_host_tensors():
+    """A GPU table never hands a host pointer to a kernel: inputs on the CPU are refused before any launch."""
+    t = _table()(16, 4, torch.device("cuda"))
+    host_ids = torch.tensor([[1, 2]], dtype=torch.int64)
+    for op in (t.need_mask, t.acquire):
+        with pytest.raises(ValueError, match="lives on cuda"):
+            op(host_ids)
+    with pytest.raises(ValueError, match="lives on cuda"):
+        t.pack(torch.zeros(16, dtype=torch.bool))
+    vram = _table()(16, 2, torch.device("cuda"))
+    with pytest.raises(ValueError, match="lives on cuda"):
+        t.seed(vram, host_ids, torch.zeros(16, dtype=torch.bool))
+    with pytest.raises(ValueError, match="lives on cuda"):
+        z = torch.zeros(16, dtype=torch.int64)
+        t.plan_chunks(z, z.bool(), z, 4, 0, 0)
