@@ -1,9 +1,13 @@
-"""CPU checks of the table oracle (oracle/table_ref.py).
+"""CPU checks of the table oracle (oracle/table_ref.py), and of the product's
+ExpertTable on CPU tensors against the same expectations.
 
 Pins the oracle with (1) the reference's own golden traces, (2) an
 independent plain LRU (the reference's ReferenceLRU rule), (3) the invariants
 and known answers of the reference's tests/test_table.py, and (4) the chunk
 loop simulator. A planted mistake in the oracle fails at least one of them.
+The tests of (2)-(4) also run on the product's table kept in CPU tensors
+(csrc/table_host.cpp through vllm_expert_pager.table), through a thin
+adapter with the oracle's numpy interface.
 """
 
 import os
@@ -11,12 +15,59 @@ import random
 
 import numpy as np
 import pytest
+import torch
 
 from conftest import GOLDEN
 from oracle import gather_ref
 from oracle.table_ref import LruRef, TableRef
 
 E = 16
+
+
+class CpuTable:
+    """The product's ExpertTable on CPU tensors with the oracle's numpy interface."""
+
+    def __init__(self, num_experts: int, num_slots: int) -> None:
+        from vllm_expert_pager.table import ExpertTable
+
+        self.t = ExpertTable(num_experts, num_slots, torch.device("cpu"))
+        self.num_experts, self.num_slots = num_experts, num_slots
+        # numpy views of the table's tensors: the host code updates them in place
+        self.slot_of = self.t.slot_of.numpy()
+        self.expert_in = self.t.expert_in.numpy()
+        self.last_used = self.t.last_used.numpy()
+
+    step = property(lambda self: int(self.t.step))
+    hits = property(lambda self: int(self.t.hits))
+    misses = property(lambda self: int(self.t.misses))
+
+    @staticmethod
+    def _ids(ids) -> torch.Tensor:
+        return torch.from_numpy(np.ascontiguousarray(np.asarray(ids), dtype=np.int64))
+
+    def need_mask(self, ids) -> np.ndarray:
+        return self.t.need_mask(self._ids(ids)).numpy()
+
+    def acquire(self, ids):
+        return tuple(x.numpy() for x in self.t.acquire(self._ids(ids)))
+
+    def pack(self, mask) -> np.ndarray:
+        return self.t.pack(torch.from_numpy(np.asarray(mask, bool))).numpy()
+
+    def seed(self, vram: "CpuTable", ids, need) -> None:
+        self.t.seed(vram.t, self._ids(ids), torch.from_numpy(np.asarray(need, bool)))
+
+    def plan_chunks(self, before, need, cached_row, rows, ram_base, working_base):
+        out = self.t.plan_chunks(torch.from_numpy(np.asarray(before, np.int64)),
+                                 torch.from_numpy(np.asarray(need, bool)),
+                                 torch.from_numpy(np.asarray(cached_row, np.int64)), rows, ram_base, working_base)
+        return tuple(x.numpy() for x in out)
+
+
+@pytest.fixture(params=["oracle", "cpu_table"])
+def Table(request):
+    """The table under test: the oracle, or the product's CPU table."""
+    return TableRef if request.param == "oracle" else CpuTable
 
 
 def cached(t: TableRef) -> set[int]:
@@ -90,9 +141,9 @@ def test_oracle_matches_reference_traces(fixture):
 
 
 @pytest.mark.parametrize("num_slots", [1, 4, 8])
-def test_acquire_matches_plain_lru(num_slots):
+def test_acquire_matches_plain_lru(Table, num_slots):
     rng = random.Random(0)
-    t = TableRef(E, num_slots)
+    t = Table(E, num_slots)
     ref = LruRef(num_slots)
     for _ in range(300):
         k = rng.randint(1, num_slots)
@@ -107,12 +158,12 @@ def test_acquire_matches_plain_lru(num_slots):
         assert cached(t) == ref.cached()
 
 
-def test_acquire_known_answers():
-    t = TableRef(E, 2)
+def test_acquire_known_answers(Table):
+    t = Table(E, 2)
     for e in (0, 1, 0, 2):
         t.acquire(np.array([[e]]))
     assert cached(t) == {0, 2} and t.hits == 1 and t.misses == 3
-    t = TableRef(E, 4)
+    t = Table(E, 4)
     t.acquire(np.array([[0, 1, 2, 3]]))
     emap, _, todo = t.acquire(np.array([[2, 3, 4, 5]]))
     check_invariants(t)
@@ -132,17 +183,17 @@ def test_pair_slots_differ_only_for_evicted_experts():
         assert np.array_equal(s1 != s2, evicted)
 
 
-def test_rejects_zero_slots():
+def test_rejects_zero_slots(Table):
     with pytest.raises(ValueError):
-        TableRef(E, 0)
+        Table(E, 0)
 
 
-def test_pack_and_negative_ids():
-    t = TableRef(E, 2)
+def test_pack_and_negative_ids(Table):
+    t = Table(E, 2)
     mask = np.zeros(E, bool)
     mask[[3, 7, 12]] = True
     assert list(t.pack(mask)) == [3, 7, 12] + [-1] * (E - 3)
-    ram, vram = TableRef(E, 4), TableRef(E, 2)
+    ram, vram = Table(E, 4), Table(E, 2)
     ids = np.array([[3, -1], [3, -1], [5, -1]])
     need = ram.need_mask(ids)
     assert list(np.nonzero(need)[0]) == [3, 5]
@@ -151,8 +202,8 @@ def test_pack_and_negative_ids():
     assert cached(ram) == {3, 5}
 
 
-def test_seed_known_answers():
-    ram, vram = TableRef(E, 6), TableRef(E, 2)
+def test_seed_known_answers(Table):
+    ram, vram = Table(E, 6), Table(E, 2)
     ram.acquire(np.array([[0, 1, 2, 3, 4, 5]]))
     vram.acquire(np.array([[4, 9]]))
     ids = np.array([[8, 7, 6, 5], [8, 7, 6, 5], [8, 7, 0, 9]])
@@ -165,7 +216,7 @@ def test_seed_known_answers():
     assert ram.last_used[ram.slot_of[9]] > ram.last_used[ram.slot_of[8]]
     assert ram.slot_of[4] == before[4] and ram.slot_of[5] == before[5]
     assert ram.hits == 0 and ram.misses == 6
-    ram, vram = TableRef(E, 4), TableRef(E, 2)
+    ram, vram = Table(E, 4), Table(E, 2)
     ram.acquire(np.array([[0, 1, 2, 3]]))
     vram.acquire(np.array([[0, 9]]))
     ids = np.array([[5, 6], [5, 6], [7, 0]])
@@ -173,9 +224,9 @@ def test_seed_known_answers():
     assert 9 not in cached(ram) and {5, 6, 0} <= cached(ram)
 
 
-def test_plan_chunks_known_answers():
+def test_plan_chunks_known_answers(Table):
     R, S, L, W, layer = 4, 2, 3, 2, 1
-    ram, vram = TableRef(E, R), TableRef(E, S)
+    ram, vram = Table(E, R), Table(E, S)
     rows = np.full(L * R + 2 * W, -1)
     ram.acquire(np.array([[0, 1, 2, 3]]))
     for e in range(4):
@@ -189,7 +240,7 @@ def test_plan_chunks_known_answers():
     assert sorted(ssd) == [0, 5, 6, 7]
     assert L * R <= src_row[7] < L * R + 2 * W and rows[src_row[7]] == 7
 
-    ram, vram = TableRef(E, 4), TableRef(E, 2)
+    ram, vram = Table(E, 4), Table(E, 2)
     rows = np.full(2 * 4 + 2 * 4, -1)
     ram.acquire(np.array([[0, 1, 2, 3]]))
     for e in range(4):
@@ -198,7 +249,7 @@ def test_plan_chunks_known_answers():
     ssd, _ = gather_ref.simulate_working_step(ram, vram, np.array([[2, 5], [3, 3]]), rows, 4, 0, 8)
     assert ssd == [5]
 
-    ram, vram = TableRef(E, 4), TableRef(E, 2)
+    ram, vram = Table(E, 4), Table(E, 2)
     rows = np.full(4 + 6, -1)
     ssd, src_row = gather_ref.simulate_working_step(ram, vram, np.arange(12).reshape(3, 4), rows, 3, 0, 4)
     assert sorted(ssd) == list(range(12))
@@ -207,10 +258,10 @@ def test_plan_chunks_known_answers():
 
 
 @pytest.mark.parametrize("W", [1, 3, 4])
-def test_plan_chunks_random_steps(W):
+def test_plan_chunks_random_steps(Table, W):
     rng = random.Random(W)
     R, S, L, layer = 6, 3, 2, 1
-    ram, vram = TableRef(E, R), TableRef(E, S)
+    ram, vram = Table(E, R), Table(E, S)
     rows = np.full(L * R + 2 * W, -1)
     for _ in range(200):
         k = rng.randint(1, 2 * E)
