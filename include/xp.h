@@ -459,7 +459,7 @@ int xp_moe_experts_noalloc(const uint8_t* xq, const float* xs, int64_t T,
  * (T * topk), H <= 4096 and topk * I <= 32768: out[T][H] gets the bits of
  * xp_moe_quant_route + xp_moe_experts + xp_moe_topk_sum, but the routing and
  * quantisation run inside the gate/up launch and each token's top-k sum
- * inside the down-projection launch (one workgroup per token and 16
+ * inside the down-projection launch (one workgroup per token and 8
  * columns). Replaces, like those calls, fused_experts + moe_sum of a step
  * whose experts are all in the slab (experts.py:579-604): every pair with a
  * valid id should have a slot (one without adds nothing here). work is

@@ -970,12 +970,13 @@ __global__ void __launch_bounds__(kThreads) gemm1_narrow_kernel(const uint8_t* _
 
 // ---- decode steps: two launches for the expert FFN ----
 //
-// For at most kDecodePairs pairs, every gemm1 workgroup routes the pairs
-// itself (wave 0, one pair per lane) and quantises the token rows of its
-// subtile into LDS, so no routing or quantisation launch precedes it. gemm2
-// then takes one token and 16 output columns per workgroup, computes each of
-// the token's pairs and sums them there, so no top-k sum launch follows. The
-// bits are those of xp_moe_quant_route, xp_moe_experts and xp_moe_topk_sum.
+// For at most kDecodePairs pairs, every wave of every gemm1 workgroup routes
+// the pairs itself (one pair per lane) and the workgroup quantises the token
+// rows it multiplies into LDS, so no routing or quantisation launch precedes
+// it. gemm2 then takes one token and 8 output columns per workgroup, computes
+// each of the token's pairs and sums them there, so no top-k sum launch
+// follows. The bits are those of xp_moe_quant_route, xp_moe_experts and
+// xp_moe_topk_sum.
 constexpr int kDecodePairs = 64;
 constexpr int kDecodeMaxH = 4096;       // 16 quantised token rows of H bytes fit in LDS
 constexpr int kDecodeActBytes = 32768;  // a token's quantised activations (topk x I) in LDS
