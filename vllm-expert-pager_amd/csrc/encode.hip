@@ -228,7 +228,7 @@ __global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, i
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const bool upper = lane >= 32;
   const uint32_t li = lane & 31;
-  const uint32_t low = upper ? 0u : ~0u;
+  const uint32_t half_shift = upper ? 16u : 0u;
   const int mwords = chunk / 8;
   const uint32_t total = static_cast<uint32_t>(gstart[G]);  // every word position is below it
   {
@@ -239,51 +239,60 @@ __global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, i
     const int gg = live ? g : G - 1;
     const uint8_t* src = raw + (int64_t(gg) * XP_LANES + li) * chunk;
     uint32_t* fx = fixed + int64_t(gg) * mwords * XP_LANES + li;
-    // Word positions of the two half-waves' groups, uniform per half.
-    uint32_t base_lo = static_cast<uint32_t>(gstart[g0]);
-    uint32_t base_hi = static_cast<uint32_t>(gstart[g0 + 1 < G ? g0 + 1 : G - 1]);
+    // Word positions within each half's group, both below 2^16 (a group's
+    // words are at most 32 chunks of 9-bit codes), packed in one scalar
+    // register: the lower half's in bits 0-15, the upper half's in 16-31
+    // biased by kBias, so that lowering the upper half's count by the lower
+    // half's refills of a symbol (at most 32) never borrows. A lane's
+    // queued positions are relative; gbase makes them absolute.
+    constexpr uint32_t kBias = 64;
+    const uint32_t gs_lo = static_cast<uint32_t>(gstart[g0]);
+    const uint32_t gs_hi = static_cast<uint32_t>(gstart[g0 + 1 < G ? g0 + 1 : G - 1]);
+    const uint32_t gbase = upper ? gs_hi - kBias : gs_lo;
+    uint32_t offs = kBias << 16;
     uint32_t level = 0;         // bits the decoder has buffered
     uint64_t acc = 0;           // bits of the lane's stream not yet emitted
     uint32_t accbits = 0;
     uint32_t q0 = 0, q1 = 0;    // positions of words refilled but not yet emitted
     uint32_t qn = 0;
     u32x4 v_next = *reinterpret_cast<const u32x4*>(src);  // the next 16 values, loaded a step ahead
+    const uint8_t* tab = reinterpret_cast<const uint8_t*>(s_tab);
     for (int i0 = 0; i0 < chunk; i0 += 16) {
       const u32x4 v = v_next;
       if (i0 + 16 < chunk) v_next = *reinterpret_cast<const u32x4*>(src + i0 + 16);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
+        // Each byte's exponent field (bits 3-6) as a byte offset into s_tab.
+        const uint32_t ex4 = (w[k] >> 1) & 0x3C3C3C3Cu;
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const uint32_t e = (w[k] >> (8 * b + 3)) & 15u;
+          // The decoder's refill rule: a lane with fewer than LIMIT bits
+          // buffered takes the next word of its group, ranked by the
+          // refilling lanes below it in its half.
           const bool refill = level < static_cast<uint32_t>(XP_LIMIT);
           const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
           const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
-          const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u) & low);
-          if (refill) {
-            const uint32_t pos = (upper ? base_hi : base_lo) + below;
-            if (qn == 0)
-              q0 = pos;
-            else
-              q1 = pos;
-            ++qn;
-            level += 32;
-          }
-          base_lo += static_cast<uint32_t>(__popc(m_lo));
-          base_hi += static_cast<uint32_t>(__popc(m_hi));
-          const uint32_t t = s_tab[e];
+          const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
+          const uint32_t bases = offs - (n_lo << 16);
+          const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+              m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, __builtin_amdgcn_ubfe(bases, half_shift, 16u)));
+          offs += n_lo + (n_hi << 16);
+          q0 = refill && qn == 0 ? pos : q0;
+          q1 = refill && qn != 0 ? pos : q1;
+          qn += refill ? 1u : 0u;
+          level += refill ? 32u : 0u;
+          const uint32_t t = *reinterpret_cast<const uint32_t*>(tab + __builtin_amdgcn_ubfe(ex4, 8u * b, 8u));
           const uint32_t len = t >> 16;
           acc |= static_cast<uint64_t>(t & 0xffffu) << accbits;
           accbits += len;
           level -= len;
-          if (accbits >= 32) {  // word q0 is complete
-            if (live && q0 < total) huff[q0] = static_cast<uint32_t>(acc);
-            acc >>= 32;
-            accbits -= 32;
-            q0 = q1;
-            --qn;
-          }
+          const bool full = accbits >= 32;  // word q0 is complete
+          if (full && live && gbase + q0 < total) huff[gbase + q0] = static_cast<uint32_t>(acc);
+          acc = full ? acc >> 32 : acc;
+          accbits &= 31u;  // below 32 + LIMIT
+          q0 = full ? q1 : q0;
+          qn -= full ? 1u : 0u;
         }
         if (k & 1) {  // 8 values: one nibble word, value j in bits 4j..4j+3
           // Per byte, sign (bit 7) to bit 3 beside the mantissa (bits 0-2);
@@ -300,7 +309,7 @@ __global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, i
     // then zeros.
     while (__builtin_amdgcn_ballot_w64(qn > 0)) {
       if (qn > 0) {
-        if (live && q0 < total) huff[q0] = static_cast<uint32_t>(acc);
+        if (live && gbase + q0 < total) huff[gbase + q0] = static_cast<uint32_t>(acc);
         acc >>= 32;
         q0 = q1;
         --qn;
