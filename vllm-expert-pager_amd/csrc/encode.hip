@@ -255,55 +255,73 @@ __global__ void __launch_bounds__(kThreads) encode_groups_kernel(EncodeArgs a, i
     uint32_t accbits = 0;
     uint32_t q0 = 0, q1 = 0;    // positions of words refilled but not yet emitted
     uint32_t qn = 0;
-    u32x4 v_next = *reinterpret_cast<const u32x4*>(src);  // the next 16 values, loaded a step ahead
+    // A lane's values in blocks of 64 (four 16-byte loads back to back, so
+    // each cache line of its chunk is fetched about twice instead of once
+    // per 16 values), the next block loaded while this one is encoded.
+    const int nv = chunk < 64 ? chunk / 16 : 4;  // loads per block
+    u32x4 cur[4], nxt[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < nv) cur[j] = *reinterpret_cast<const u32x4*>(src + 16 * j);
     const uint8_t* tab = reinterpret_cast<const uint8_t*>(s_tab);
-    for (int i0 = 0; i0 < chunk; i0 += 16) {
-      const u32x4 v = v_next;
-      if (i0 + 16 < chunk) v_next = *reinterpret_cast<const u32x4*>(src + i0 + 16);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    for (int i0 = 0; i0 < chunk; i0 += 16 * nv) {
+      if (i0 + 16 * nv < chunk) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        // Each byte's exponent field (bits 3-6) as a byte offset into s_tab.
-        const uint32_t ex4 = (w[k] >> 1) & 0x3C3C3C3Cu;
+        for (int j = 0; j < 4; ++j)
+          if (j < nv) nxt[j] = *reinterpret_cast<const u32x4*>(src + i0 + 16 * nv + 16 * j);
+      }
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          // The decoder's refill rule: a lane with fewer than LIMIT bits
-          // buffered takes the next word of its group, ranked by the
-          // refilling lanes below it in its half.
-          const bool refill = level < static_cast<uint32_t>(XP_LIMIT);
-          const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
-          const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
-          const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
-          const uint32_t bases = offs - (n_lo << 16);
-          const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
-              m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, __builtin_amdgcn_ubfe(bases, half_shift, 16u)));
-          offs += n_lo + (n_hi << 16);
-          q0 = refill && qn == 0 ? pos : q0;
-          q1 = refill && qn != 0 ? pos : q1;
-          qn += refill ? 1u : 0u;
-          level += refill ? 32u : 0u;
-          const uint32_t t = *reinterpret_cast<const uint32_t*>(tab + __builtin_amdgcn_ubfe(ex4, 8u * b, 8u));
-          const uint32_t len = t >> 16;
-          acc |= static_cast<uint64_t>(t & 0xffffu) << accbits;
-          accbits += len;
-          level -= len;
-          const bool full = accbits >= 32;  // word q0 is complete
-          if (full && live && gbase + q0 < total) huff[gbase + q0] = static_cast<uint32_t>(acc);
-          acc = full ? acc >> 32 : acc;
-          accbits &= 31u;  // below 32 + LIMIT
-          q0 = full ? q1 : q0;
-          qn -= full ? 1u : 0u;
-        }
-        if (k & 1) {  // 8 values: one nibble word, value j in bits 4j..4j+3
-          // Per byte, sign (bit 7) to bit 3 beside the mantissa (bits 0-2);
-          // then two bytes' nibbles joined and the four pairs picked.
-          const uint32_t x0 = w[k - 1], x1 = w[k];
-          const uint32_t t0 = (x0 & 0x07070707u) | ((x0 >> 4) & 0x08080808u);
-          const uint32_t t1 = (x1 & 0x07070707u) | ((x1 >> 4) & 0x08080808u);
-          const uint32_t nib = __builtin_amdgcn_perm(t1 | (t1 >> 4), t0 | (t0 >> 4), 0x06040200u);
-          if (live) fx[int64_t((i0 + 8 * (k >> 1)) / 8) * XP_LANES] = nib;
+      for (int jv = 0; jv < 4; ++jv) {
+        if (jv >= nv) break;
+        const u32x4 v = cur[jv];
+        const int i1 = i0 + 16 * jv;
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          // Each byte's exponent field (bits 3-6) as a byte offset into s_tab.
+          const uint32_t ex4 = (w[k] >> 1) & 0x3C3C3C3Cu;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            // The decoder's refill rule: a lane with fewer than LIMIT bits
+            // buffered takes the next word of its group, ranked by the
+            // refilling lanes below it in its half.
+            const bool refill = level < static_cast<uint32_t>(XP_LIMIT);
+            const unsigned long long mask = __builtin_amdgcn_ballot_w64(refill);
+            const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
+            const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
+            const uint32_t bases = offs - (n_lo << 16);
+            const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+                m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, __builtin_amdgcn_ubfe(bases, half_shift, 16u)));
+            offs += n_lo + (n_hi << 16);
+            q0 = refill && qn == 0 ? pos : q0;
+            q1 = refill && qn != 0 ? pos : q1;
+            qn += refill ? 1u : 0u;
+            level += refill ? 32u : 0u;
+            const uint32_t t = *reinterpret_cast<const uint32_t*>(tab + __builtin_amdgcn_ubfe(ex4, 8u * b, 8u));
+            const uint32_t len = t >> 16;
+            acc |= static_cast<uint64_t>(t & 0xffffu) << accbits;
+            accbits += len;
+            level -= len;
+            const bool full = accbits >= 32;  // word q0 is complete
+            if (full && live && gbase + q0 < total) huff[gbase + q0] = static_cast<uint32_t>(acc);
+            acc = full ? acc >> 32 : acc;
+            accbits &= 31u;  // below 32 + LIMIT
+            q0 = full ? q1 : q0;
+            qn -= full ? 1u : 0u;
+          }
+          if (k & 1) {  // 8 values: one nibble word, value j in bits 4j..4j+3
+            // Per byte, sign (bit 7) to bit 3 beside the mantissa (bits 0-2);
+            // then two bytes' nibbles joined and the four pairs picked.
+            const uint32_t x0 = w[k - 1], x1 = w[k];
+            const uint32_t t0 = (x0 & 0x07070707u) | ((x0 >> 4) & 0x08080808u);
+            const uint32_t t1 = (x1 & 0x07070707u) | ((x1 >> 4) & 0x08080808u);
+            const uint32_t nib = __builtin_amdgcn_perm(t1 | (t1 >> 4), t0 | (t0 >> 4), 0x06040200u);
+            if (live) fx[int64_t((i1 + 8 * (k >> 1)) / 8) * XP_LANES] = nib;
+          }
         }
       }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cur[j] = nxt[j];
     }
     // Words whose refill came but whose bits ran out: the rest of the stream,
     // then zeros.
