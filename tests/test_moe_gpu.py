@@ -420,5 +420,8 @@ def test_decode_experts_limits():
     ids = torch.zeros((9, 8), dtype=torch.int64, device="cuda")
     assert not moe.decode_fits(x, ids, 512)  # 72 pairs
     assert moe.decode_fits(x[:8], ids[:8], 512)
+    # the pager takes the fused step up to 40 pairs, the separate calls above
+    assert moe.decode_pays(x[:5], ids[:5], 512) and not moe.decode_pays(x[:6], ids[:6], 512)
+    assert not moe.decode_pays(x[:1], ids[:1], 8192)
     assert not moe.decode_fits(x[:1], ids[:1], 8192)  # topk * I above 32 KiB
     assert not moe.decode_fits(torch.zeros((1, 8192), dtype=torch.bfloat16, device="cuda"), ids[:1], 512)

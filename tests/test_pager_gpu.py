@@ -110,18 +110,20 @@ def test_decode_steps_match_one_shot(model, compress, R):
 
 @pytest.mark.parametrize("compress, R", [(True, 160), (False, 256)])
 def test_batched_decode_steps_beyond_the_fused_step(model, compress, R):
-    """12 tokens x top-8 = 96 pairs over 128 cache slots: still the decode
-    path (96 <= S), but more pairs than the fused two-launch step takes, so
-    quantise + route, the expert launches and the top-k sum run separately.
-    The compressed case pages through the SSD tier (R < E)."""
+    """12, 9 and 6 tokens x top-8 = 96, 72 and 48 pairs over 128 cache slots:
+    still the decode path (pairs <= S), but more pairs than the fused
+    two-launch step is used for (96 and 72 are more than it takes, 48 more
+    than it pays for), so quantise + route, the expert launches and the top-k
+    sum run separately. The compressed case pages through the SSD tier (R < E)."""
     moe = _mods()[0]
     m = model(256, 128, R, 8, compress)
     rng = np.random.default_rng(11)
     layer = m.layers[0]
     for step in range(12):
-        T = 12 if step % 3 else 9  # 72 pairs: also above the fused limit
+        T = (9, 12, 6)[step % 3]
         x, tw, ids = routing(rng, T, m.E, 8, zipf=0.8)
-        assert ids.numel() <= 128 and not moe.decode_fits(x, ids, I)
+        assert ids.numel() <= 128 and not moe.decode_pays(x, ids, I)
+        assert moe.decode_fits(x, ids, I) == (T == 6)
         out = layer.forward(x, tw, ids)
         assert same(out, m.one_shot(0, x, tw, ids)), f"step {step}"
     vh, vm, rh, rm = layer.hit_rates()

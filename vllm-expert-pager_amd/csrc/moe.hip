@@ -999,29 +999,31 @@ __device__ __forceinline__ int decode_slot(int p, int n, const void* ids, int eb
 
 // The step's routing as route_kernel lists it (pairs by slot, then by pair
 // index; one tile per occupied slot, since a slot holds at most 64 of these
-// pairs), computed by one wave from the pairs' slots (lane p: pair p):
-// whether lane p's pair is its slot's first, and that slot's tile index (the
-// number of occupied slots below it). The loops run over uniform pair
-// indices, so each read of another lane's slot is a readlane.
+// pairs), computed by one wave from the pairs' slots (lane p: pair p): on
+// the lane of each slot's first pair, the slot's 16-row subtiles (nsub) and
+// the index of its first one among all the step's subtiles in slot order
+// (start); zero subtiles on the other lanes. The loops run over uniform pair
+// indices, so each read of another lane's value is a readlane.
 struct DecodeRoute {
-  int slot, tile;
-  bool first;
+  int slot, start, nsub;
 };
 
 __device__ __forceinline__ DecodeRoute decode_route(int slot, int n) {
   const int lane = threadIdx.x & 63;
   bool first = slot >= 0;
+  int count = 0;
   for (int q = 0; q < n; ++q) {
     const int sq = __builtin_amdgcn_readlane(slot, q);
     if (q < lane && sq == slot) first = false;
+    count += sq == slot ? 1 : 0;
   }
-  const unsigned long long firsts = __ballot(first);
-  int tile = 0;
+  const int nsub = first ? (count + 15) >> 4 : 0;
+  int start = 0;
   for (int q = 0; q < n; ++q) {
-    const int sq = __builtin_amdgcn_readlane(slot, q);
-    if (((firsts >> q) & 1ull) && sq < slot) ++tile;
+    const int sq = __builtin_amdgcn_readlane(slot, q), nq = __builtin_amdgcn_readlane(nsub, q);
+    if (sq < slot) start += nq;
   }
-  return DecodeRoute{slot, tile, first};
+  return DecodeRoute{slot, start, nsub};
 }
 
 // gemm1_narrow_kernel over a decode step's pairs, with their routing and the
@@ -1035,7 +1037,7 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
     const uint16_t* __restrict__ x, int64_t H, int64_t I, const void* ids, int eb, int npairs, int topk,
     const int32_t* __restrict__ expert_map, const int32_t* __restrict__ pair_slot, int E, int slots,
     const uint8_t* __restrict__ w13,
-    const float* __restrict__ w13_scale, int nsub, Work work) {
+    const float* __restrict__ w13_scale, Work work) {
   constexpr int kPerWave = kSplitRound / (kThreads / 64);
   constexpr int kPre = 4;  // token pieces per thread requested before the routing
   extern __shared__ __attribute__((aligned(16))) uint8_t s_aq[];  // [16][H] fp8 token rows
@@ -1077,18 +1079,23 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
     *reinterpret_cast<uint2*>(s_aq + r * H + c8) = make_uint2(q0, q1);
     if ((tid & 15) == 0) s_xs[r * KB + c8 / kKB] = sc;
   };
-  // With at most 16 tokens, all their rows are quantised (piece i of the
-  // step: token i / (H / 8)); otherwise each workgroup quantises its
-  // subtile's rows once they are known.
+  // With one or two tokens, all their rows are requested before the routing
+  // and quantised (piece i of the step: token i / (H / 8)): a batch-1 step
+  // is bound by load latency. With more, each workgroup quantises only its
+  // subtile's rows once they are known (its pairs are mostly of different
+  // tokens, and every token row of the step would be quantised in each of
+  // hundreds of workgroups: 143 against 31 us at 8 tokens).
   const int ntok = npairs / topk;
-  const bool by_token = ntok <= 16;
+  const bool by_token = ntok <= 2;
   const int nc8 = static_cast<int>(H / 8), npiece = by_token ? ntok * nc8 : 0;
   auto piece_ptr = [&](int i) { return x + static_cast<int64_t>(i / nc8) * H + (i % nc8) * 8; };
   u32x4 xr[kPre];
+  if (by_token) {
 #pragma unroll
-  for (int i = 0; i < kPre; ++i) {
-    const int it = tid + kThreads * i;
-    xr[i] = *reinterpret_cast<const u32x4*>(piece_ptr(it < npiece ? it : 0));
+    for (int i = 0; i < kPre; ++i) {
+      const int it = tid + kThreads * i;
+      xr[i] = *reinterpret_cast<const u32x4*>(piece_ptr(it < npiece ? it : 0));
+    }
   }
 
   const int slot_l = decode_slot(lane, npairs, ids, eb, expert_map, pair_slot, E, slots);
@@ -1096,19 +1103,21 @@ __global__ void __launch_bounds__(kThreads) gemm1_decode_kernel(
   // activation-scale region, which the decode path does not use).
   if (blockIdx.x == 0 && wave == 0 && lane < npairs) reinterpret_cast<int32_t*>(work.acts)[lane] = slot_l;
   const DecodeRoute rt = decode_route(slot_l, npairs);
-  const int ntiles = __popcll(__ballot(rt.first));
 
+  // The workgroup's subtile among all the step's, in slot order, and its
+  // column block; the grid bounds the subtiles (the same in every wave).
   const int ncb = static_cast<int>(I / 16);
-  int ti, item;
-  xcd_item(nsub * ncb, ti, item);
-  if (ti >= ntiles) return;  // the same in every wave
-  const unsigned long long lead = __ballot(rt.first && rt.tile == ti);
-  const int slot = __builtin_amdgcn_readlane(slot_l, __ffsll(static_cast<long long>(lead)) - 1);
+  int gsi, cbk;
+  xcd_item(ncb, gsi, cbk);
+  const unsigned long long own = __ballot(rt.nsub > 0 && rt.start <= gsi && gsi < rt.start + rt.nsub);
+  if (own == 0) return;
+  const int lead = __ffsll(static_cast<long long>(own)) - 1;
+  const int slot = __builtin_amdgcn_readlane(slot_l, lead);
+  const int sub = gsi - __builtin_amdgcn_readlane(rt.start, lead);
   const unsigned long long mine = __ballot(slot_l == slot);
   const int count = __popcll(mine);
-  const int sub = item / ncb, r0 = 16 * sub;
-  if (r0 >= count) return;
-  const int c0 = (item - sub * ncb) * 16;
+  const int r0 = 16 * sub;  // below count
+  const int c0 = cbk * 16;
   const int nrow = count - r0 < 16 ? count - r0 : 16;
 
   // The slot's gate and up scales, then its weight rows, requested at once.
@@ -2116,20 +2125,23 @@ int xp_moe_decode_experts(const uint16_t* x, int64_t T, int64_t H, const void* t
   XP_REQUIRE(work_bytes >= need, "%s: workspace of %lld B, needs %lld", what, (long long)work_bytes, (long long)need);
   Work w;
   work_layout(npairs, I, &w, static_cast<uint8_t*>(work));
-  // A tile per occupied slot: at most min(npairs, slots) of them.
-  const int64_t tiles8 = ((npairs < slots ? npairs : slots) + 7) / 8 * 8;
-  const int nsub = static_cast<int>(((npairs < kBM ? npairs : kBM) + 15) / 16);
-  const dim3 g1(static_cast<unsigned>(tiles8 * nsub * (I / 16)));
+  // One workgroup per 16-row subtile of an occupied slot and 16 columns.
+  // The subtiles number at most min(npairs, slots), plus npairs / 16 when a
+  // slot can hold more than 16 pairs (sum over slots of ceil(c / 16) with
+  // the counts c summing to npairs).
+  const int64_t subs = (npairs < slots ? npairs : slots) + (npairs > 16 ? npairs / 16 : 0);
+  const int64_t subs8 = (subs + 7) / 8 * 8;  // the XCD-aware grid covers whole groups of 8
+  const dim3 g1(static_cast<unsigned>(subs8 * (I / 16)));
   if (activation == XP_ACT_GELU)
     hipLaunchKernelGGL(gemm1_decode_kernel<XP_ACT_GELU>, g1, dim3(kThreads), static_cast<size_t>(16 * H),
                        as_stream(stream), x, H, I, topk_ids, topk_elem_bytes, static_cast<int>(npairs),
                        static_cast<int>(topk), expert_map, pair_slot, static_cast<int>(num_experts),
-                       static_cast<int>(slots), w13, w13_scale, nsub, w);
+                       static_cast<int>(slots), w13, w13_scale, w);
   else
     hipLaunchKernelGGL(gemm1_decode_kernel<XP_ACT_SILU>, g1, dim3(kThreads), static_cast<size_t>(16 * H),
                        as_stream(stream), x, H, I, topk_ids, topk_elem_bytes, static_cast<int>(npairs),
                        static_cast<int>(topk), expert_map, pair_slot, static_cast<int>(num_experts),
-                       static_cast<int>(slots), w13, w13_scale, nsub, w);
+                       static_cast<int>(slots), w13, w13_scale, w);
   int rc = check_launch("gemm1_decode_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(gemm2_decode_kernel, dim3(static_cast<unsigned>(T * (H / kDecodeCols2))), dim3(kThreads),

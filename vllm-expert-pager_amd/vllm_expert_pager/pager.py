@@ -286,7 +286,7 @@ class PagedExperts:
         if shared is not None:
             shared()
         with trace.range(f"expert_pager L{layer} experts"):
-            if moe.decode_fits(x, topk_ids, self.pager.intermediate):
+            if moe.decode_pays(x, topk_ids, self.pager.intermediate):
                 slab = self.cache_slab
                 out = moe.decode_experts(x, topk_weights, topk_ids, self.expert_map, E, slab[PARAMS[0]],
                                          slab[SCALES[0]], slab[PARAMS[1]], slab[SCALES[1]], self.table.num_slots,
