@@ -86,59 +86,112 @@ __device__ __forceinline__ void ring_put(uint32_t* ring, uint32_t w_index, uint3
   if (s < kMirror) ring[s + kRing] = value;
 }
 
-// One lane's stream: a chunk of the group of this lane's half, plus the
-// state of that group's ring (uniform over the half).
+// One lane's stream: a chunk of the group of this lane's half.
 struct Chain {
   uint64_t buf;      // {hi, lo}: the last two words loaded
   uint32_t pos;      // next bit in buf minus one (the window shift then scales the LUT
                      // index to a byte offset); the fill level is 63 - pos. At least 1
                      // bit is always consumed before a window is read, so it never wraps.
-  uint32_t rp;       // words of the group consumed
-  uint32_t fe;       // ring holds words [rp, fe)
-  uint32_t q;        // words requested so far (landed or in flight)
-  uint32_t b_base, b_n, b_val0, b_val1;  // request in flight, issued at this half's start
-  uint32_t ab0;      // byte address of word rp in LDS at the half's start
+  uint32_t b_val0, b_val1;  // this lane's words of the request in flight
   uint32_t x_next;   // nibble word of the next iteration
   uint32_t x_next1;  // and the one after it, when both are fetched an iteration ahead
-  uint32_t count;    // Huffman words of the group
   uint32_t wsrc;     // byte offset in the record of the group's word li (this lane's column)
   uint32_t nib;      // byte offset in the record of this lane's first nibble word
   uint32_t* ring;
-  uint32_t ring_addr;
 };
 
-// Start of a half-iteration: make sure the ring holds the next kAhead words,
-// then request up to kFetch more (landed at the end of this half).
-__device__ __forceinline__ void half_begin(Chain& c, uint32_t li, __amdgpu_buffer_rsrc_t rec) {
-  while (c.fe < c.count && c.fe < c.rp + kAhead) {  // slow path: the stream outran the requests
-    const uint32_t w = c.fe + li;
-    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * c.fe, 0, 0);
-    if (w < c.count) ring_put(c.ring, w, v);
-    c.fe = c.fe + 32 < c.count ? c.fe + 32 : c.count;
-  }
-  c.q = c.q > c.fe ? c.q : c.fe;
-  const uint32_t room = c.rp + kRing - c.q;
-  const uint32_t want = c.count - c.q;
-  uint32_t n = want < room ? want : room;
-  n = n < kFetch ? n : kFetch;
-  c.b_base = c.q;
-  c.b_n = n;
-  // Reads past the group's words return other bytes of the record (never
-  // used), past the record zeros: the buffer's range check bounds them.
-  c.b_val0 = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * c.q, 0, 0);
-  c.b_val1 = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * c.q + 128u, 0, 0);
-  c.q += n;
-  c.ab0 = c.ring_addr + 4u * (c.rp & (kRing - 1));
+// The ring state of the wave's two groups (index h: lanes 32h .. 32h + 31).
+// Every field is the same in all lanes, so it lives in scalar registers and
+// its upkeep is scalar work; a lane takes its half's value, with one
+// bit-field extract from a pair packed in 16-bit halves, only where an
+// address needs it. Word indices stay below 2^16: a group's word count is
+// clamped to 65535, above the words any group can consume (chunk <= 4096
+// symbols per lane of at most LIMIT bits: 32 * 4096 * 9 / 32 words, plus
+// one refill per lane).
+struct Rings {
+  uint32_t rp[2];     // words of the group consumed
+  uint32_t fe[2];     // the ring holds words [rp, fe)
+  uint32_t q[2];      // words requested so far (landed or in flight)
+  uint32_t count[2];  // Huffman words of the group
+  uint32_t base[2];   // LDS word address (byte address / 4) of the group's ring
+  uint32_t bb[2];     // first word of the request in flight
+  uint32_t bn[2];     // and its word count
+  uint32_t ab0[2];    // LDS word address of word rp at the half's start
+};
+
+// Minimum of two wave-uniform values on the scalar unit. Written as an
+// instruction because the compiler otherwise fuses two minimums into a
+// vector min3 and reads the result back into a scalar register.
+__device__ __forceinline__ uint32_t smin(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("s_min_u32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b));
+  return r;
 }
 
-// End of a half-iteration: land the request in the ring (its slots hold
+// lo | hi << 16 for wave-uniform values below 2^16, as one scalar pack.
+__device__ __forceinline__ uint32_t spack(uint32_t lo, uint32_t hi) {
+  uint32_t r;
+  asm("s_pack_ll_b32_b16 %0, %1, %2" : "=s"(r) : "s"(lo), "s"(hi));
+  return r;
+}
+
+// This lane's value of a per-group pair (both below 2^16).
+__device__ __forceinline__ uint32_t lane_half(const uint32_t (&v)[2], uint32_t half_shift) {
+  return __builtin_amdgcn_ubfe(spack(v[0], v[1]), half_shift, 16u);
+}
+
+// Start of a half-iteration: make sure each ring holds the next kAhead words,
+// then request up to kFetch more (landed at the end of this half).
+__device__ __forceinline__ void half_begin(Rings& r, Chain& c, uint32_t li, bool upper, uint32_t half_shift,
+                                           __amdgpu_buffer_rsrc_t rec) {
+  bool slow = false;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) slow = slow || (r.fe[h] < r.count[h] && r.fe[h] < r.rp[h] + kAhead);
+  if (slow) {  // the stream outran the requests: this lane's group, 32 words at a time
+    uint32_t fe = upper ? r.fe[1] : r.fe[0];
+    const uint32_t count = upper ? r.count[1] : r.count[0];
+    const uint32_t lim = (upper ? r.rp[1] : r.rp[0]) + kAhead;
+    while (fe < count && fe < lim) {
+      const uint32_t w = fe + li;
+      const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rec, c.wsrc + 4u * fe, 0, 0);
+      if (w < count) ring_put(c.ring, w, v);
+      fe = fe + 32 < count ? fe + 32 : count;
+    }
+    r.fe[0] = __builtin_amdgcn_readlane(fe, 0);
+    r.fe[1] = __builtin_amdgcn_readlane(fe, 32);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    r.q[h] = r.q[h] > r.fe[h] ? r.q[h] : r.fe[h];
+    const uint32_t room = r.rp[h] + kRing - r.q[h];
+    const uint32_t want = r.count[h] - r.q[h];
+    const uint32_t n = smin(smin(want, room), kFetch);
+    r.bb[h] = r.q[h];
+    r.bn[h] = n;
+    r.q[h] += n;
+    r.ab0[h] = r.base[h] + (r.rp[h] & (kRing - 1));
+  }
+  // Reads past the group's words return other bytes of the record (never
+  // used), past the record zeros: the buffer's range check bounds them.
+  const uint32_t a = c.wsrc + 4u * lane_half(r.bb, half_shift);
+  c.b_val0 = __builtin_amdgcn_raw_buffer_load_b32(rec, a, 0, 0);
+  c.b_val1 = __builtin_amdgcn_raw_buffer_load_b32(rec, a + 128u, 0, 0);
+}
+
+// End of a half-iteration: offs holds each group's next unread ring word
+// address (low | high << 16); land the request in the ring (its slots hold
 // words already consumed).
-__device__ __forceinline__ void half_end(Chain& c, uint32_t li, uint32_t ab) {
-  c.rp += (ab - c.ab0) >> 2;
-  if (li < c.b_n) ring_put(c.ring, c.b_base + li, c.b_val0);
-  if (li + 32 < c.b_n) ring_put(c.ring, c.b_base + 32 + li, c.b_val1);
-  const uint32_t landed = c.b_base + c.b_n;
-  c.fe = c.fe > landed ? c.fe : landed;
+__device__ __forceinline__ void half_end(Rings& r, Chain& c, uint32_t li, uint32_t half_shift, uint32_t offs) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) r.rp[h] += ((offs >> (16 * h)) & 0xFFFFu) - r.ab0[h];
+  const uint32_t bb = lane_half(r.bb, half_shift), bn = lane_half(r.bn, half_shift);
+  if (li < bn) ring_put(c.ring, bb + li, c.b_val0);
+  if (li + 32 < bn) ring_put(c.ring, bb + 32 + li, c.b_val1);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t landed = r.bb[h] + r.bn[h];
+    r.fe[h] = r.fe[h] > landed ? r.fe[h] : landed;
+  }
 }
 
 // mask[lane] ? if1 : if0, as one v_cndmask. Written as an instruction so
@@ -164,10 +217,11 @@ __device__ __forceinline__ uint32_t add_byte0(uint32_t pos, uint32_t e) {
 // len | (symbol << 3) << 8 per 9-bit code, followed by the 64-byte position
 // table: entry p is p - 32 for a position that refills (p > 63 - LIMIT),
 // else p. Reading it replaces a select and an add per symbol by one LDS
-// read issued beside the ring read. offs packs the LDS byte
-// addresses of the next unread ring word of the groups of the lower and
-// upper half-wave (low | high << 16; both below 2^16): wave-uniform, so it
-// advances in a scalar register.
+// read issued beside the ring read. offs packs the LDS word
+// addresses (byte address / 4) of the next unread ring word of the groups of
+// the lower and upper half-wave (low | high << 16; both below 2^16):
+// wave-uniform, so it advances in a scalar register, by one 16-bit pack and
+// one add.
 // A lane's refill word is (refilling lanes below it in its half) words on;
 // mbcnt over the whole ballot also counts, for an upper-half lane, every
 // refilling lane of the lower half, so that half's base is lowered by as
@@ -180,11 +234,11 @@ __device__ __forceinline__ uint32_t decode_symbol(uint64_t& buf, uint32_t& pos, 
   const unsigned long long mask = __builtin_amdgcn_ballot_w64(pos > 63u - kLimit);
   const uint32_t m_lo = static_cast<uint32_t>(mask), m_hi = static_cast<uint32_t>(mask >> 32);
   const uint32_t n_lo = static_cast<uint32_t>(__popc(m_lo)), n_hi = static_cast<uint32_t>(__popc(m_hi));
-  const uint32_t bases = offs - (n_lo << 18);  // the upper half's base lowered by n_lo words
+  const uint32_t bases = offs - (n_lo << 16);  // the upper half's base lowered by n_lo words
   const uint32_t below = __builtin_amdgcn_mbcnt_hi(m_hi, __builtin_amdgcn_mbcnt_lo(m_lo, 0u));
-  const uint32_t addr = __builtin_amdgcn_ubfe(bases, half_shift, 16u) + 4u * below;
+  const uint32_t addr = (__builtin_amdgcn_ubfe(bases, half_shift, 16u) + below) << 2;
   const uint32_t w = *reinterpret_cast<const __attribute__((address_space(3))) uint32_t*>(addr);
-  offs += (n_lo << 2) + (n_hi << 18);
+  offs += spack(n_lo, n_hi);
   const uint32_t lo = static_cast<uint32_t>(buf), hi = static_cast<uint32_t>(buf >> 32);
   const uint32_t nlo = lane_select(mask, lo, hi), nhi = lane_select(mask, hi, w);
   buf = (static_cast<uint64_t>(nhi) << 32) | nlo;
@@ -431,7 +485,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
     ge = ge < gs ? gs : (ge > maxw ? maxw : ge);
   }
   Chain ch;
-  ch.count = static_cast<uint32_t>(ge - gs);
+  // Words of the group, clamped as the ring state needs (no group consumes 65535).
+  const uint32_t count = static_cast<uint32_t>(ge - gs < 0xFFFF ? ge - gs : 0xFFFF);
   // The record as a raw buffer of pitch bytes (stride 0; word 3 of the
   // descriptor 0x00020000 selects 32-bit data on gfx9-family chips): the
   // hardware range check returns zero for loads beyond it, so the group's
@@ -440,13 +495,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
       const_cast<uint32_t*>(rec), 0, static_cast<int>(nm.pitch), 0x00020000);
   ch.wsrc = static_cast<uint32_t>(4 * (huff_off + gs) + 4 * li);
   ch.ring = s_ring[gl];
-  ch.ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ch.ring));
+  const uint32_t ring_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ch.ring));
   ch.nib = static_cast<uint32_t>(4 * ((G + 1) + (int64_t(g) * msteps) * 32 + li));
   ch.buf = 0;
   ch.pos = 63u;  // nothing loaded: the first symbol refills every lane
-  ch.rp = 0;
-  ch.b_n = 0;
-  ch.b_base = ch.b_val0 = ch.b_val1 = 0;
+  ch.b_val0 = ch.b_val1 = 0;
   uint8_t* out = nm.dst + drow * nm.N + int64_t(g) * 32 * a.chunk;  // chunk 0 of the group
   // The wave's two groups as one run of 64 chunks (the 16-iteration flush).
   const int g_lo = r * kGroupsPerBlock + 2 * __builtin_amdgcn_readfirstlane(wave);
@@ -454,7 +507,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   const bool valid_lo = g_lo < G, valid_hi = g_lo + 1 < G;
   // Initial fill of the ring: the group's first kRing words (8 loads per lane).
   {
-    const uint32_t fill = ch.count < kRing ? ch.count : kRing;
+    const uint32_t fill = count < kRing ? count : kRing;
     uint32_t v[kRing / 32];
 #pragma unroll
     for (uint32_t i = 0; i < kRing / 32; ++i) {
@@ -466,9 +519,17 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
       ch.ring[w] = v[i];
       if (w < kMirror) ch.ring[w + kRing] = v[i];
     }
-    ch.fe = ch.q = fill;
     ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 0, 0);
     ch.x_next1 = early ? __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128, 0) : 0u;
+  }
+  Rings rg;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    rg.count[h] = __builtin_amdgcn_readlane(count, 32 * h);
+    rg.base[h] = __builtin_amdgcn_readlane(ring_addr, 32 * h) >> 2;
+    rg.rp[h] = rg.bb[h] = rg.bn[h] = 0;
+    rg.fe[h] = rg.q[h] = rg.count[h] < kRing ? rg.count[h] : kRing;
+    rg.ab0[h] = rg.base[h];
   }
   __syncthreads();
 
@@ -497,16 +558,16 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
         }
         ch.x_next = __builtin_amdgcn_raw_buffer_load_b32(rrec, ch.nib, 128 * (m + 2 < msteps ? m + 2 : m), 0);
         uint2 o0 = nibble_template(x0), o1 = nibble_template(x1);
-        half_begin(ch, li, rrec);
+        half_begin(rg, ch, li, upper, half_shift, rrec);
         // The next unread ring word of each half's group, packed in a scalar register.
-        uint32_t offs = __builtin_amdgcn_readlane(ch.ab0, 0) | (__builtin_amdgcn_readlane(ch.ab0, 32) << 16);
+        uint32_t offs = spack(rg.ab0[0], rg.ab0[1]);
         __builtin_amdgcn_wave_barrier();
         o0.x = quad(ch, offs, half_shift, s_lut, o0.x);
         o0.y = quad(ch, offs, half_shift, s_lut, o0.y);
         o1.x = quad(ch, offs, half_shift, s_lut, o1.x);
         o1.y = quad(ch, offs, half_shift, s_lut, o1.y);
         __builtin_amdgcn_wave_barrier();
-        half_end(ch, li, __builtin_amdgcn_ubfe(offs, half_shift, 16u));
+        half_end(rg, ch, li, half_shift, offs);
         ob[u >> 1] = make_uint4(o0.x, o0.y, o1.x, o1.y);
       }
       if constexpr (F == 16)
