@@ -253,6 +253,62 @@ def test_decode_from_ram_matches_staging_full_size():
             assert torch.equal(scale_dst[k][int(dst_row[j])], scale[k][j])
 
 
+@pytest.mark.parametrize("chunk", [32, 64, 96, 512])
+def test_decode_from_ram_single_row(chunk):
+    """A launch with a single row to expand from the RAM tier takes the
+    kernel's latency path (both nibble words of an iteration fetched an
+    iteration ahead). A valid record gives its raw bytes alone, in a two-row
+    launch (the paced path) and from staging. Records of random bytes with
+    a table of 9-bit codes (a refill every 3 symbols: the most ring traffic,
+    with the stream outrunning its requests) or a random table expand to the
+    same bytes alone as in a two-row launch, and to nothing outside their
+    own row."""
+    codec = _codec()
+    dev = torch.device("cuda")
+    ns = (4 * chunk * 32, 2 * chunk * 32)
+    pitches = [codec_ref.pitch_of(n, 1.25, 4096) for n in ns]
+    E, rows_ram = 4, 6
+    rng = np.random.default_rng(chunk)
+    raw = [rows(300 + k, n) for k, n in enumerate(ns)]
+    lut_np = rng.integers(0, 256, (E, 2, 512), dtype=np.uint8)
+    lut_np[1] = 0x09
+    recs = [rng.integers(0, 256, (E, p), dtype=np.uint8) for p in pitches]
+    for k in range(2):
+        recs[k][0], lut_np[0, k] = codec_ref.encode(raw[k], pitches[k], chunk)
+    src_row = torch.tensor([3, 0, 5, 2], dtype=torch.int64, device=dev)  # RAM row of each expert
+    tiers = [_ram_tier({int(src_row[e]): recs[k][e] for e in range(E)}, rows_ram, pitches[k]) for k in range(2)]
+    lut = torch.from_numpy(lut_np).to(dev)
+    scale = [torch.randint(1, 2**30, (E, 4), dtype=torch.int32, device=dev) for _ in range(2)]
+    cache_row = torch.full((E,), -1, dtype=torch.int64, device=dev)
+    dst_row = torch.arange(E, dtype=torch.int64, device=dev)
+
+    def from_ram(todo):
+        dst = [torch.zeros((E, n), dtype=torch.uint8, device=dev) for n in ns]
+        sdst = [torch.zeros_like(s) for s in scale]
+        codec.decode_rows_from_ram(torch.tensor(todo, dtype=torch.int64, device=dev), dst_row, cache_row, src_row,
+                                   0, [t[1] for t in tiers], dst, lut, scale, sdst, chunk=chunk)
+        torch.cuda.synchronize()
+        return dst, sdst
+
+    stg = [torch.from_numpy(r).to(dev) for r in recs]
+    want = [torch.zeros((E, n), dtype=torch.uint8, device=dev) for n in ns]
+    codec.decode_rows(torch.arange(E, dtype=torch.int64, device=dev), dst_row, cache_row, stg, want, lut,
+                      chunk=chunk)
+    torch.cuda.synchronize()
+    for k in range(2):
+        np.testing.assert_array_equal(want[k][0].cpu().numpy(), raw[k])
+    for e in range(E):
+        alone, sdst = from_ram([e, -1])
+        pair, _ = from_ram([e, (e + 1) % E])
+        for k in range(2):
+            assert torch.equal(alone[k][e], pair[k][e]), (e, k)
+            if e == 0:
+                assert torch.equal(alone[k][e], want[k][e]), k
+            assert torch.equal(sdst[k][e], scale[k][e])
+            others = [d for d in range(E) if d != e]
+            assert not alone[k][others].any() and not sdst[k][others].any(), (e, k)
+
+
 @pytest.mark.parametrize("chunk", [64, 512])
 def test_garbage_records_stay_in_bounds(chunk):
     """Records and LUTs of random bytes (start words out of range, code
