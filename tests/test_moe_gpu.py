@@ -326,15 +326,20 @@ def _separate(moe, xb, tw_t, ids_t, emap, E, slots, w, act="silu"):
 
 
 @pytest.mark.parametrize(
-    "T, topk, E, slots, H, I, idbits",
-    [(1, 8, 256, 32, 2048, 512, 64), (5, 8, 64, 64, 2048, 512, 32), (8, 8, 256, 200, 2048, 512, 64),
-     (3, 4, 12, 12, 256, 128, 32), (16, 4, 32, 32, 640, 1024, 64),
+    "T, topk, E, slots, H, I, idbits, route",
+    [(1, 8, 256, 32, 2048, 512, 64, "random"), (5, 8, 64, 64, 2048, 512, 32, "random"),
+     (8, 8, 256, 200, 2048, 512, 64, "random"), (3, 4, 12, 12, 256, 128, 32, "random"),
+     (16, 4, 32, 32, 640, 1024, 64, "random"),
      # more than 16 tokens: each workgroup quantises its own subtile's rows
-     (32, 2, 40, 40, 384, 256, 64),
+     (32, 2, 40, 40, 384, 256, 64, "random"),
      # H = 4096: two rounds of 16 K blocks in the gate/up launch
-     (2, 8, 16, 16, 4096, 256, 32)],
+     (2, 8, 16, 16, 4096, 256, 32, "random"),
+     # a slot with more than 16 pairs takes several 16-row subtiles: every
+     # token's first choice is one expert (32 pairs there, two subtiles), or
+     # all 64 pairs are one expert's (four subtiles of one slot)
+     (32, 2, 16, 16, 512, 256, 64, "first"), (64, 1, 8, 8, 512, 256, 32, "one")],
 )
-def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits):
+def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits, route):
     """The two-launch decode FFN (routing and quantisation inside gate/up, each
     token's top-k sum inside the down projection) gives the bits of
     quant_route + run_experts + topk_sum, with invalid ids skipped as topk_sum
@@ -342,6 +347,11 @@ def test_decode_experts_equals_separate_calls(T, topk, E, slots, H, I, idbits):
     moe = _moe()
     rng = np.random.default_rng(T * 100 + E)
     x, tw, ids, w13, w13s, w2, w2s = _case(T * 31 + E, E, H, I, T, topk)
+    if route == "first":  # expert 5 first for every token, the second choice elsewhere
+        ids[:, 0] = 5
+        ids[:, 1] = (5 + 1 + rng.integers(0, E - 1, T)) % E
+    elif route == "one":
+        ids[:] = 3
     if T > 2:
         ids[1, 0] = -1
         ids[2, topk - 1] = E + 3
