@@ -109,6 +109,26 @@ def test_decode_steps_match_one_shot(model, compress, R):
 
 
 @pytest.mark.parametrize("compress, R", [(True, 160), (False, 256)])
+def test_batched_decode_steps_in_the_fused_step(model, compress, R):
+    """2, 4 and 5 tokens x top-8 = 16, 32 and 40 pairs: the fused two-launch
+    step, fed the acquire's per-pair slots, equals a one-shot run; the
+    compressed case pages through the SSD tier (R < E)."""
+    moe = _mods()[0]
+    m = model(256, 128, R, 8, compress)
+    rng = np.random.default_rng(12)
+    layer = m.layers[0]
+    for step in range(12):
+        T = (2, 4, 5)[step % 3]
+        x, tw, ids = routing(rng, T, m.E, 8, zipf=0.8)
+        assert moe.decode_pays(x, ids, I)
+        out = layer.forward(x, tw, ids)
+        assert same(out, m.one_shot(0, x, tw, ids)), f"step {step}"
+    vh, vm, rh, rm = layer.hit_rates()
+    assert vh > 0 and vm > 0 and (rm > 0) == (R < 256)
+    assert m.pager.store.failed is None
+
+
+@pytest.mark.parametrize("compress, R", [(True, 160), (False, 256)])
 def test_batched_decode_steps_beyond_the_fused_step(model, compress, R):
     """12, 9 and 6 tokens x top-8 = 96, 72 and 48 pairs over 128 cache slots:
     still the decode path (pairs <= S), but more pairs than the fused
