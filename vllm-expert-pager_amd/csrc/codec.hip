@@ -507,7 +507,6 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
   const bool valid_lo = g_lo < G, valid_hi = g_lo + 1 < G;
   // Initial fill of the ring: the group's first kRing words (8 loads per lane).
   {
-    const uint32_t fill = count < kRing ? count : kRing;
     uint32_t v[kRing / 32];
 #pragma unroll
     for (uint32_t i = 0; i < kRing / 32; ++i) {
