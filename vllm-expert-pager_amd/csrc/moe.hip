@@ -225,12 +225,24 @@ __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npa
   const int64_t per = (npairs + kW - 1) / kW;
   const int64_t lo = wave * per, hi = lo + per < npairs ? lo + per : npairs;
   int* hist = s_hist + wave * slots;
-  for (int64_t b = lo; b < hi; b += 64 * kRouteBatch) {
-    int sl[kRouteBatch];
-    route_slots(ids, eb, b + lane, hi, expert_map, E, slots, sl);
+  // A wave whose range is one batch (up to 16384 pairs in all) keeps its
+  // slots in registers for the scatter below instead of loading the ids and
+  // expert_map again (two memory round trips).
+  const bool one = hi - lo <= 64 * kRouteBatch;
+  int sl1[kRouteBatch];
+  if (one) {
+    route_slots(ids, eb, lo + lane, hi, expert_map, E, slots, sl1);
 #pragma unroll
     for (int j = 0; j < kRouteBatch; ++j)
-      if (sl[j] >= 0) atomicAdd(&hist[sl[j]], 1);
+      if (sl1[j] >= 0) atomicAdd(&hist[sl1[j]], 1);
+  } else {
+    for (int64_t b = lo; b < hi; b += 64 * kRouteBatch) {
+      int sl[kRouteBatch];
+      route_slots(ids, eb, b + lane, hi, expert_map, E, slots, sl);
+#pragma unroll
+      for (int j = 0; j < kRouteBatch; ++j)
+        if (sl[j] >= 0) atomicAdd(&hist[sl[j]], 1);
+    }
   }
   __syncthreads();
   int c = 0;
@@ -264,6 +276,12 @@ __device__ __forceinline__ void route_block(const void* ids, int eb, int64_t npa
     if (wide) wide[0] = total.z;
   }
   __syncthreads();
+  if (one) {
+#pragma unroll
+    for (int j = 0; j < kRouteBatch; ++j)
+      if (sl1[j] >= 0) pairs[atomicAdd(&hist[sl1[j]], 1)] = static_cast<int32_t>(lo + lane + 64 * j);
+    return;
+  }
   for (int64_t b = lo; b < hi; b += 64 * kRouteBatch) {
     int sl[kRouteBatch];
     route_slots(ids, eb, b + lane, hi, expert_map, E, slots, sl);
