@@ -71,8 +71,9 @@ def test_golden_records():
 
 
 @pytest.mark.parametrize("dist", ["realistic", "uniform", "geometric", "constant", "long_codes"])
-# 128-byte stores for chunks of 128 and 512, 64-byte for 64 and 192, plain for 32 and 96
-@pytest.mark.parametrize("chunk", [32, 64, 96, 128, 192, 512])
+# 128-byte stores for chunks of 128, 512 and 4096 (the largest chunk a
+# record may use), 64-byte for 64 and 192, plain for 32 and 96
+@pytest.mark.parametrize("chunk", [32, 64, 96, 128, 192, 512, 4096])
 def test_round_trip(dist, chunk):
     codec = _codec()
     n = 2 * chunk * 32
@@ -253,7 +254,7 @@ def test_decode_from_ram_matches_staging_full_size():
             assert torch.equal(scale_dst[k][int(dst_row[j])], scale[k][j])
 
 
-@pytest.mark.parametrize("chunk", [32, 64, 96, 512])
+@pytest.mark.parametrize("chunk", [32, 64, 96, 512, 4096])
 def test_decode_from_ram_single_row(chunk):
     """A launch with a single row to expand from the RAM tier takes the
     kernel's latency path (both nibble words of an iteration fetched an
@@ -309,7 +310,10 @@ def test_decode_from_ram_single_row(chunk):
             assert not alone[k][others].any() and not sdst[k][others].any(), (e, k)
 
 
-@pytest.mark.parametrize("chunk", [64, 512])
+# 4096: a table of 9-bit codes makes a group consume its most words (about
+# 36900), and random start words give header counts above 65535, which the
+# decoder clamps
+@pytest.mark.parametrize("chunk", [64, 512, 4096])
 def test_garbage_records_stay_in_bounds(chunk):
     """Records and LUTs of random bytes (start words out of range, code
     lengths 0-15) expand to arbitrary bytes in their own rows only: the
