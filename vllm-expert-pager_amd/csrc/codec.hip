@@ -194,27 +194,6 @@ __device__ __forceinline__ void half_end(Rings& r, Chain& c, uint32_t li, uint32
   }
 }
 
-// Wave priority by the part of its chunk a wave has decoded: 3 in the first
-// quarter down to 0 in the last. The arbiter issues from the highest
-// priority first and, among equals, from the oldest wave, so with one
-// priority the workgroups dispatched first run ahead (78 against 116 us in
-// the first round of a 256-row launch) and the last ones dispatched finish
-// late, alone, as the CU empties. With the waves that have the most left
-// going first, a CU's waves keep the same pace, each round of workgroups
-// ends together and the next one starts full: a 256-row launch 3-4% and a
-// 64-row launch 10% faster.
-__device__ __forceinline__ void progress_priority(int m0, int msteps) {
-  const int q = (4 * m0) / msteps;
-  if (q == 0)
-    __builtin_amdgcn_s_setprio(3);
-  else if (q == 1)
-    __builtin_amdgcn_s_setprio(2);
-  else if (q == 2)
-    __builtin_amdgcn_s_setprio(1);
-  else
-    __builtin_amdgcn_s_setprio(0);
-}
-
 // mask[lane] ? if1 : if0, as one v_cndmask. Written as an instruction so
 // that the compiler keeps the step branch-free instead of turning the
 // select back into a branch around the ring read.
@@ -565,6 +544,9 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8
 #pragma unroll
     for (int i = 0; i < F / 2; ++i) ob[i] = make_uint4(0, 0, 0, 0);
     for (int m0 = 0; m0 < msteps; m0 += F) {
+      // Priority by progress through the chunk: the first workgroups of a
+      // 256-row launch otherwise took 78 against 116 us for those dispatched
+      // a microsecond later, and the launch 3% longer; a 64-row launch 10%.
       progress_priority(m0, msteps);
 #pragma unroll
       for (int u = 0; u < F; u += 2) {

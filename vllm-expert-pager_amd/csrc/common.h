@@ -62,5 +62,26 @@ __device__ __forceinline__ int64_t load_id(const void* p, int elem_bytes, int64_
                          : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
 }
 
+// Wave priority by the part of its sequential work a wave has done (done of
+// total, uniform over the wave): 3 in the first quarter down to 0 in the
+// last. The arbiter issues from the highest priority first and, among
+// equal priorities, from the oldest wave. In a kernel whose waves all do
+// the same sequential work over several rounds of workgroups, one priority
+// lets the first-dispatched workgroups run ahead and the last-dispatched
+// finish late, alone, as the CU empties; with the waves that have the most
+// left going first, a CU's waves keep the same pace, each round ends
+// together and the next one starts full.
+__device__ __forceinline__ void progress_priority(int done, int total) {
+  const int q = (4 * done) / total;
+  if (q == 0)
+    __builtin_amdgcn_s_setprio(3);
+  else if (q == 1)
+    __builtin_amdgcn_s_setprio(2);
+  else if (q == 2)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 }  // namespace xp
 #endif  // __HIP__
