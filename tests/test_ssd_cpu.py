@@ -328,11 +328,12 @@ def test_requests_published_together_answer_in_order(server, which, bounce):
 
 
 def test_one_reader_bounced_requests_back_to_back(tmp_path):
-    """One reader with bounced reads: it alternates between its two bounce
-    buffers while the copier empties them, so requests of several records
-    published back to back still land whole and answer in order; a stop with
-    reads and copies still queued waits for the copies out of the buffers it
-    frees (the sanitizer runs repeat this test)."""
+    """One reader with bounced reads: it rotates through its bounce buffers
+    while the copier empties them (45 records, more than it has buffers, so
+    each is reused), and requests of several records published back to back
+    still land whole and answer in order; a stop with reads and copies still
+    queued waits for the copies out of the buffers it frees (the sanitizer
+    runs repeat this test)."""
     pitches = (258 * 4096, 515 * 4096)
     s = Server(str(tmp_path / "one.bin"), nworkers=0, which="xp", pitches=pitches)
     s.lib.xp_ssd_test_bounce(s.h)
