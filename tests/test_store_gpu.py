@@ -203,9 +203,9 @@ def test_one_request_uses_every_reader(tiers):
 
 def test_readers_are_sized_from_the_disk_after_sync(tiers, monkeypatch):
     """sync() probes the paging file at 1, 2, 4 and 8 reads in flight and
-    restarts the server with the smallest depth within 10% of the fastest;
-    it still serves the ring afterwards. VLLM_EXPERT_PAGER_READ_WORKERS fixes
-    the count instead."""
+    restarts the server with the smallest depth of at least 2 within 10% of
+    the fastest (1 when no deeper one is); it still serves the ring
+    afterwards. VLLM_EXPERT_PAGER_READ_WORKERS fixes the count instead."""
     monkeypatch.delenv("VLLM_EXPERT_PAGER_READ_WORKERS", raising=False)
     t = tiers(layers=2, experts=12, ram=4)
     st = t.store
@@ -216,7 +216,9 @@ def test_readers_are_sized_from_the_disk_after_sync(tiers, monkeypatch):
     best = max(st.reader_probe.values())
     # the probe's rates are rounded to 3 decimals
     assert st.reader_probe[str(st.readers)] >= 0.9 * best - 1e-3
-    assert all(st.reader_probe[str(d)] < 0.9 * best + 1e-3 for d in (1, 2, 4, 8) if d < st.readers)
+    assert all(st.reader_probe[str(d)] < 0.9 * best + 1e-3 for d in (2, 4, 8) if d < st.readers)
+    if st.readers == 1:  # only when no deeper depth is within 10%
+        assert all(st.reader_probe[str(d)] < 0.9 * best + 1e-3 for d in (2, 4, 8))
     fetch = Fetch(t, 4, layer=1)
     fetch({5: 0, 9: 3, 11: 1})
     assert st.failed is None and (st.fetches, st.reads) == (1, 3)

@@ -38,9 +38,10 @@ _ALIGN = 4096
 # (store.py:59-64), sized by hand for its NVMe disk. Here the server starts
 # with _READERS_UNSIZED and, once the paging file is complete (sync), probes
 # the disk with record-sized O_DIRECT reads of the file from each of
-# _READER_DEPTHS threads and restarts with the depth that read fastest: disks
-# differ in how much a deeper queue helps, and on some every extra read in
-# flight only slows the others down. VLLM_EXPERT_PAGER_READ_WORKERS (1..64),
+# _READER_DEPTHS threads and restarts with the smallest depth of at least 2
+# within 10% of the fastest (see size_readers): disks differ in how much a
+# deeper queue helps, and on some every extra read in flight only slows the
+# others down. VLLM_EXPERT_PAGER_READ_WORKERS (1..64),
 # not a reference setting, fixes the count and skips the probe.
 _READERS_UNSIZED = 2
 _READER_DEPTHS = (1, 2, 4, 8)
@@ -286,10 +287,14 @@ class Store:
         """Probe the paging file with record-sized O_DIRECT reads of random
         records from 1, 2, 4 and 8 threads (two passes in opposite orders,
         each about ``seconds`` long at 3 GB/s, the better kept), and restart
-        the server with the smallest depth within 10% of the fastest (fewer
-        reads in flight serve a decode step's single records sooner). Only
-        while no request has been made: a new server starts from seq 1.
-        Returns the rates (GB/s by depth), or None when nothing was done."""
+        the server with the smallest depth of at least 2 within 10% of the
+        fastest, or 1 when no deeper one is (fewer reads in flight serve a
+        decode step's single records sooner; a second reader still pays:
+        while one reads, the other's bounce copy is under way, and the
+        server's own sweeps moved 6 GB/s at two readers against 3-5.6 at
+        one on disks whose probe put the two depths within 10%). Only while
+        no request has been made: a new server starts from seq 1. Returns
+        the rates (GB/s by depth), or None when nothing was done."""
         if not self._handle or self.fd_r is None:
             return None
         slots = self.req[2:].view(self.ring, self.slot_words)
@@ -311,7 +316,9 @@ class Store:
                     return None
                 rates[depth] = max(rates.get(depth, 0.0), count * self.record_bytes / sec.value / 1e9)
         best = max(rates.values())
-        readers = min(d for d, r in rates.items() if r >= 0.9 * best)
+        close = [d for d, r in rates.items() if r >= 0.9 * best]
+        deeper = [d for d in close if d >= 2]
+        readers = min(deeper) if deeper else 1
         self.reader_probe = {str(d): round(r, 3) for d, r in sorted(rates.items())}
         if readers != self.readers:
             self._so.ssd_stop(ctypes.c_void_p(self._handle))
