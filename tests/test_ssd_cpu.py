@@ -274,9 +274,10 @@ def test_read_probe_reads_every_record(tmp_path, use_uring, depth):
 
 @pytest.mark.parametrize("bounce", [False, True], ids=["direct", "bounce"])
 def test_records_larger_than_a_copy_chunk(tmp_path, which, bounce):
-    """Records whose names are longer than 1 MiB (258 and 515 pages, so a
-    bounced copy is cut into 1 MiB chunks with short last ones, spread over
-    the readers) land whole in their rows, one preadv per record."""
+    """Records whose names are longer than a copy chunk (258 and 515 pages,
+    so a bounced copy is cut into 256 KiB chunks with short last ones, spread
+    over the copiers and readers) land whole in their rows, one preadv per
+    record."""
     if bounce and which != "xp":
         pytest.skip("the bounce hook is this build's")
     pitches = (258 * 4096, 515 * 4096)

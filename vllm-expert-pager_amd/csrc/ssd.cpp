@@ -29,10 +29,13 @@
 //     pinned memory cannot be an O_DIRECT target (preadv fails with EFAULT,
 //     seen with the GPU driver's pinned allocations) it goes into the next of
 //     the reader's kBounce aligned bounce buffers instead, in rotation, and
-//     the copy into the rows is cut into chunks on a second queue. Two copier
-//     threads take those chunks, and so do idle readers (non-temporal
-//     stores), while the reader goes on to its next read in its next bounce
-//     buffer: reads and copies overlap even with one reader. A reader whose
+//     the copy into the rows is cut into 256 KiB chunks on a second queue.
+//     Four copier threads take those chunks, and so do idle readers
+//     (non-temporal stores), while the reader goes on to its next read in
+//     its next bounce buffer: reads and copies overlap even with one reader,
+//     and one record's copy is spread over up to a dozen threads (against 1
+//     MiB chunks and two copiers, single-record requests were answered 7%
+//     sooner on average in alternating runs on one disk). A reader whose
 //     next bounce buffer is still being copied out helps with the copies
 //     first. The rotation is long because a read into a buffer that was just
 //     copied out is slower (0.52 against 0.34 ms for a record in a plain
@@ -78,10 +81,10 @@ namespace {
 constexpr int kMaxNames = 4;
 constexpr int kHead = 2;                  // [re-publishes, give-ups]
 constexpr long kAlign = 4096;             // O_DIRECT alignment of offsets, lengths and buffers
-constexpr long kCopyChunk = 1L << 20;     // longest run of a bounce copy one thread takes
+constexpr long kCopyChunk = 1L << 18;     // longest run of a bounce copy one thread takes
 constexpr int kBounce = 32;               // bounce buffers per reader, allocated when first used
 constexpr int kMaxInFlight = 64;          // requests picked up and not yet answered
-constexpr int kCopiers = 2;               // copier threads (one copies about 6 GB/s into pinned rows)
+constexpr int kCopiers = 4;               // copier threads (one copies about 6 GB/s into pinned rows)
 
 inline void cpu_relax() {
 #if defined(__x86_64__) || defined(__i386__)
