@@ -17,6 +17,7 @@ import argparse
 import concurrent.futures as cf
 import ctypes
 import json
+import mmap
 import os
 import shutil
 import sys
@@ -1106,6 +1107,51 @@ def server_sweep(store, path: str, readers=(1, 2, 4, 8), seconds: float = 0.6) -
     return out
 
 
+def _o_direct_ok(d: str) -> bool:
+    """Whether files in directory d can be read with O_DIRECT (a 4 KiB probe file)."""
+    probe = os.path.join(d, f"xp_odirect_{os.getpid()}.bin")
+    try:
+        with open(probe, "wb") as f:
+            f.write(b"\0" * 4096)
+        fd = os.open(probe, os.O_RDONLY | os.O_DIRECT)
+        try:
+            buf = mmap.mmap(-1, 4096)
+            os.readv(fd, [buf])
+        finally:
+            os.close(fd)
+        return True
+    except OSError:
+        return False
+    finally:
+        if os.path.exists(probe):
+            os.unlink(probe)
+
+
+def paging_dir(args) -> tuple[str | None, str]:
+    """The directory for the paging file: --paging-dir when given, else the one of $TMPDIR,
+    /tmp, /var/tmp and the repository with the most free space that takes O_DIRECT reads.
+    Returns (directory or None, what was considered)."""
+    if args.paging_dir:
+        return args.paging_dir, f"--paging-dir {args.paging_dir}"
+    seen, best, notes = set(), None, []
+    for d in (os.environ.get("TMPDIR"), "/tmp", "/var/tmp", ROOT):
+        if not d or not os.path.isdir(d):
+            continue
+        real = os.path.realpath(d)
+        if real in seen:
+            continue
+        seen.add(real)
+        try:
+            free = shutil.disk_usage(d).free
+        except OSError:
+            continue
+        ok = _o_direct_ok(d)
+        notes.append(f"{d}: {free / 2**30:.1f} GiB free{'' if ok else ', no O_DIRECT'}")
+        if ok and (best is None or free > best[1]):
+            best = (d, free)
+    return (best[0] if best else None), "; ".join(notes)
+
+
 def bench_tiered(args, dev, decode_steps: int | None = None):
     """The compressed tier: 40 layers x 256 experts, 32 cache slots, 128 RAM slots holding rows
     compressed at pitch 0.89, the rest in a paging file read with O_DIRECT by the host server.
@@ -1121,14 +1167,18 @@ def bench_tiered(args, dev, decode_steps: int | None = None):
     L, E, H, k = c["layers"], c["experts"], c["hidden"], c["topk"]
     T = args.prefill_tokens
     need = L * E * (1_867_776 + 933_888)  # records at pitch 0.89
+    pdir, considered = paging_dir(args)
+    if pdir is None:
+        return {"skipped": f"no directory for the paging file takes O_DIRECT reads ({considered})"}
     try:
-        free = shutil.disk_usage(args.paging_dir).free
+        free = shutil.disk_usage(pdir).free
     except OSError as e:
-        return {"skipped": f"paging directory {args.paging_dir}: {e}"}
+        return {"skipped": f"paging directory {pdir}: {e}"}
     if free < need + (4 << 30):
-        return {"skipped": f"the paging file needs {need / 2**30:.1f} GiB and {args.paging_dir} has "
-                           f"{free / 2**30:.1f} GiB free (4 GiB kept spare)"}
-    path = os.path.join(args.paging_dir, f"xp_paging_{os.getpid()}.bin")
+        return {"skipped": f"the paging file needs {need / 2**30:.1f} GiB and the roomiest directory has "
+                           f"{free / 2**30:.1f} GiB free (4 GiB kept spare; {considered})"}
+    log(f"paging file in {pdir} ({considered})")
+    path = os.path.join(pdir, f"xp_paging_{os.getpid()}.bin")
     settings = pg.Settings(cache_slots=32, ram_slots=128, ssd_path=path, compress="on", pitch_ratio=0.89,
                            working_rows=64, log_interval=0)
     pager, layers, weights = build_paged_model(dev, settings, keep_weights=True)
@@ -1232,7 +1282,9 @@ def main() -> None:
     ap.add_argument("--tiered-decode-steps", type=int, default=2000,
                     help="decode steps of the compressed tier in the default run (the configured 2000)")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
-    ap.add_argument("--paging-dir", default=os.environ.get("TMPDIR", "/tmp"))
+    ap.add_argument("--paging-dir", default=None,
+                    help="directory for the tiered leg's paging file (default: the roomiest of $TMPDIR, "
+                         "/tmp, /var/tmp and the repository that takes O_DIRECT reads)")
     ap.add_argument("--decode-steps", type=int, default=2000)
     ap.add_argument("--decode-warmup", type=int, default=20)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
